@@ -1,0 +1,190 @@
+/*
+ * wmx_attn.h - C ABI of the MI355X (gfx950) attention library libwmx_attn.so.
+ *
+ * The library holds the hand-written CDNA4 HIP kernels behind WhiteMatter's
+ * two attention operators, `cyclic_attention` and `strict_causal_attention`.
+ * Every entry point:
+ *   - takes plain device pointers, element strides and sizes (no C++ types),
+ *   - launches asynchronously on the given hipStream_t (passed as void*),
+ *   - allocates nothing: outputs and workspaces come from the caller,
+ *   - returns 0 on success or a negative WMX_E* code; wmx_last_error() then
+ *     returns a thread-local message naming the failed check.
+ *
+ * Tensors are bf16 (Q/K/V/O and gradients) with unit stride along head_dim.
+ * Logical shapes follow the reference operators: Q (B, Hq, Tq, D) and
+ * K/V (B, Hkv, Tk, D) with Hq % Hkv == 0; query head h reads KV head h / (Hq/Hkv).
+ *
+ * Reference interfaces replaced (paths in Cy-47/White-Matter):
+ *   wmx_attn_fwd      src/white_matter/ops/cyclic_attention/_tilelang/registration.py:123-140
+ *                     (TileLang kernels forward.py:15-133, document_forward.py:17-165),
+ *                     src/white_matter/ops/strict_causal_attention.py:397-442
+ *                     (flash_attn_varlen_func / TorchFlashVarlen / flash_attn_func),
+ *                     src/white_matter/ops/flash_attention.py:125-145,170-211
+ *   wmx_attn_bwd_preprocess
+ *                     src/white_matter/ops/cyclic_attention/_tilelang/backward_preprocess.py:34-49
+ *   wmx_attn_bwd      src/white_matter/ops/cyclic_attention/_tilelang/registration.py:143-161
+ *                     (backward_query.py, backward_key_value.py, document_backward_*.py),
+ *                     src/white_matter/ops/flash_attention.py:147-167,213-236
+ *   wmx_decode        src/white_matter/ops/flash_attention.py:15-49 (flash_attn_with_kvcache),
+ *                     src/white_matter/ops/flash_attention.py:52-103 (torch_flash_decode),
+ *                     src/white_matter/ops/strict_causal_attention.py:238-263,338-358
+ */
+#ifndef WMX_ATTN_H
+#define WMX_ATTN_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define WMX_ABI_VERSION 1
+
+enum {
+  WMX_OK = 0,
+  WMX_E_INVALID = -1,     /* argument check failed */
+  WMX_E_UNSUPPORTED = -2, /* head_dim or layout the kernels do not implement */
+  WMX_E_WORKSPACE = -3,   /* workspace missing or too small */
+  WMX_E_LAUNCH = -4       /* HIP reported an error at launch */
+};
+
+/*
+ * Arguments shared by the forward and backward entry points.
+ *
+ * Visibility of key slot j to query row i (all modes):
+ *   j <= lim(i), lim(i) = min(offset_b + query_stride * i, limit_b)
+ *   or (keep_slot0 and j == 0),
+ *   and key_mask[b, j] when key_mask is given,
+ *   and the document rule when q_seg/k_seg/q_start/k_qend are given:
+ *   (q_seg[i] == k_seg[j] and j >= q_start[i] or k_seg[j] == -1) and i < k_qend[j].
+ * offset_b is row_offset[b] when row_offset is given, else query_offset;
+ * limit_b is row_limit[b] when row_limit is given, else unbounded.
+ * Rows with no visible key produce a zero output, lse = +inf and zero gradients.
+ *
+ * Varlen mode (query_indices != NULL): segment s holds queries
+ * query_indices[cu_queries[s] : cu_queries[s+1]] (flat b * query_extent + t)
+ * and keys key_indices[cu_keys[s] : cu_keys[s+1]] (flat b * key_extent + slot);
+ * local key j is visible to local query i iff j <= (nk - nq) + i
+ * (bottom-right causal). Output rows not named by any segment are left
+ * untouched, so callers zero-fill o/dq/dk/dv first.
+ */
+typedef struct wmx_attn_args {
+  const void* q;
+  const void* k;
+  const void* v;
+  void* o;              /* bf16, logical (B, Hq, Tq, D), strides o_stride */
+  float* lse;           /* fp32 (B, Hq, Tq) contiguous; natural log; +inf for empty rows */
+  const void* dout;     /* bf16 gradient of o, strides do_stride (backward only) */
+  float* delta;         /* fp32 (B, Hq, Tq) contiguous; rowsum(dout * o) (backward) */
+  void* dq;
+  void* dk;
+  void* dv;
+  void* workspace;      /* device scratch for the backward (see wmx_attn_bwd_workspace_size) */
+  int64_t workspace_bytes;
+  /* element strides [batch, head, token]; head_dim stride is 1 */
+  int64_t q_stride[3];
+  int64_t k_stride[3];
+  int64_t v_stride[3];
+  int64_t o_stride[3];
+  int64_t do_stride[3];
+  int64_t dq_stride[3];
+  int64_t dk_stride[3];
+  int64_t dv_stride[3];
+  int32_t batch;
+  int32_t q_heads;
+  int32_t kv_heads;
+  int32_t q_len;
+  int32_t kv_len;
+  int32_t head_dim;     /* 64, 96 or 128 */
+  int32_t query_stride;
+  int32_t query_offset;
+  const int32_t* row_offset;  /* optional (B,) */
+  const int32_t* row_limit;   /* optional (B,) */
+  const uint8_t* key_mask;    /* optional (B, Tk) bool rows */
+  int64_t key_mask_stride;
+  int32_t keep_slot0;
+  int32_t keys_unique;        /* varlen: no key row appears in two segments */
+  const int32_t* q_seg;       /* optional cyclic document metadata, int32 contiguous */
+  const int32_t* k_seg;
+  const int32_t* q_start;
+  const int32_t* k_qend;
+  const int64_t* query_indices;  /* optional varlen schedule */
+  const int64_t* key_indices;
+  const int32_t* cu_queries;
+  const int32_t* cu_keys;
+  int32_t num_segments;
+  int32_t max_queries;        /* largest segment query count */
+  int32_t max_keys;           /* largest segment key count */
+  int32_t query_extent;       /* T: row width of flat query indices */
+  int32_t key_extent;         /* N: row width of flat key indices */
+  float softmax_scale;
+} wmx_attn_args;
+
+/*
+ * Single-query decode over a KV pool (no gradient).
+ * Query head h of row b attends to slots j of KV head h / (Hq/Hkv) with
+ *   j < len_b,  len_b = clamp(min(start_b, kvlen_b), 0, capacity - dummy) + dummy,
+ * or, when key_mask is given, key_mask[b, j] and j < min(start_b, kvlen_b) + dummy.
+ * start_b is query_start[b] when given, else query_start_scalar; kvlen_b is
+ * kv_lengths[b] when given, else unbounded.
+ * The work is split over num_splits key ranges per (b, kv head) whose partial
+ * (o, max, sum) rows live in the workspace and are merged by a second kernel.
+ */
+typedef struct wmx_decode_args {
+  const void* q;        /* bf16 (B, Hq, 1, D) */
+  const void* k;        /* bf16 (B, Hkv, capacity, D) */
+  const void* v;
+  void* o;              /* bf16 output, logical (B, Hq, D) */
+  const int64_t* query_start;   /* optional (B,) int64 */
+  const int64_t* kv_lengths;    /* optional (B,) int64 */
+  const uint8_t* key_mask;      /* optional (B, capacity) bool rows */
+  int64_t key_mask_stride;
+  void* workspace;
+  int64_t workspace_bytes;
+  int64_t q_stride[2];  /* [batch, head] */
+  int64_t k_stride[3];  /* [batch, head, slot] */
+  int64_t v_stride[3];
+  int64_t o_stride[2];  /* [batch, head] */
+  int64_t query_start_scalar;
+  int32_t batch;
+  int32_t q_heads;
+  int32_t kv_heads;
+  int32_t capacity;
+  int32_t head_dim;
+  int32_t use_dummy;
+  int32_t num_splits;   /* <= 0: chosen by the library */
+  float softmax_scale;
+} wmx_decode_args;
+
+/* Library identity and struct layout checks for FFI bindings. */
+int wmx_abi_version(void);
+size_t wmx_attn_args_size(void);
+size_t wmx_decode_args_size(void);
+const char* wmx_last_error(void);
+
+/* Forward: o and lse. (see replaced interfaces above) */
+int wmx_attn_fwd(const wmx_attn_args* args, void* stream);
+
+/* delta[b,h,i] = sum_d dout[b,h,i,d] * o[b,h,i,d] in fp32. */
+int wmx_attn_bwd_preprocess(const wmx_attn_args* args, void* stream);
+
+/* Workspace bytes wmx_attn_bwd needs for these arguments (0 when none). */
+int64_t wmx_attn_bwd_workspace_size(const wmx_attn_args* args);
+
+/* Backward: delta, then dq, dk, dv. Varlen mode accumulates into dk/dv,
+ * which the caller zero-fills. */
+int wmx_attn_bwd(const wmx_attn_args* args, void* stream);
+
+/* Workspace bytes wmx_decode needs, and the split count it will use. */
+int64_t wmx_decode_workspace_size(const wmx_decode_args* args);
+int32_t wmx_decode_num_splits(const wmx_decode_args* args);
+
+/* Single-query decode forward. */
+int wmx_decode(const wmx_decode_args* args, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* WMX_ATTN_H */

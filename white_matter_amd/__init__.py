@@ -1,0 +1,21 @@
+"""WhiteMatter's attention hot path on MI355X (gfx950).
+
+Drop-in replacement for ``white_matter.ops`` (src/white_matter/ops/__init__.py:3-13):
+the same six public names with the same signatures, plus the model-side
+``prepare_feedback_metadata``. GPU work runs in hand-written HIP kernels
+loaded from ``lib/libwmx_attn.so`` through a C ABI (include/wmx_attn.h).
+"""
+
+from .cyclic_attention import cyclic_attention
+from .metadata import CyclicAttentionMetadata, prepare_cyclic_attention_metadata, prepare_feedback_metadata
+from .strict_causal_attention import StrictCausalMetadata, prepare_strict_causal_metadata, strict_causal_attention
+
+__all__ = [
+    "StrictCausalMetadata",
+    "prepare_strict_causal_metadata",
+    "strict_causal_attention",
+    "CyclicAttentionMetadata",
+    "cyclic_attention",
+    "prepare_cyclic_attention_metadata",
+    "prepare_feedback_metadata",
+]

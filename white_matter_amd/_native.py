@@ -1,0 +1,206 @@
+"""ctypes binding of libwmx_attn.so (the C ABI in include/wmx_attn.h).
+
+The structures below mirror ``wmx_attn_args`` and ``wmx_decode_args`` field by
+field; ``load()`` checks their sizes against the library's own ``sizeof`` so a
+header/binding mismatch fails at load time instead of corrupting a launch.
+Nothing here falls back to another implementation: when the library is
+missing or fails to load, every entry point raises ``RuntimeError``.
+"""
+
+from __future__ import annotations
+
+import ctypes
+import functools
+import os
+from pathlib import Path
+
+import torch
+
+LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
+ABI_VERSION = 1
+
+_c_i64_3 = ctypes.c_int64 * 3
+_c_i64_2 = ctypes.c_int64 * 2
+_vp = ctypes.c_void_p
+
+
+class AttnArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp),
+        ("k", _vp),
+        ("v", _vp),
+        ("o", _vp),
+        ("lse", _vp),
+        ("dout", _vp),
+        ("delta", _vp),
+        ("dq", _vp),
+        ("dk", _vp),
+        ("dv", _vp),
+        ("workspace", _vp),
+        ("workspace_bytes", ctypes.c_int64),
+        ("q_stride", _c_i64_3),
+        ("k_stride", _c_i64_3),
+        ("v_stride", _c_i64_3),
+        ("o_stride", _c_i64_3),
+        ("do_stride", _c_i64_3),
+        ("dq_stride", _c_i64_3),
+        ("dk_stride", _c_i64_3),
+        ("dv_stride", _c_i64_3),
+        ("batch", ctypes.c_int32),
+        ("q_heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("q_len", ctypes.c_int32),
+        ("kv_len", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("query_stride", ctypes.c_int32),
+        ("query_offset", ctypes.c_int32),
+        ("row_offset", _vp),
+        ("row_limit", _vp),
+        ("key_mask", _vp),
+        ("key_mask_stride", ctypes.c_int64),
+        ("keep_slot0", ctypes.c_int32),
+        ("keys_unique", ctypes.c_int32),
+        ("q_seg", _vp),
+        ("k_seg", _vp),
+        ("q_start", _vp),
+        ("k_qend", _vp),
+        ("query_indices", _vp),
+        ("key_indices", _vp),
+        ("cu_queries", _vp),
+        ("cu_keys", _vp),
+        ("num_segments", ctypes.c_int32),
+        ("max_queries", ctypes.c_int32),
+        ("max_keys", ctypes.c_int32),
+        ("query_extent", ctypes.c_int32),
+        ("key_extent", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
+class DecodeArgs(ctypes.Structure):
+    _fields_ = [
+        ("q", _vp),
+        ("k", _vp),
+        ("v", _vp),
+        ("o", _vp),
+        ("query_start", _vp),
+        ("kv_lengths", _vp),
+        ("key_mask", _vp),
+        ("key_mask_stride", ctypes.c_int64),
+        ("workspace", _vp),
+        ("workspace_bytes", ctypes.c_int64),
+        ("q_stride", _c_i64_2),
+        ("k_stride", _c_i64_3),
+        ("v_stride", _c_i64_3),
+        ("o_stride", _c_i64_2),
+        ("query_start_scalar", ctypes.c_int64),
+        ("batch", ctypes.c_int32),
+        ("q_heads", ctypes.c_int32),
+        ("kv_heads", ctypes.c_int32),
+        ("capacity", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("use_dummy", ctypes.c_int32),
+        ("num_splits", ctypes.c_int32),
+        ("softmax_scale", ctypes.c_float),
+    ]
+
+
+EXPORTS = (
+    "wmx_abi_version",
+    "wmx_attn_args_size",
+    "wmx_decode_args_size",
+    "wmx_last_error",
+    "wmx_attn_fwd",
+    "wmx_attn_bwd_preprocess",
+    "wmx_attn_bwd_workspace_size",
+    "wmx_attn_bwd",
+    "wmx_decode_workspace_size",
+    "wmx_decode_num_splits",
+    "wmx_decode",
+)
+
+
+@functools.cache
+def load() -> ctypes.CDLL:
+    """Load the gfx950 library once; raise RuntimeError if it is absent or stale."""
+    path = Path(os.environ.get("WMX_ATTN_LIBRARY", LIBRARY))
+    if not path.exists():
+        raise RuntimeError(
+            f"libwmx_attn.so not found at {path}; build it with `python -c \"import __graft_entry__ as g; g.build()\"`"
+        )
+    lib = ctypes.CDLL(str(path))
+    for name in EXPORTS:
+        if not hasattr(lib, name):
+            raise RuntimeError(f"{path} does not export {name}")
+    lib.wmx_abi_version.restype = ctypes.c_int
+    lib.wmx_attn_args_size.restype = ctypes.c_size_t
+    lib.wmx_decode_args_size.restype = ctypes.c_size_t
+    lib.wmx_last_error.restype = ctypes.c_char_p
+    for name in ("wmx_attn_fwd", "wmx_attn_bwd_preprocess", "wmx_attn_bwd"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(AttnArgs), _vp]
+        getattr(lib, name).restype = ctypes.c_int
+    lib.wmx_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnArgs)]
+    lib.wmx_attn_bwd_workspace_size.restype = ctypes.c_int64
+    lib.wmx_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+    lib.wmx_decode.restype = ctypes.c_int
+    lib.wmx_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs)]
+    lib.wmx_decode_workspace_size.restype = ctypes.c_int64
+    lib.wmx_decode_num_splits.argtypes = [ctypes.POINTER(DecodeArgs)]
+    lib.wmx_decode_num_splits.restype = ctypes.c_int32
+    if lib.wmx_abi_version() != ABI_VERSION:
+        raise RuntimeError(f"{path} has ABI {lib.wmx_abi_version()}, expected {ABI_VERSION}")
+    if lib.wmx_attn_args_size() != ctypes.sizeof(AttnArgs):
+        raise RuntimeError("wmx_attn_args layout differs between the library and the binding")
+    if lib.wmx_decode_args_size() != ctypes.sizeof(DecodeArgs):
+        raise RuntimeError("wmx_decode_args layout differs between the library and the binding")
+    return lib
+
+
+def _check(lib: ctypes.CDLL, rc: int, what: str) -> None:
+    if rc != 0:
+        message = lib.wmx_last_error().decode(errors="replace")
+        kind = ValueError if rc == -1 else RuntimeError
+        raise kind(f"{what} failed ({rc}): {message}")
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def ptr(t: torch.Tensor | None) -> int | None:
+    return None if t is None else t.data_ptr()
+
+
+def strides3(t: torch.Tensor | None) -> tuple[int, int, int]:
+    """Element strides [batch, head, token] of a (B, H, T, D) tensor."""
+    if t is None:
+        return (0, 0, 0)
+    return (t.stride(0), t.stride(1), t.stride(2))
+
+
+def attn_fwd(args: AttnArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_attn_fwd(ctypes.byref(args), _stream(device)), "wmx_attn_fwd")
+
+
+def attn_bwd_preprocess(args: AttnArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_attn_bwd_preprocess(ctypes.byref(args), _stream(device)), "wmx_attn_bwd_preprocess")
+
+
+def attn_bwd_workspace_size(args: AttnArgs) -> int:
+    return int(load().wmx_attn_bwd_workspace_size(ctypes.byref(args)))
+
+
+def attn_bwd(args: AttnArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_attn_bwd(ctypes.byref(args), _stream(device)), "wmx_attn_bwd")
+
+
+def decode_workspace_size(args: DecodeArgs) -> int:
+    return int(load().wmx_decode_workspace_size(ctypes.byref(args)))
+
+
+def decode(args: DecodeArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_decode(ctypes.byref(args), _stream(device)), "wmx_decode")

@@ -1,0 +1,577 @@
+// Attention backward for gfx950 (CDNA4): delta, dQ and dK/dV kernels.
+//
+// Math (softmax scale c, exp2 form, LSE in natural log from the forward):
+//   P  = exp2(S * c * log2e - LSE * log2e)   on visible pairs, else 0
+//   dP = dO V^T,  dS = P * (dP - delta),  delta = rowsum(dO * O)
+//   dQ = c * dS K,  dK = c * dS^T Q,  dV = P^T dO
+// following the reference's backward contract
+// (src/white_matter/ops/cyclic_attention/_tilelang/backward_query.py:86-109,
+//  backward_key_value.py:102-132, backward_preprocess.py:34-49).
+//
+// Two deterministic kernels, no atomics on the dense paths:
+//   dQ  : query-parallel (4 waves x 32 query rows), loops over visible key
+//         tiles of 64; a lane owns one query column of S^T = K Q^T, so its
+//         LSE and delta are scalars; dQ^T = K^T dS^T accumulates in registers.
+//   dKV : key-parallel (4 waves x 32 keys), loops over the query heads of the
+//         KV head and over the query tiles of 64 that can see the key tile;
+//         a lane owns one key column of S = Q K^T; dV^T = dO^T P and
+//         dK^T = Q^T dS accumulate in registers.
+// Varlen schedules whose key rows repeat across segments (the shared dummy
+// slot, capped histories) accumulate dK/dV in fp32 workspace rows with
+// atomics and convert once at the end.
+#include <climits>
+
+#include "wmx_kernels.h"
+
+namespace wmx {
+
+// ---------------------------------------------------------------- delta ----
+// 16 lanes per row, 8 elements per lane; 16 rows per 256-thread block.
+template <int D>
+__global__ __launch_bounds__(256) void bwd_delta_kernel(const wmx_attn_args a, int64_t rows) {
+  const int tid = threadIdx.x;
+  const int64_t r = (int64_t)blockIdx.x * 16 + (tid >> 4);
+  const int l16 = tid & 15;
+  float acc = 0.f;
+  if (r < rows && 8 * l16 < D) {
+    const int i = (int)(r % a.q_len);
+    const int64_t bh = r / a.q_len;
+    const int h = (int)(bh % a.q_heads);
+    const int b = (int)(bh / a.q_heads);
+    const bf16* o = (const bf16*)a.o + (int64_t)b * a.o_stride[0] + (int64_t)h * a.o_stride[1] +
+                    (int64_t)i * a.o_stride[2] + 8 * l16;
+    const bf16* g = (const bf16*)a.dout + (int64_t)b * a.do_stride[0] + (int64_t)h * a.do_stride[1] +
+                    (int64_t)i * a.do_stride[2] + 8 * l16;
+    const u32x4 ow = load16(o), gw = load16(g);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = fmaf(bf16_lo(ow[e]), bf16_lo(gw[e]), acc);
+      acc = fmaf(bf16_hi(ow[e]), bf16_hi(gw[e]), acc);
+    }
+  }
+#pragma unroll
+  for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+  if (r < rows && l16 == 0) a.delta[r] = acc;
+}
+
+// ------------------------------------------------------------ visibility --
+// The bound lim(i) = clamp(min(offset + stride * i, limit), -1, nk - 1).
+struct Bound {
+  int64_t offset, limit, stride;
+  int nk;
+  __device__ __forceinline__ int operator()(int i) const {
+    int64_t l = offset + stride * (int64_t)i;
+    l = l < limit ? l : limit;
+    l = l < (int64_t)nk - 1 ? l : (int64_t)nk - 1;
+    return (int)(l < -1 ? -1 : l);
+  }
+  // Smallest query row whose bound reaches key j (nq when none does).
+  __device__ __forceinline__ int first_row(int j, int nq) const {
+    if (j > nk - 1 || limit < j) return nq;
+    const int64_t need = (int64_t)j - offset;
+    int64_t m = need <= 0 ? 0 : (need + stride - 1) / stride;
+    return m < nq ? (int)m : nq;
+  }
+};
+
+// ------------------------------------------------------------------- dQ ----
+template <int D, int MODE>
+__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const wmx_attn_args a) {
+  constexpr int BM = 128, BN = 64;
+  constexpr int KLD = D + 8, TLD = BN + 8;
+  constexpr int KS = D / 16, DB = D / 32;
+  __shared__ __attribute__((aligned(16))) bf16 k_lds[BN * KLD];
+  __shared__ __attribute__((aligned(16))) bf16 v_lds[BN * KLD];
+  __shared__ __attribute__((aligned(16))) bf16 kt_lds[D * TLD];
+  __shared__ int kseg_lds[BN];
+  __shared__ int kqend_lds[BN];
+  __shared__ int red_lds[4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int h = blockIdx.y;
+  const int hk = h / (a.q_heads / a.kv_heads);
+
+  int b = 0, nq, nk, q0, qs = 0, ks = 0;
+  Bound bound;
+  if constexpr (MODE == kVarlen) {
+    const int qtiles = (a.max_queries + BM - 1) / BM;
+    const int seg = blockIdx.x / qtiles;
+    const int tile = qtiles - 1 - (int)(blockIdx.x % qtiles);
+    qs = a.cu_queries[seg];
+    nq = a.cu_queries[seg + 1] - qs;
+    ks = a.cu_keys[seg];
+    nk = a.cu_keys[seg + 1] - ks;
+    q0 = tile * BM;
+    if (q0 >= nq) return;
+    bound = Bound{nk - nq, INT_MAX, 1, nk};
+  } else {
+    b = blockIdx.z;
+    nq = a.q_len;
+    nk = a.kv_len;
+    q0 = (gridDim.x - 1 - blockIdx.x) * BM;
+    bound = Bound{a.row_offset ? a.row_offset[b] : a.query_offset, a.row_limit ? a.row_limit[b] : INT_MAX,
+                  a.query_stride, nk};
+  }
+  const bool slot0 = a.keep_slot0 && nk > 0;
+  const int lim_max_wg = bound(min(q0 + BM, nq) - 1);
+  const int i = q0 + wave * 32 + col;
+  const bool valid_q = i < nq;
+  const int lim_i = bound(i);
+  const int wave_first = q0 + wave * 32;
+  const bool wave_live = wave_first < nq;
+  const int lim_min_wave = bound(wave_first);
+  const int lim_max_wave = bound(min(wave_first + 31, nq - 1));
+
+  int qb = b, qt = i;
+  if constexpr (MODE == kVarlen) {
+    if (valid_q) split_flat(a.query_indices[qs + i], a.query_extent, qb, qt);
+  }
+  bf16x8 qf[KS], gf[KS];
+  float lse2 = kPosInf, delta = 0.f;
+  {
+    const bf16* qrow = (const bf16*)a.q + (int64_t)qb * a.q_stride[0] + (int64_t)h * a.q_stride[1] +
+                       (int64_t)qt * a.q_stride[2];
+    const bf16* grow = (const bf16*)a.dout + (int64_t)qb * a.do_stride[0] + (int64_t)h * a.do_stride[1] +
+                       (int64_t)qt * a.do_stride[2];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 wq = {0u, 0u, 0u, 0u}, wg = {0u, 0u, 0u, 0u};
+      if (valid_q) {
+        wq = load16(qrow + 16 * s + 8 * half);
+        wg = load16(grow + 16 * s + 8 * half);
+      }
+      qf[s] = as_bf16x8(wq);
+      gf[s] = as_bf16x8(wg);
+    }
+    if (valid_q) {
+      const int64_t r = ((int64_t)qb * a.q_heads + h) * a.q_len + qt;
+      lse2 = a.lse[r] * kLog2e;
+      delta = a.delta[r];
+    }
+  }
+
+  int qseg_i = 0, qstart_i = 0, kt_begin_main = 0;
+  if constexpr (MODE == kDoc) {
+    if (valid_q) {
+      qseg_i = a.q_seg[(int64_t)b * a.q_len + i];
+      qstart_i = a.q_start[(int64_t)b * a.q_len + i];
+    }
+    int v = INT_MAX;
+    if (tid < BM && q0 + tid < nq) v = a.q_start[(int64_t)b * a.q_len + q0 + tid];
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+    if (lane == 0) red_lds[wave] = v;
+    __syncthreads();
+    v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
+    kt_begin_main = v < 0 ? 0 : v / BN;
+  }
+  int kt_end = (lim_max_wg + 1 + BN - 1) / BN;
+  if (slot0 && kt_end < 1) kt_end = 1;
+  const int first_main = kt_begin_main > 1 ? kt_begin_main : 1;
+  const bool gap = (MODE == kDoc) && first_main > 1;
+  const int ntiles = gap ? 1 + max(0, kt_end - first_main) : kt_end;
+  auto tile_of = [&](int it) { return gap ? (it == 0 ? 0 : first_main + it - 1) : it; };
+
+  auto key_ptr = [&](const void* base, const int64_t* st, int j) -> const bf16* {
+    if (j >= nk || !(j <= lim_max_wg || (slot0 && j == 0))) return nullptr;
+    if (MODE == kDense && a.key_mask && !a.key_mask[(int64_t)b * a.key_mask_stride + j]) return nullptr;
+    int kb = b, kt = j;
+    if constexpr (MODE == kVarlen) split_flat(a.key_indices[ks + j], a.key_extent, kb, kt);
+    return (const bf16*)base + (int64_t)kb * st[0] + (int64_t)hk * st[1] + (int64_t)kt * st[2];
+  };
+
+  PairTile<BN, D> ktile, vtile;
+  f32x16 dqacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) dqacc[d] = f32x16{};
+  const float sl2 = a.softmax_scale * kLog2e;
+
+  auto load = [&](int n0) {
+    ktile.load(tid, [&](int r) { return key_ptr(a.k, a.k_stride, n0 + r); });
+    vtile.load(tid, [&](int r) { return key_ptr(a.v, a.v_stride, n0 + r); });
+  };
+  if (ntiles > 0) load(tile_of(0) * BN);
+  for (int it = 0; it < ntiles; ++it) {
+    const int n0 = tile_of(it) * BN;
+    __syncthreads();
+    ktile.store_rows(tid, k_lds, KLD);
+    ktile.store_cols(tid, kt_lds, TLD);
+    vtile.store_rows(tid, v_lds, KLD);
+    if constexpr (MODE == kDoc) {
+      if (tid < BN) {
+        const int j = n0 + tid;
+        kseg_lds[tid] = j < nk ? a.k_seg[(int64_t)b * a.kv_len + j] : INT_MIN;
+        kqend_lds[tid] = j < nk ? a.k_qend[(int64_t)b * a.kv_len + j] : 0;
+      }
+    } else if constexpr (MODE == kDense) {
+      if (a.key_mask && tid < BN) {
+        const int j = n0 + tid;
+        kseg_lds[tid] = j < nk ? (int)a.key_mask[(int64_t)b * a.key_mask_stride + j] : 0;
+      }
+    }
+    __syncthreads();
+    if (it + 1 < ntiles) load(tile_of(it + 1) * BN);
+
+    const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    if (!wave_sees) continue;
+
+    f32x16 sacc[BN / 32], pacc[BN / 32];
+#pragma unroll
+    for (int nb = 0; nb < BN / 32; ++nb) {
+      sacc[nb] = f32x16{};
+      pacc[nb] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        sacc[nb] = mfma32(lds_row_operand(k_lds, KLD, nb * 32 + col, s, half), qf[s], sacc[nb]);
+        pacc[nb] = mfma32(lds_row_operand(v_lds, KLD, nb * 32 + col, s, half), gf[s], pacc[nb]);
+      }
+    }
+    const bool full = (MODE != kDoc) && !(MODE == kDense && a.key_mask) && (n0 + BN - 1 <= lim_min_wave) &&
+                      (n0 + BN <= nk);
+#pragma unroll
+    for (int nb = 0; nb < BN / 32; ++nb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        bool keep = true;
+        if (!full) {
+          const int jl = nb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const int j = n0 + jl;
+          keep = (j <= lim_i) || (slot0 && j == 0);
+          if constexpr (MODE == kDense) {
+            if (a.key_mask) keep = keep && kseg_lds[jl] != 0;
+          }
+          if constexpr (MODE == kDoc) {
+            const int ksg = kseg_lds[jl];
+            keep = keep && j < nk && ((ksg == qseg_i && j >= qstart_i) || ksg == -1) && (i < kqend_lds[jl]);
+          }
+        }
+        const float p = keep ? __builtin_amdgcn_exp2f(sacc[nb][r] * sl2 - lse2) : 0.f;
+        sacc[nb][r] = p * (pacc[nb][r] - delta);
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < BN / 16; ++s) {
+      const bf16x8 ds = acc_kperm_operand(sacc[s >> 1], s);
+#pragma unroll
+      for (int d = 0; d < DB; ++d) dqacc[d] = mfma32(lds_kperm_operand(kt_lds, TLD, d * 32 + col, s, half), ds, dqacc[d]);
+    }
+  }
+  if (!valid_q) return;
+  bf16* dqrow = (bf16*)a.dq + (int64_t)qb * a.dq_stride[0] + (int64_t)h * a.dq_stride[1] + (int64_t)qt * a.dq_stride[2];
+  store_acc_row<DB>(dqrow, dqacc, a.softmax_scale, half);
+}
+
+// ------------------------------------------------------------------ dKV ----
+template <int D, int MODE, bool ATOMIC>
+__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a) {
+  constexpr int BNK = 128, BMQ = 64;
+  constexpr int QLD = D + 8, TLD = BMQ + 8;
+  constexpr int KS = D / 16, DB = D / 32;
+  __shared__ __attribute__((aligned(16))) bf16 q_lds[BMQ * QLD];
+  __shared__ __attribute__((aligned(16))) bf16 g_lds[BMQ * QLD];
+  __shared__ __attribute__((aligned(16))) bf16 qt_lds[D * TLD];
+  __shared__ __attribute__((aligned(16))) bf16 gt_lds[D * TLD];
+  __shared__ __attribute__((aligned(16))) float lse_lds[BMQ];
+  __shared__ __attribute__((aligned(16))) float delta_lds[BMQ];
+  __shared__ __attribute__((aligned(16))) int qseg_lds[BMQ];
+  __shared__ __attribute__((aligned(16))) int qstart_lds[BMQ];
+  __shared__ int red_lds[4];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int half = lane >> 5, col = lane & 31;
+  const int hk = blockIdx.y;
+  const int group = a.q_heads / a.kv_heads;
+
+  int b = 0, nq, nk, n0, qs = 0, ks = 0;
+  Bound bound;
+  if constexpr (MODE == kVarlen) {
+    const int ktiles = (a.max_keys + BNK - 1) / BNK;
+    const int seg = blockIdx.x / ktiles;
+    const int tile = (int)(blockIdx.x % ktiles);
+    qs = a.cu_queries[seg];
+    nq = a.cu_queries[seg + 1] - qs;
+    ks = a.cu_keys[seg];
+    nk = a.cu_keys[seg + 1] - ks;
+    n0 = tile * BNK;
+    if (n0 >= nk) return;
+    bound = Bound{nk - nq, INT_MAX, 1, nk};
+  } else {
+    b = blockIdx.z;
+    nq = a.q_len;
+    nk = a.kv_len;
+    n0 = blockIdx.x * BNK;
+    bound = Bound{a.row_offset ? a.row_offset[b] : a.query_offset, a.row_limit ? a.row_limit[b] : INT_MAX,
+                  a.query_stride, nk};
+  }
+  const bool slot0 = a.keep_slot0 && nk > 0;
+
+  // this lane's key
+  const int n = n0 + wave * 32 + col;
+  const bool valid_k = n < nk;
+  bool k_masked_out = false;
+  if (MODE == kDense && a.key_mask && valid_k) k_masked_out = !a.key_mask[(int64_t)b * a.key_mask_stride + n];
+  int kb = b, kslot = n;
+  if constexpr (MODE == kVarlen) {
+    if (valid_k) split_flat(a.key_indices[ks + n], a.key_extent, kb, kslot);
+  }
+  int kseg_n = 0, kqend_n = 0;
+  if constexpr (MODE == kDoc) {
+    if (valid_k) {
+      kseg_n = a.k_seg[(int64_t)b * a.kv_len + n];
+      kqend_n = a.k_qend[(int64_t)b * a.kv_len + n];
+    }
+  }
+  // first query row that can see any key of the workgroup / of this wave
+  const int wg_first_key = n0;
+  int m_begin = (slot0 && wg_first_key == 0) ? 0 : bound.first_row(wg_first_key, nq);
+  int m_end = nq;
+  if constexpr (MODE == kDoc) {
+    int v = valid_k ? kqend_n : 0;
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    if (lane == 0) red_lds[wave] = v;
+    __syncthreads();
+    v = max(max(red_lds[0], red_lds[1]), max(red_lds[2], red_lds[3]));
+    m_end = min(m_end, v);
+  }
+  const int wave_key0 = n0 + wave * 32;
+  const bool wave_live = wave_key0 < nk;
+  const int wave_m_begin = (slot0 && wave_key0 == 0) ? 0 : bound.first_row(wave_key0, nq);
+
+  bf16x8 kf[KS], vf[KS];
+  {
+    const bool live = valid_k && !k_masked_out;
+    const bf16* krow = (const bf16*)a.k + (int64_t)kb * a.k_stride[0] + (int64_t)hk * a.k_stride[1] +
+                       (int64_t)kslot * a.k_stride[2];
+    const bf16* vrow = (const bf16*)a.v + (int64_t)kb * a.v_stride[0] + (int64_t)hk * a.v_stride[1] +
+                       (int64_t)kslot * a.v_stride[2];
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      u32x4 wk = {0u, 0u, 0u, 0u}, wv = {0u, 0u, 0u, 0u};
+      if (live) {
+        wk = load16(krow + 16 * s + 8 * half);
+        wv = load16(vrow + 16 * s + 8 * half);
+      }
+      kf[s] = as_bf16x8(wk);
+      vf[s] = as_bf16x8(wv);
+    }
+  }
+
+  f32x16 dkacc[DB], dvacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+    dkacc[d] = f32x16{};
+    dvacc[d] = f32x16{};
+  }
+  const float sl2 = a.softmax_scale * kLog2e;
+  PairTile<BMQ, D> qtile, gtile;
+
+  for (int hq = hk * group; hq < (hk + 1) * group; ++hq) {
+    for (int m0 = (m_begin / BMQ) * BMQ; m0 < m_end; m0 += BMQ) {
+      auto qloc = [&](int m, int& rb, int& rt) -> bool {
+        if (m >= nq) return false;
+        rb = b;
+        rt = m;
+        if constexpr (MODE == kVarlen) split_flat(a.query_indices[qs + m], a.query_extent, rb, rt);
+        return true;
+      };
+      qtile.load(tid, [&](int r) -> const bf16* {
+        int rb, rt;
+        if (!qloc(m0 + r, rb, rt)) return nullptr;
+        return (const bf16*)a.q + (int64_t)rb * a.q_stride[0] + (int64_t)hq * a.q_stride[1] + (int64_t)rt * a.q_stride[2];
+      });
+      gtile.load(tid, [&](int r) -> const bf16* {
+        int rb, rt;
+        if (!qloc(m0 + r, rb, rt)) return nullptr;
+        return (const bf16*)a.dout + (int64_t)rb * a.do_stride[0] + (int64_t)hq * a.do_stride[1] +
+               (int64_t)rt * a.do_stride[2];
+      });
+      float lse_v = kPosInf, delta_v = 0.f;
+      int qseg_v = INT_MIN, qstart_v = INT_MAX;
+      if (tid < BMQ) {
+        int rb, rt;
+        if (qloc(m0 + tid, rb, rt)) {
+          const int64_t r = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
+          lse_v = a.lse[r] * kLog2e;
+          delta_v = a.delta[r];
+          if constexpr (MODE == kDoc) {
+            qseg_v = a.q_seg[(int64_t)b * a.q_len + m0 + tid];
+            qstart_v = a.q_start[(int64_t)b * a.q_len + m0 + tid];
+          }
+        }
+      }
+      __syncthreads();
+      qtile.store_rows(tid, q_lds, QLD);
+      qtile.store_cols(tid, qt_lds, TLD);
+      gtile.store_rows(tid, g_lds, QLD);
+      gtile.store_cols(tid, gt_lds, TLD);
+      if (tid < BMQ) {
+        lse_lds[tid] = lse_v;
+        delta_lds[tid] = delta_v;
+        qseg_lds[tid] = qseg_v;
+        qstart_lds[tid] = qstart_v;
+      }
+      __syncthreads();
+      if (!wave_live || m0 + BMQ <= wave_m_begin) continue;
+
+      f32x16 sacc[BMQ / 32], pacc[BMQ / 32];
+#pragma unroll
+      for (int mb = 0; mb < BMQ / 32; ++mb) {
+        sacc[mb] = f32x16{};
+        pacc[mb] = f32x16{};
+#pragma unroll
+        for (int s = 0; s < KS; ++s) {
+          sacc[mb] = mfma32(lds_row_operand(q_lds, QLD, mb * 32 + col, s, half), kf[s], sacc[mb]);
+          pacc[mb] = mfma32(lds_row_operand(g_lds, QLD, mb * 32 + col, s, half), vf[s], pacc[mb]);
+        }
+      }
+#pragma unroll
+      for (int mb = 0; mb < BMQ / 32; ++mb) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ml = mb * 32 + 8 * g + 4 * half;
+          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse_lds[ml]);
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&delta_lds[ml]);
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int r = 4 * g + e;
+            const int m = m0 + ml + e;
+            bool keep = valid_k && !k_masked_out && m < nq && ((n <= bound(m)) || (slot0 && n == 0));
+            if constexpr (MODE == kDoc) {
+              const int qsg = qseg_lds[ml + e];
+              keep = keep && ((qsg == kseg_n && n >= qstart_lds[ml + e]) || kseg_n == -1) && (m < kqend_n);
+            }
+            const float p = keep ? __builtin_amdgcn_exp2f(sacc[mb][r] * sl2 - l4[e]) : 0.f;
+            sacc[mb][r] = p;
+            pacc[mb][r] = p * (pacc[mb][r] - d4[e]);
+          }
+        }
+      }
+#pragma unroll
+      for (int s = 0; s < BMQ / 16; ++s) {
+        const bf16x8 pop = acc_kperm_operand(sacc[s >> 1], s);
+        const bf16x8 dsop = acc_kperm_operand(pacc[s >> 1], s);
+#pragma unroll
+        for (int d = 0; d < DB; ++d) {
+          dvacc[d] = mfma32(lds_kperm_operand(gt_lds, TLD, d * 32 + col, s, half), pop, dvacc[d]);
+          dkacc[d] = mfma32(lds_kperm_operand(qt_lds, TLD, d * 32 + col, s, half), dsop, dkacc[d]);
+        }
+      }
+    }
+  }
+
+  if (!valid_k) return;
+  if constexpr (ATOMIC) {
+    // fp32 accumulators laid out [key_indices row][kv head][D]
+    const int64_t row = (int64_t)kb * a.key_extent + kslot;
+    float* acck = (float*)a.workspace + (row * a.kv_heads + hk) * D;
+    float* accv = acck + (int64_t)a.batch * a.key_extent * a.kv_heads * D;
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const int dd = d * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+        atomicAdd(acck + dd, dkacc[d][r] * a.softmax_scale);
+        atomicAdd(accv + dd, dvacc[d][r]);
+      }
+    }
+  } else {
+    bf16* dkrow = (bf16*)a.dk + (int64_t)kb * a.dk_stride[0] + (int64_t)hk * a.dk_stride[1] + (int64_t)kslot * a.dk_stride[2];
+    bf16* dvrow = (bf16*)a.dv + (int64_t)kb * a.dv_stride[0] + (int64_t)hk * a.dv_stride[1] + (int64_t)kslot * a.dv_stride[2];
+    store_acc_row<DB>(dkrow, dkacc, a.softmax_scale, half);
+    store_acc_row<DB>(dvrow, dvacc, 1.f, half);
+  }
+}
+
+// ----------------------------------------------- varlen accumulator glue ----
+__global__ void zero_f32_kernel(float* p, int64_t n) {
+  const int64_t i = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * 4;
+  if (i + 3 < n) {
+    *reinterpret_cast<f32x4*>(p + i) = f32x4{0.f, 0.f, 0.f, 0.f};
+  } else {
+    for (int64_t k = i; k < n; ++k) p[k] = 0.f;
+  }
+}
+
+// Convert the fp32 [B*N][Hkv][D] accumulators to bf16 dK/dV with their strides.
+__global__ void acc_to_bf16_kernel(const wmx_attn_args a) {
+  const int D = a.head_dim;
+  const int64_t total = (int64_t)a.batch * a.key_extent * a.kv_heads * D;
+  const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (idx >= total) return;
+  const int d = (int)(idx % D);
+  const int64_t rh = idx / D;
+  const int h = (int)(rh % a.kv_heads);
+  const int64_t row = rh / a.kv_heads;
+  const int b = (int)(row / a.key_extent);
+  const int slot = (int)(row % a.key_extent);
+  const float* acck = (const float*)a.workspace;
+  const float* accv = acck + total;
+  ((bf16*)a.dk)[(int64_t)b * a.dk_stride[0] + (int64_t)h * a.dk_stride[1] + (int64_t)slot * a.dk_stride[2] + d] =
+      (__bf16)acck[idx];
+  ((bf16*)a.dv)[(int64_t)b * a.dv_stride[0] + (int64_t)h * a.dv_stride[1] + (int64_t)slot * a.dv_stride[2] + d] =
+      (__bf16)accv[idx];
+}
+
+// ------------------------------------------------------------- launchers ----
+int launch_bwd_preprocess(const wmx_attn_args& a, hipStream_t stream) {
+  const int64_t rows = (int64_t)a.batch * a.q_heads * a.q_len;
+  if (rows == 0) return WMX_OK;
+  const dim3 grid((unsigned)((rows + 15) / 16));
+  switch (a.head_dim) {
+    case 64: hipLaunchKernelGGL(bwd_delta_kernel<64>, grid, dim3(256), 0, stream, a, rows); break;
+    case 96: hipLaunchKernelGGL(bwd_delta_kernel<96>, grid, dim3(256), 0, stream, a, rows); break;
+    case 128: hipLaunchKernelGGL(bwd_delta_kernel<128>, grid, dim3(256), 0, stream, a, rows); break;
+    default: return WMX_E_UNSUPPORTED;
+  }
+  return WMX_OK;
+}
+
+int64_t bwd_workspace_size(const wmx_attn_args& a) {
+  if (!a.query_indices || a.keys_unique) return 0;
+  return (int64_t)2 * a.batch * a.key_extent * a.kv_heads * a.head_dim * (int64_t)sizeof(float);
+}
+
+template <int D, int MODE>
+static int launch_bwd_t(const wmx_attn_args& a, hipStream_t stream) {
+  dim3 gq, gk;
+  if (MODE == kVarlen) {
+    if (a.num_segments <= 0) return WMX_OK;
+    gq = dim3((unsigned)(((a.max_queries + 127) / 128) * (int64_t)a.num_segments), a.q_heads, 1);
+    gk = dim3((unsigned)(((a.max_keys + 127) / 128) * (int64_t)a.num_segments), a.kv_heads, 1);
+  } else {
+    gq = dim3((a.q_len + 127) / 128, a.q_heads, a.batch);
+    gk = dim3((a.kv_len + 127) / 128, a.kv_heads, a.batch);
+  }
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), gq, dim3(256), 0, stream, a);
+  if (MODE == kVarlen && !a.keys_unique) {
+    const int64_t n = bwd_workspace_size(a) / (int64_t)sizeof(float);
+    hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,
+                       (float*)a.workspace, n);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true>), gk, dim3(256), 0, stream, a);
+    const int64_t total = n / 2;
+    hipLaunchKernelGGL(acc_to_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false>), gk, dim3(256), 0, stream, a);
+  }
+  return WMX_OK;
+}
+
+template <int MODE>
+static int launch_bwd_mode(const wmx_attn_args& a, hipStream_t stream) {
+  switch (a.head_dim) {
+    case 64: return launch_bwd_t<64, MODE>(a, stream);
+    case 96: return launch_bwd_t<96, MODE>(a, stream);
+    case 128: return launch_bwd_t<128, MODE>(a, stream);
+    default: return WMX_E_UNSUPPORTED;
+  }
+}
+
+int launch_bwd(const wmx_attn_args& a, hipStream_t stream) {
+  int rc = launch_bwd_preprocess(a, stream);
+  if (rc != WMX_OK) return rc;
+  if (a.query_indices) return launch_bwd_mode<kVarlen>(a, stream);
+  if (a.q_seg) return launch_bwd_mode<kDoc>(a, stream);
+  return launch_bwd_mode<kDense>(a, stream);
+}
+
+}  // namespace wmx

@@ -1,0 +1,159 @@
+// extern "C" entry points of libwmx_attn.so (declared in include/wmx_attn.h).
+// Each entry point checks what the kernels assume about shapes, strides and
+// alignment before anything is launched, so a bad call returns an error code
+// instead of reaching the GPU.
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "wmx_kernels.h"
+
+namespace {
+
+thread_local char g_error[512] = "";
+
+int fail(int code, const char* fmt, ...) __attribute__((format(printf, 2, 3)));
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_error, sizeof(g_error), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+bool aligned16(const void* p) { return ((uintptr_t)p & 15u) == 0; }
+bool aligned8(const void* p) { return ((uintptr_t)p & 7u) == 0; }
+
+// Row starts must stay 16-byte aligned for the 16-byte loads.
+bool strides_vec8(const int64_t* s, int n) {
+  for (int i = 0; i < n; ++i)
+    if (s[i] % 8 != 0) return false;
+  return true;
+}
+
+int check_common(const wmx_attn_args* a, bool backward) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->head_dim != 64 && a->head_dim != 96 && a->head_dim != 128)
+    return fail(WMX_E_UNSUPPORTED, "head_dim %d is not 64, 96 or 128", a->head_dim);
+  if (a->batch < 0 || a->q_heads <= 0 || a->kv_heads <= 0 || a->q_len < 0 || a->kv_len < 0)
+    return fail(WMX_E_INVALID, "negative or zero shape");
+  if (a->q_heads % a->kv_heads != 0) return fail(WMX_E_INVALID, "q_heads %% kv_heads != 0");
+  if (a->query_stride < 1) return fail(WMX_E_INVALID, "query_stride must be >= 1");
+  if (!(a->softmax_scale == a->softmax_scale)) return fail(WMX_E_INVALID, "softmax_scale is NaN");
+  if (!a->q || !a->k || !a->v || !a->o || !a->lse) return fail(WMX_E_INVALID, "q/k/v/o/lse pointer is NULL");
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v))
+    return fail(WMX_E_INVALID, "q/k/v must be 16-byte aligned");
+  if (!aligned8(a->o)) return fail(WMX_E_INVALID, "o must be 8-byte aligned");
+  if (!strides_vec8(a->q_stride, 3) || !strides_vec8(a->k_stride, 3) || !strides_vec8(a->v_stride, 3))
+    return fail(WMX_E_INVALID, "q/k/v strides must be multiples of 8 elements");
+  if (!strides_vec8(a->o_stride, 3)) return fail(WMX_E_INVALID, "o strides must be multiples of 8 elements");
+  if (a->query_indices) {
+    if (!a->key_indices || !a->cu_queries || !a->cu_keys)
+      return fail(WMX_E_INVALID, "varlen schedule needs key_indices, cu_queries and cu_keys");
+    if (a->num_segments < 0 || a->max_queries < 0 || a->max_keys < 0 || a->query_extent <= 0 || a->key_extent <= 0)
+      return fail(WMX_E_INVALID, "invalid varlen sizes");
+    if (a->q_seg) return fail(WMX_E_INVALID, "varlen schedule and document metadata are exclusive");
+    if (a->key_mask) return fail(WMX_E_INVALID, "varlen schedule and key_mask are exclusive");
+    if (a->row_offset || a->row_limit) return fail(WMX_E_INVALID, "varlen schedule takes no row offsets");
+  }
+  if (a->q_seg && (!a->k_seg || !a->q_start || !a->k_qend))
+    return fail(WMX_E_INVALID, "document metadata needs all four arrays");
+  if (a->q_seg && a->key_mask) return fail(WMX_E_INVALID, "document metadata and key_mask are exclusive");
+  if (backward) {
+    if (!a->dout || !a->delta || !a->dq || !a->dk || !a->dv)
+      return fail(WMX_E_INVALID, "dout/delta/dq/dk/dv pointer is NULL");
+    if (!aligned16(a->dout)) return fail(WMX_E_INVALID, "dout must be 16-byte aligned");
+    if (!aligned8(a->dq) || !aligned8(a->dk) || !aligned8(a->dv))
+      return fail(WMX_E_INVALID, "dq/dk/dv must be 8-byte aligned");
+    if (!strides_vec8(a->do_stride, 3) || !strides_vec8(a->dq_stride, 3) || !strides_vec8(a->dk_stride, 3) ||
+        !strides_vec8(a->dv_stride, 3))
+      return fail(WMX_E_INVALID, "gradient strides must be multiples of 8 elements");
+    const int64_t need = wmx::bwd_workspace_size(*a);
+    if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+      return fail(WMX_E_WORKSPACE, "backward needs %lld workspace bytes", (long long)need);
+  }
+  return WMX_OK;
+}
+
+int launched(int rc) {
+  if (rc != WMX_OK) {
+    if (rc == WMX_E_UNSUPPORTED) return fail(rc, "unsupported configuration");
+    return rc;
+  }
+  const hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return fail(WMX_E_LAUNCH, "launch failed: %s", hipGetErrorString(e));
+  return WMX_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int wmx_abi_version(void) { return WMX_ABI_VERSION; }
+size_t wmx_attn_args_size(void) { return sizeof(wmx_attn_args); }
+size_t wmx_decode_args_size(void) { return sizeof(wmx_decode_args); }
+const char* wmx_last_error(void) { return g_error; }
+
+int wmx_attn_fwd(const wmx_attn_args* args, void* stream) {
+  int rc = check_common(args, false);
+  if (rc != WMX_OK) return rc;
+  if (args->batch == 0 || args->q_len == 0) return WMX_OK;
+  return launched(wmx::launch_fwd(*args, (hipStream_t)stream));
+}
+
+int wmx_attn_bwd_preprocess(const wmx_attn_args* args, void* stream) {
+  if (!args) return fail(WMX_E_INVALID, "args is NULL");
+  if (args->head_dim != 64 && args->head_dim != 96 && args->head_dim != 128)
+    return fail(WMX_E_UNSUPPORTED, "head_dim %d is not 64, 96 or 128", args->head_dim);
+  if (!args->o || !args->dout || !args->delta) return fail(WMX_E_INVALID, "o/dout/delta pointer is NULL");
+  if (!aligned16(args->o) || !aligned16(args->dout)) return fail(WMX_E_INVALID, "o/dout must be 16-byte aligned");
+  if (!strides_vec8(args->o_stride, 3) || !strides_vec8(args->do_stride, 3))
+    return fail(WMX_E_INVALID, "o/dout strides must be multiples of 8 elements");
+  return launched(wmx::launch_bwd_preprocess(*args, (hipStream_t)stream));
+}
+
+int64_t wmx_attn_bwd_workspace_size(const wmx_attn_args* args) {
+  return args ? wmx::bwd_workspace_size(*args) : 0;
+}
+
+int wmx_attn_bwd(const wmx_attn_args* args, void* stream) {
+  int rc = check_common(args, true);
+  if (rc != WMX_OK) return rc;
+  if (!aligned16(args->o)) return fail(WMX_E_INVALID, "o must be 16-byte aligned for the backward");
+  if (args->batch == 0 || args->q_len == 0) return WMX_OK;
+  return launched(wmx::launch_bwd(*args, (hipStream_t)stream));
+}
+
+int64_t wmx_decode_workspace_size(const wmx_decode_args* args) {
+  return args ? wmx::decode_workspace_size(*args) : 0;
+}
+
+int32_t wmx_decode_num_splits(const wmx_decode_args* args) { return args ? wmx::decode_num_splits(*args) : 0; }
+
+int wmx_decode(const wmx_decode_args* a, void* stream) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->head_dim != 64 && a->head_dim != 96 && a->head_dim != 128)
+    return fail(WMX_E_UNSUPPORTED, "head_dim %d is not 64, 96 or 128", a->head_dim);
+  if (a->batch < 0 || a->q_heads <= 0 || a->kv_heads <= 0 || a->capacity < 0)
+    return fail(WMX_E_INVALID, "negative or zero shape");
+  if (a->q_heads % a->kv_heads != 0) return fail(WMX_E_INVALID, "q_heads %% kv_heads != 0");
+  const int g = a->q_heads / a->kv_heads;
+  if (g != 1 && g != 2 && g != 4 && g != 8)
+    return fail(WMX_E_UNSUPPORTED, "decode supports query heads per KV head in {1,2,4,8}, got %d", g);
+  if (!a->q || !a->k || !a->v || !a->o) return fail(WMX_E_INVALID, "q/k/v/o pointer is NULL");
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v))
+    return fail(WMX_E_INVALID, "q/k/v must be 16-byte aligned");
+  if (a->q_stride[0] % 8 || a->q_stride[1] % 8 || !strides_vec8(a->k_stride, 3) || !strides_vec8(a->v_stride, 3))
+    return fail(WMX_E_INVALID, "q/k/v strides must be multiples of 8 elements");
+  if (a->use_dummy != 0 && a->use_dummy != 1) return fail(WMX_E_INVALID, "use_dummy must be 0 or 1");
+  const int64_t need = wmx::decode_workspace_size(*a);
+  if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+    return fail(WMX_E_WORKSPACE, "decode needs %lld workspace bytes", (long long)need);
+  if (a->batch == 0 || a->capacity == 0) {
+    // nothing visible: the caller's zero-filled output stands
+    return WMX_OK;
+  }
+  return launched(wmx::launch_decode(*a, (hipStream_t)stream));
+}
+
+}  // extern "C"

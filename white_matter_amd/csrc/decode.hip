@@ -1,0 +1,276 @@
+// Single-query decode over a KV pool for gfx950: bandwidth-bound split-K.
+//
+// Replaces the reference's cached decode (flash_attn_with_kvcache /
+// aten._flash_attention_forward with seqused_k,
+// src/white_matter/ops/flash_attention.py:15-103) and its key_mask packing
+// (src/white_matter/ops/strict_causal_attention.py:238-263): the mask is
+// applied while streaming, so the cache is never gathered or copied.
+//
+// Work unit: one workgroup = (batch row b, KV head, key split). It streams
+// its key range once and serves all G = Hq/Hkv query heads of the KV head,
+// so each K/V byte is read from HBM once. A key row of D bf16 is read by
+// LPR lanes with 16-byte loads (D=128: 16 lanes, 4 rows per wave load),
+// UNROLL row groups are in flight per wave. Scores are dot products on the
+// VALU (arithmetic intensity ~2G flop/byte, far below the MFMA ridge).
+// Each split writes an unnormalised (o, max, sum) partial; a second kernel
+// merges the splits in log-sum-exp form and writes bf16 output.
+#include <climits>
+
+#include "wmx_kernels.h"
+
+namespace wmx {
+
+constexpr int kDecodeUnroll = 8;
+constexpr int kDecodeChunkMin = 256;
+
+struct DecodeLen {
+  int64_t len;        // keys j < len may be visible
+  bool masked;        // key_mask applies
+};
+
+__device__ __forceinline__ DecodeLen decode_len(const wmx_decode_args& a, int b) {
+  const int64_t start = a.query_start ? a.query_start[b] : a.query_start_scalar;
+  int64_t bound = start;
+  if (a.kv_lengths) bound = min(bound, a.kv_lengths[b]);
+  DecodeLen r;
+  if (a.key_mask) {
+    r.len = bound + a.use_dummy;
+    r.masked = true;
+  } else {
+    const int64_t cap = (int64_t)a.capacity - a.use_dummy;
+    bound = bound < 0 ? 0 : (bound > cap ? cap : bound);
+    r.len = bound + a.use_dummy;
+    r.masked = false;
+  }
+  if (r.len > a.capacity) r.len = a.capacity;
+  return r;
+}
+
+template <int D, int G>
+__global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args a, int chunk) {
+  constexpr int LPR = D <= 64 ? 8 : 16;   // lanes per key row
+  constexpr int RPW = 64 / LPR;           // rows per wave load
+  constexpr int ROWS_ITER = 4 * RPW * kDecodeUnroll;
+  __shared__ float lds_m[4][G], lds_l[4][G];
+  __shared__ __attribute__((aligned(16))) float lds_o[4][G][D];
+
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int dch = lane % LPR, rslot = lane / LPR;
+  const bool dlive = 8 * dch < D;
+  const int split = blockIdx.x, hk = blockIdx.y, b = blockIdx.z;
+  const int nsplit = gridDim.x;
+  const int group = a.q_heads / a.kv_heads;
+  const int h0 = hk * group;  // first query head of this KV head (G == group)
+
+  const DecodeLen dl = decode_len(a, b);
+  const int64_t j_begin = (int64_t)split * chunk;
+  int64_t j_end = j_begin + chunk;
+  if (j_end > dl.len) j_end = dl.len;
+
+  const float qscale = a.softmax_scale * kLog2e;
+  float q[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    u32x4 w = {0u, 0u, 0u, 0u};
+    if (dlive) w = load16((const bf16*)a.q + (int64_t)b * a.q_stride[0] + (int64_t)(h0 + g) * a.q_stride[1] + 8 * dch);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      q[g][2 * e] = bf16_lo(w[e]) * qscale;
+      q[g][2 * e + 1] = bf16_hi(w[e]) * qscale;
+    }
+  }
+  float m[G], l[G], o[G][8];
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    m[g] = kNegInf;
+    l[g] = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = 0.f;
+  }
+
+  const bf16* kbase = (const bf16*)a.k + (int64_t)b * a.k_stride[0] + (int64_t)hk * a.k_stride[1] + 8 * dch;
+  const bf16* vbase = (const bf16*)a.v + (int64_t)b * a.v_stride[0] + (int64_t)hk * a.v_stride[1] + 8 * dch;
+  const uint8_t* kmask = a.key_mask ? a.key_mask + (int64_t)b * a.key_mask_stride : nullptr;
+
+  for (int64_t it = j_begin; it < j_end; it += ROWS_ITER) {
+    u32x4 kw[kDecodeUnroll], vw[kDecodeUnroll];
+    bool vis[kDecodeUnroll];
+#pragma unroll
+    for (int u = 0; u < kDecodeUnroll; ++u) {
+      const int64_t j = it + (int64_t)(u * 4 + wave) * RPW + rslot;
+      bool ok = j < j_end;
+      if (ok && dl.masked) ok = kmask[j] != 0;
+      vis[u] = ok;
+      u32x4 zk = {0u, 0u, 0u, 0u}, zv = {0u, 0u, 0u, 0u};
+      if (ok && dlive) {
+        zk = load16(kbase + j * a.k_stride[2]);
+        zv = load16(vbase + j * a.v_stride[2]);
+      }
+      kw[u] = zk;
+      vw[u] = zv;
+    }
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      float s[kDecodeUnroll];
+      float smax = kNegInf;
+#pragma unroll
+      for (int u = 0; u < kDecodeUnroll; ++u) {
+        float acc = 0.f;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          acc = fmaf(q[g][2 * e], bf16_lo(kw[u][e]), acc);
+          acc = fmaf(q[g][2 * e + 1], bf16_hi(kw[u][e]), acc);
+        }
+#pragma unroll
+        for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        s[u] = vis[u] ? acc : kNegInf;
+        smax = fmaxf(smax, s[u]);
+      }
+      const float m_new = fmaxf(m[g], smax);
+      const float m_use = fmaxf(m_new, kMaxFloor);
+      const float alpha = __builtin_amdgcn_exp2f(m[g] - m_use);
+      l[g] *= alpha;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] *= alpha;
+#pragma unroll
+      for (int u = 0; u < kDecodeUnroll; ++u) {
+        const float p = __builtin_amdgcn_exp2f(s[u] - m_use);
+        l[g] += p;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          o[g][2 * e] = fmaf(p, bf16_lo(vw[u][e]), o[g][2 * e]);
+          o[g][2 * e + 1] = fmaf(p, bf16_hi(vw[u][e]), o[g][2 * e + 1]);
+        }
+      }
+      m[g] = m_new;
+    }
+  }
+
+  // merge the RPW row slots of the wave (lanes with equal dch)
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+#pragma unroll
+    for (int off = LPR; off < 64; off <<= 1) {
+      const float mo = __shfl_xor(m[g], off);
+      const float lo = __shfl_xor(l[g], off);
+      const float mx = fmaxf(fmaxf(m[g], mo), kMaxFloor);
+      const float sa = __builtin_amdgcn_exp2f(m[g] - mx), sb = __builtin_amdgcn_exp2f(mo - mx);
+      l[g] = l[g] * sa + lo * sb;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) o[g][e] = o[g][e] * sa + __shfl_xor(o[g][e], off) * sb;
+      m[g] = fmaxf(m[g], mo);
+    }
+  }
+  if (rslot == 0) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+      if (dch == 0) {
+        lds_m[wave][g] = m[g];
+        lds_l[wave][g] = l[g];
+      }
+      if (dlive) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) lds_o[wave][g][8 * dch + e] = o[g][e];
+      }
+    }
+  }
+  __syncthreads();
+  // merge the 4 waves and write the split's partial row
+  float* ws_o = (float*)a.workspace;
+  float* ws_ml = ws_o + (int64_t)a.batch * a.q_heads * nsplit * D;
+  for (int idx = tid; idx < G * D; idx += 256) {
+    const int g = idx / D, d = idx % D;
+    float mx = kMaxFloor;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, lds_m[w][g]);
+    float acc = 0.f;
+#pragma unroll
+    for (int w = 0; w < 4; ++w) acc += lds_o[w][g][d] * __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
+    const int64_t prow = ((int64_t)b * a.q_heads + h0 + g) * nsplit + split;
+    ws_o[prow * D + d] = acc;
+    if (d == 0) {
+      float lsum = 0.f, mraw = kNegInf;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        lsum += lds_l[w][g] * __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
+        mraw = fmaxf(mraw, lds_m[w][g]);
+      }
+      ws_ml[prow * 2 + 0] = mraw == kNegInf ? kNegInf : mx;
+      ws_ml[prow * 2 + 1] = lsum;
+    }
+  }
+}
+
+// One workgroup of D threads per (b, query head): merge the splits.
+__global__ void decode_combine_kernel(const wmx_decode_args a, int nsplit) {
+  const int D = a.head_dim;
+  const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  const float* ws_o = (const float*)a.workspace;
+  const float* ws_ml = ws_o + (int64_t)a.batch * a.q_heads * nsplit * D;
+  const int64_t prow0 = ((int64_t)b * a.q_heads + h) * nsplit;
+  float mx = kMaxFloor;
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ws_ml[(prow0 + s) * 2]);
+  float lsum = 0.f, acc = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float w = __builtin_amdgcn_exp2f(ws_ml[(prow0 + s) * 2] - mx);
+    lsum += ws_ml[(prow0 + s) * 2 + 1] * w;
+    if (d < D) acc += ws_o[(prow0 + s) * D + d] * w;
+  }
+  if (d < D) {
+    const float r = lsum > 0.f ? acc / lsum : 0.f;
+    ((bf16*)a.o)[(int64_t)b * a.o_stride[0] + (int64_t)h * a.o_stride[1] + d] = (__bf16)r;
+  }
+}
+
+int decode_num_splits(const wmx_decode_args& a) {
+  if (a.num_splits > 0) return a.num_splits;
+  // aim for >= 4 workgroups per CU (256 CUs) with chunks of at least kDecodeChunkMin keys
+  const int64_t units = (int64_t)a.batch * a.kv_heads;
+  int64_t splits = (4 * 256 + units - 1) / units;
+  const int64_t max_splits = (a.capacity + kDecodeChunkMin - 1) / kDecodeChunkMin;
+  if (splits > max_splits) splits = max_splits;
+  if (splits < 1) splits = 1;
+  return (int)splits;
+}
+
+int64_t decode_workspace_size(const wmx_decode_args& a) {
+  const int64_t s = decode_num_splits(a);
+  return (int64_t)a.batch * a.q_heads * s * (a.head_dim + 2) * (int64_t)sizeof(float);
+}
+
+template <int D, int G>
+static void launch_decode_t(const wmx_decode_args& a, int nsplit, int chunk, hipStream_t stream) {
+  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3(nsplit, a.kv_heads, a.batch), dim3(256), 0, stream, a, chunk);
+}
+
+template <int D>
+static int launch_decode_d(const wmx_decode_args& a, int nsplit, int chunk, hipStream_t stream) {
+  switch (a.q_heads / a.kv_heads) {
+    case 1: launch_decode_t<D, 1>(a, nsplit, chunk, stream); return WMX_OK;
+    case 2: launch_decode_t<D, 2>(a, nsplit, chunk, stream); return WMX_OK;
+    case 4: launch_decode_t<D, 4>(a, nsplit, chunk, stream); return WMX_OK;
+    case 8: launch_decode_t<D, 8>(a, nsplit, chunk, stream); return WMX_OK;
+    default: return WMX_E_UNSUPPORTED;
+  }
+}
+
+int launch_decode(const wmx_decode_args& a, hipStream_t stream) {
+  if (a.batch == 0 || a.q_heads == 0) return WMX_OK;
+  const int nsplit = decode_num_splits(a);
+  int chunk = (a.capacity + nsplit - 1) / nsplit;
+  chunk = (chunk + 63) / 64 * 64;
+  if (chunk < 64) chunk = 64;
+  int rc;
+  switch (a.head_dim) {
+    case 64: rc = launch_decode_d<64>(a, nsplit, chunk, stream); break;
+    case 96: rc = launch_decode_d<96>(a, nsplit, chunk, stream); break;
+    case 128: rc = launch_decode_d<128>(a, nsplit, chunk, stream); break;
+    default: return WMX_E_UNSUPPORTED;
+  }
+  if (rc != WMX_OK) return rc;
+  const int threads = (a.head_dim + 63) / 64 * 64;
+  hipLaunchKernelGGL(decode_combine_kernel, dim3(a.q_heads, a.batch), dim3(threads), 0, stream, a, nsplit);
+  return WMX_OK;
+}
+
+}  // namespace wmx

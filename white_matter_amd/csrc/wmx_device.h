@@ -1,0 +1,178 @@
+// Device helpers shared by the gfx950 attention kernels.
+//
+// Operand layouts of v_mfma_f32_32x32x16_bf16 (one wave64):
+//   A (32 x 16): lane l holds row l % 32, k = 8 * (l / 32) + [0, 8)
+//   B (16 x 32): lane l holds column l % 32, k = 8 * (l / 32) + [0, 8)
+//   C (32 x 32): lane l, register r holds column l % 32,
+//                row 8 * (r / 4) + 4 * (l / 32) + r % 4
+// A product whose contraction index is read from an accumulator (for
+// example P in O^T = V^T P^T) uses the accumulator's row order as its k
+// order: lane half h supplies k = {16s + 4h + [0,4), 16s + 8 + 4h + [0,4)}
+// for k-step s, which is registers 8(s%2) .. 8(s%2)+7 of 32-row block s/2.
+// The other operand of that product reads the same k order from LDS.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "wmx_attn.h"
+
+namespace wmx {
+
+typedef __bf16 bf16;
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef __bf16 bf16x4 __attribute__((ext_vector_type(4)));
+typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.6931471805599453f;
+constexpr float kNegInf = -__builtin_inff();
+constexpr float kPosInf = __builtin_inff();
+// An unchanged running maximum must rescale by exactly one, and a row that
+// has seen only masked scores must produce zero weights (not NaN).
+constexpr float kMaxFloor = -1e30f;
+
+__device__ __forceinline__ f32x16 mfma32(const bf16x8& a, const bf16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_bf16(a, b, c, 0, 0, 0);
+}
+
+__device__ __forceinline__ float bf16_lo(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16_hi(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
+
+// Two fp32 values to a packed bf16 pair (round to nearest even, hardware cvt).
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+  typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+  bf16x2 r;
+  r[0] = (__bf16)lo;
+  r[1] = (__bf16)hi;
+  return __builtin_bit_cast(uint32_t, r);
+}
+
+__device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_bit_cast(bf16x8, v); }
+
+__device__ __forceinline__ u32x4 load16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
+__device__ __forceinline__ void store8(bf16* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
+
+// Swap values between lane l and lane l ^ 32 (the two halves of a wave).
+__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+
+// Row-addressing of one operand: dense (b fixed, row t) or varlen (flat index).
+struct RowSource {
+  const bf16* base;
+  int64_t sb, sh, st;
+};
+
+__device__ __forceinline__ const bf16* row_ptr(const RowSource& s, int b, int h, int t) {
+  return s.base + (int64_t)b * s.sb + (int64_t)h * s.sh + (int64_t)t * s.st;
+}
+
+// Flat varlen index -> (row, slot) for a row width `extent`.
+__device__ __forceinline__ void split_flat(int64_t flat, int extent, int& b, int& t) {
+  b = (int)(flat / extent);
+  t = (int)(flat - (int64_t)b * extent);
+}
+
+// A [ROWS x D] bf16 tile staged through registers, read as row pairs so the
+// same registers can be written to LDS row-major, transposed, or both.
+// rp(r) returns the global row pointer of tile row r, or nullptr for a row
+// that must read as zeros (outside the problem or beyond every reader's reach).
+template <int ROWS, int D, int NT = 256>
+struct PairTile {
+  static constexpr int CPR = D / 8;
+  static constexpr int N = ROWS / 2 * CPR;
+  static constexpr int PER = (N + NT - 1) / NT;
+  u32x4 x[PER], y[PER];
+
+  template <class RowPtr>
+  __device__ __forceinline__ void load(int tid, RowPtr rp) {
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int c = tid + NT * r;
+      u32x4 wx = {0u, 0u, 0u, 0u}, wy = {0u, 0u, 0u, 0u};
+      if (c < N) {
+        const int p = c / CPR, cc = c % CPR;
+        const bf16* ra = rp(2 * p);
+        const bf16* rb = rp(2 * p + 1);
+        if (ra) wx = load16(ra + 8 * cc);
+        if (rb) wy = load16(rb + 8 * cc);
+      }
+      x[r] = wx;
+      y[r] = wy;
+    }
+  }
+  // lds[row * ld + d]
+  __device__ __forceinline__ void store_rows(int tid, bf16* lds, int ld) const {
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int c = tid + NT * r;
+      if (c < N) {
+        const int p = c / CPR, cc = c % CPR;
+        *reinterpret_cast<u32x4*>(lds + (2 * p) * ld + 8 * cc) = x[r];
+        *reinterpret_cast<u32x4*>(lds + (2 * p + 1) * ld + 8 * cc) = y[r];
+      }
+    }
+  }
+  // lds[d * ld + row]; ld must be even
+  __device__ __forceinline__ void store_cols(int tid, bf16* lds, int ld) const {
+#pragma unroll
+    for (int r = 0; r < PER; ++r) {
+      const int c = tid + NT * r;
+      if (c < N) {
+        const int p = c / CPR, cc = c % CPR;
+        uint32_t* dst = reinterpret_cast<uint32_t*>(lds + (8 * cc) * ld + 2 * p);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          dst[(2 * e) * (ld / 2)] = (x[r][e] & 0xffffu) | (y[r][e] << 16);
+          dst[(2 * e + 1) * (ld / 2)] = (x[r][e] >> 16) | (y[r][e] & 0xffff0000u);
+        }
+      }
+    }
+  }
+};
+
+// MFMA operand whose k order follows an accumulator's row order, read from a
+// transposed LDS tile t[row * ld + k]: k = {16s + 4h + [0,4), 16s + 8 + 4h + [0,4)}.
+__device__ __forceinline__ bf16x8 lds_kperm_operand(const bf16* t, int ld, int row, int s, int half) {
+  const bf16* p = t + row * ld + 16 * s + 4 * half;
+  const u32x2 lo = *reinterpret_cast<const u32x2*>(p);
+  const u32x2 hi = *reinterpret_cast<const u32x2*>(p + 8);
+  const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
+  return as_bf16x8(v);
+}
+
+// Registers 8(s%2)..8(s%2)+7 of accumulator block acc as a bf16 MFMA operand.
+__device__ __forceinline__ bf16x8 acc_kperm_operand(const f32x16& acc, int s) {
+  const int base = 8 * (s & 1);
+  u32x4 w;
+  w[0] = pack_bf16x2(acc[base + 0], acc[base + 1]);
+  w[1] = pack_bf16x2(acc[base + 2], acc[base + 3]);
+  w[2] = pack_bf16x2(acc[base + 4], acc[base + 5]);
+  w[3] = pack_bf16x2(acc[base + 6], acc[base + 7]);
+  return as_bf16x8(w);
+}
+
+// Row of a row-major LDS tile as the MFMA operand for k-step s (k = d).
+__device__ __forceinline__ bf16x8 lds_row_operand(const bf16* t, int ld, int row, int s, int half) {
+  return as_bf16x8(*reinterpret_cast<const u32x4*>(t + row * ld + 16 * s + 8 * half));
+}
+
+// Store an accumulator holding X^T (rows d, column = this lane's row) as
+// bf16 row x[d] scaled by `scale`: 4 consecutive d per 8-byte store.
+template <int DB>
+__device__ __forceinline__ void store_acc_row(bf16* row, const f32x16 (&acc)[DB], float scale, int half) {
+#pragma unroll
+  for (int d = 0; d < DB; ++d) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      u32x2 w;
+      w[0] = pack_bf16x2(acc[d][4 * g + 0] * scale, acc[d][4 * g + 1] * scale);
+      w[1] = pack_bf16x2(acc[d][4 * g + 2] * scale, acc[d][4 * g + 3] * scale);
+      store8(row + d * 32 + 8 * g + 4 * half, w);
+    }
+  }
+}
+
+}  // namespace wmx

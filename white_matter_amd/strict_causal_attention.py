@@ -1,0 +1,582 @@
+"""Strict-past attention for Jacobi passes, cached prefill and KV-pool decode.
+
+Drop-in for ``white_matter.ops.strict_causal_attention``
+(src/white_matter/ops/strict_causal_attention.py:36-474): same names,
+signatures, validation messages, masking contract and output layout
+(Q/K/V in (B, H, T, D), output (B, T, H, D)). On ROCm devices every
+non-"reference" backend literal runs the gfx950 HIP kernels of
+libwmx_attn.so:
+
+  * packed documents (``metadata``)      -> varlen kernels, gather on load
+  * int/tensor ``query_start``, ragged ``kv_lengths`` or single-query training
+                                          -> dense kernels with per-row bounds
+  * one query token without gradient      -> split-K decode kernel
+
+``backend="reference"`` (and "auto" on CPU) is the reference's portable
+PyTorch math path.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Literal
+
+import torch
+
+from . import _kernels, portable
+
+_BACKENDS = ("auto", "reference", "torch_flash", "flash_attention_2")
+
+
+@dataclass(frozen=True)
+class StrictCausalMetadata:
+    """Reusable varlen gather/scatter schedule, independent of heads and values
+    (reference strict_causal_attention.py:36-72).
+
+    Segment s holds queries ``query_indices[cu_queries[s]:cu_queries[s+1]]``
+    (flat row * query_length + t) and keys ``key_indices[cu_keys[s]:cu_keys[s+1]]``
+    (flat row * key_extent + slot); its local key j is visible to its local
+    query i iff j <= (keys - queries) + i.
+    """
+
+    query_indices: torch.Tensor
+    key_indices: torch.Tensor
+    cu_queries: torch.Tensor
+    cu_keys: torch.Tensor
+    max_queries: int
+    max_keys: int
+    key_extent: int
+    segments: tuple[tuple[int, int, int, int], ...] = ()
+
+    def __post_init__(self) -> None:
+        if not self.segments and self.cu_queries.numel() > 1:
+            q = self.cu_queries.tolist()
+            k = self.cu_keys.tolist()
+            object.__setattr__(self, "segments", tuple((q[s], q[s + 1], k[s], k[s + 1]) for s in range(len(q) - 1)))
+
+    def with_key_extent(self, key_extent: int) -> StrictCausalMetadata:
+        """Address the same key slots in storage rows of width ``key_extent``."""
+        if key_extent == self.key_extent:
+            return self
+        row, slot = torch.div(self.key_indices, self.key_extent, rounding_mode="floor"), self.key_indices % self.key_extent
+        remapped = StrictCausalMetadata(
+            self.query_indices,
+            row * key_extent + slot,
+            self.cu_queries,
+            self.cu_keys,
+            self.max_queries,
+            self.max_keys,
+            key_extent,
+            self.segments,
+        )
+        facts = getattr(self, "_facts", None)
+        if facts is not None:
+            object.__setattr__(remapped, "_facts", facts)
+        return remapped
+
+
+@torch.compiler.disable
+def prepare_strict_causal_metadata(
+    document_ids: torch.Tensor,
+    query_length: int,
+    *,
+    query_start: int | torch.Tensor = 0,
+    kv_lengths: torch.Tensor | None = None,
+    use_dummy_token: bool = False,
+) -> StrictCausalMetadata:
+    """Pack document runs into varlen segments; negative ids are padding
+    (reference strict_causal_attention.py:75-155).
+
+    ``document_ids`` (B, extent) labels real key slots, the current query
+    tokens included and the optional leading dummy excluded; query i of row b
+    sits at slot query_start[b] + i. A run is a maximal sequence of present
+    (id >= 0) slots with one id, padding slots in between not breaking it.
+    Query at slot p sees the present slots of its run before min(p, kv_len),
+    plus the dummy. Consecutive valid queries share a segment while they stay
+    in one run and each sees exactly one more key than the previous one; a
+    segment's keys are the visible set of its last query, dummy first.
+    """
+    batch, extent = document_ids.shape
+    device = document_ids.device
+    offset = int(use_dummy_token)
+    start = torch.as_tensor(query_start, device=device, dtype=torch.long).expand(batch)
+    position = start[:, None] + torch.arange(query_length, device=device)
+    if bool(((position < 0) | (position >= extent)).any()):
+        raise ValueError("document_ids must label every query position")
+
+    present = document_ids >= 0
+    # rank[b, s]: present slots before s (width extent + 1 so rank[:, extent] is the row total)
+    rank = torch.zeros(batch, extent + 1, device=device, dtype=torch.long)
+    rank[:, 1:] = present.cumsum(1)
+    slot = torch.arange(extent, device=device).expand(batch, extent)
+    last_present = torch.where(present, slot, -1).cummax(1).values
+    before = torch.full_like(last_present, -1)
+    before[:, 1:] = last_present[:, :-1]
+    run_begins = present & ((before < 0) | (document_ids != document_ids.gather(1, before.clamp_min(0))))
+    # rank of the first slot of the run that holds (or last precedes) each slot
+    run_rank = torch.where(run_begins, rank[:, :-1], 0).cummax(1).values
+
+    first = run_rank.gather(1, position)
+    reach = position if kv_lengths is None else torch.minimum(position, kv_lengths[:, None])
+    visible_end = rank.gather(1, reach.clamp(0, extent))
+    valid = (document_ids.gather(1, position) >= 0) & ((visible_end > first) | use_dummy_token)
+    query_indices = valid.flatten().nonzero().flatten()
+
+    # segment breaks: another row, another run, or a visible end that is not previous + 1
+    q_row = torch.div(query_indices, max(query_length, 1), rounding_mode="floor")
+    q_first = first.flatten()[query_indices]
+    q_end = visible_end.flatten()[query_indices]
+    breaks = torch.ones_like(query_indices, dtype=torch.bool)
+    breaks[1:] = (q_row[1:] != q_row[:-1]) | (q_first[1:] != q_first[:-1]) | (q_end[1:] != q_end[:-1] + 1)
+    seg_start = breaks.nonzero().flatten()
+    cu_queries = torch.cat((seg_start, seg_start.new_full((1,), query_indices.numel())))
+    key_extent = extent + offset
+    if query_indices.numel() == 0:
+        return StrictCausalMetadata(
+            query_indices, query_indices, cu_queries.int(), cu_queries.int(), query_length, key_extent, key_extent
+        )
+
+    last = cu_queries[1:] - 1
+    seg_row = q_row[last]
+    seg_first = q_first[last]
+    seg_keys = (q_end[last] - seg_first).clamp_min(0) + offset
+    cu_keys = torch.zeros(seg_keys.numel() + 1, device=device, dtype=torch.long)
+    cu_keys[1:] = seg_keys.cumsum(0)
+    owner = torch.repeat_interleave(torch.arange(seg_keys.numel(), device=device), seg_keys)
+    local = torch.arange(owner.numel(), device=device) - cu_keys[owner]
+    # slot of the r-th present slot of a row: index into the row-major list of present slots
+    present_slots = present.flatten().nonzero().flatten() % max(extent, 1)
+    row_base = rank[:, extent].cumsum(0) - rank[:, extent]
+    pick = (row_base[seg_row[owner]] + seg_first[owner] + local - offset).clamp_min(0)
+    key_slot = present_slots[pick] + offset
+    if use_dummy_token:
+        key_slot = torch.where(local == 0, 0, key_slot)
+    key_indices = seg_row[owner] * key_extent + key_slot
+    metadata = StrictCausalMetadata(
+        query_indices, key_indices, cu_queries.int(), cu_keys.int(), query_length, key_extent, key_extent
+    )
+    for tensor in (metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys):
+        torch._dynamo.mark_dynamic(tensor, 0)
+    return metadata
+
+
+# ---------------------------------------------------------------- schedules --
+def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int, int]:
+    """Host facts the kernels need, computed once per metadata object and kept
+    on it: largest segment (queries, keys), whether key rows repeat across
+    segments, and the largest query and key index (for bounds checks)."""
+    facts = getattr(metadata, "_facts", None)
+    if facts is None:
+        segments = metadata.segments
+        max_q = max((qe - qs for qs, qe, _, _ in segments), default=0)
+        max_k = max((ke - ks for _, _, ks, ke in segments), default=0)
+        qi, ki = metadata.query_indices, metadata.key_indices
+        if segments and (segments[-1][1] != qi.numel() or segments[-1][3] != ki.numel()):
+            raise ValueError("metadata segments do not cover query_indices/key_indices")
+        n = ki.numel()
+        unique = n == 0 or int(torch.unique(ki).numel()) == n
+        top_q = int(qi.max()) if qi.numel() else -1
+        top_k = int(ki.max()) if n else -1
+        if (qi.numel() and int(qi.min()) < 0) or (n and int(ki.min()) < 0):
+            raise ValueError("metadata indices must be nonnegative")
+        facts = (max_q, max_k, unique, top_q, top_k)
+        object.__setattr__(metadata, "_facts", facts)
+    return facts
+
+
+# ------------------------------------------------------------ custom ops ----
+def _dense_visibility(
+    query_offset: int, row_offset: torch.Tensor | None, row_limit: torch.Tensor | None, key_mask, keep_slot0: bool
+) -> _kernels.Visibility:
+    return _kernels.Visibility(
+        query_stride=1,
+        query_offset=query_offset,
+        row_offset=row_offset,
+        row_limit=row_limit,
+        keep_slot0=keep_slot0,
+        key_mask=None if key_mask is None else key_mask.contiguous().view(torch.uint8),
+    )
+
+
+@torch.library.custom_op("white_matter::strict_dense_fwd", mutates_args=())
+def strict_dense_fwd(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    query_offset: int,
+    row_offset: torch.Tensor | None,
+    row_limit: torch.Tensor | None,
+    key_mask: torch.Tensor | None,
+    keep_slot0: bool,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Strict-causal attention with per-row bounds; output (B, T, H, D) bf16.
+
+    Key slot j is visible to query i of row b iff j <= min(offset_b + i, limit_b),
+    or j == 0 with keep_slot0, and key_mask[b, j] when given.
+    """
+    q, k, v = (_kernels.operand(t) for t in (query, key, value))
+    batch, heads, length, dim = q.shape
+    out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
+    lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
+    vis = _dense_visibility(query_offset, row_offset, row_limit, key_mask, keep_slot0)
+    _kernels.forward(q, k, v, out.transpose(1, 2), lse, scale, vis)
+    return out, lse
+
+
+@strict_dense_fwd.register_fake
+def _(query, key, value, query_offset, row_offset, row_limit, key_mask, keep_slot0, scale):
+    batch, heads, length, dim = query.shape
+    return (
+        query.new_empty(batch, length, heads, dim, dtype=torch.bfloat16),
+        query.new_empty(batch, heads, length, dtype=torch.float32),
+    )
+
+
+@torch.library.custom_op("white_matter::strict_dense_bwd", mutates_args=())
+def strict_dense_bwd(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    dout: torch.Tensor,
+    query_offset: int,
+    row_offset: torch.Tensor | None,
+    row_limit: torch.Tensor | None,
+    key_mask: torch.Tensor | None,
+    keep_slot0: bool,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    q, k, v = (_kernels.operand(t) for t in (query, key, value))
+    o = _kernels.operand(out.transpose(1, 2))
+    g = _kernels.operand(dout.transpose(1, 2))
+    dq = torch.empty(q.shape, device=q.device, dtype=torch.bfloat16)
+    dk = torch.empty(k.shape, device=q.device, dtype=torch.bfloat16)
+    dv = torch.empty(v.shape, device=q.device, dtype=torch.bfloat16)
+    vis = _dense_visibility(query_offset, row_offset, row_limit, key_mask, keep_slot0)
+    _kernels.backward(q, k, v, o, lse, g, dq, dk, dv, scale, vis)
+    return dq, dk, dv
+
+
+@strict_dense_bwd.register_fake
+def _(query, key, value, out, lse, dout, *args):
+    return (
+        query.new_empty(query.shape, dtype=torch.bfloat16),
+        key.new_empty(key.shape, dtype=torch.bfloat16),
+        value.new_empty(value.shape, dtype=torch.bfloat16),
+    )
+
+
+def _dense_setup(ctx, inputs, output):
+    query, key, value, ctx.query_offset, row_offset, row_limit, key_mask, ctx.keep_slot0, ctx.scale = inputs
+    ctx.has = (row_offset is not None, row_limit is not None, key_mask is not None)
+    extras = [t for t in (row_offset, row_limit, key_mask) if t is not None]
+    ctx.dtypes = (query.dtype, key.dtype, value.dtype)
+    ctx.save_for_backward(query, key, value, *output, *extras)
+
+
+def _dense_backward(ctx, dout, dlse):
+    query, key, value, out, lse, *extras = ctx.saved_tensors
+    it = iter(extras)
+    row_offset, row_limit, key_mask = (next(it) if flag else None for flag in ctx.has)
+    dq, dk, dv = strict_dense_bwd(
+        query, key, value, out, lse, dout, ctx.query_offset, row_offset, row_limit, key_mask, ctx.keep_slot0, ctx.scale
+    )
+    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2]), None, None, None, None, None, None)
+
+
+strict_dense_fwd.register_autograd(_dense_backward, setup_context=_dense_setup)
+
+
+def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, max_k, keys_unique):
+    return _kernels.Varlen(
+        query_indices=query_indices.contiguous(),
+        key_indices=key_indices.contiguous(),
+        cu_queries=cu_queries.to(torch.int32).contiguous(),
+        cu_keys=cu_keys.to(torch.int32).contiguous(),
+        num_segments=cu_queries.numel() - 1,
+        max_queries=max_q,
+        max_keys=max_k,
+        query_extent=query.shape[2],
+        key_extent=key.shape[2],
+        keys_unique=keys_unique,
+    )
+
+
+@torch.library.custom_op("white_matter::strict_varlen_fwd", mutates_args=())
+def strict_varlen_fwd(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    query_indices: torch.Tensor,
+    key_indices: torch.Tensor,
+    cu_queries: torch.Tensor,
+    cu_keys: torch.Tensor,
+    max_queries: int,
+    max_keys: int,
+    keys_unique: bool,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Packed-segment attention read straight from (B, H, T, D) storage;
+    output (B, T, H, D) with zeros for queries outside every segment."""
+    q, k, v = (_kernels.operand(t) for t in (query, key, value))
+    batch, heads, length, dim = q.shape
+    out = torch.zeros(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
+    lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
+    vis = _kernels.Visibility(
+        varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, keys_unique)
+    )
+    _kernels.forward(q, k, v, out.transpose(1, 2), lse, scale, vis)
+    return out, lse
+
+
+@strict_varlen_fwd.register_fake
+def _(query, key, value, *args):
+    batch, heads, length, dim = query.shape
+    return (
+        query.new_empty(batch, length, heads, dim, dtype=torch.bfloat16),
+        query.new_empty(batch, heads, length, dtype=torch.float32),
+    )
+
+
+@torch.library.custom_op("white_matter::strict_varlen_bwd", mutates_args=())
+def strict_varlen_bwd(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    dout: torch.Tensor,
+    query_indices: torch.Tensor,
+    key_indices: torch.Tensor,
+    cu_queries: torch.Tensor,
+    cu_keys: torch.Tensor,
+    max_queries: int,
+    max_keys: int,
+    keys_unique: bool,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    q, k, v = (_kernels.operand(t) for t in (query, key, value))
+    o = _kernels.operand(out.transpose(1, 2))
+    g = _kernels.operand(dout.transpose(1, 2))
+    dq = torch.zeros(q.shape, device=q.device, dtype=torch.bfloat16)
+    dk = torch.zeros(k.shape, device=q.device, dtype=torch.bfloat16)
+    dv = torch.zeros(v.shape, device=q.device, dtype=torch.bfloat16)
+    vis = _kernels.Visibility(
+        varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, keys_unique)
+    )
+    _kernels.backward(q, k, v, o, lse, g, dq, dk, dv, scale, vis)
+    return dq, dk, dv
+
+
+@strict_varlen_bwd.register_fake
+def _(query, key, value, *args):
+    return (
+        query.new_empty(query.shape, dtype=torch.bfloat16),
+        key.new_empty(key.shape, dtype=torch.bfloat16),
+        value.new_empty(value.shape, dtype=torch.bfloat16),
+    )
+
+
+def _varlen_setup(ctx, inputs, output):
+    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.unique, ctx.scale = inputs
+    ctx.dtypes = (query.dtype, key.dtype, value.dtype)
+    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck)
+
+
+def _varlen_backward(ctx, dout, dlse):
+    query, key, value, out, lse, qi, ki, cq, ck = ctx.saved_tensors
+    dq, dk, dv = strict_varlen_bwd(
+        query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.unique, ctx.scale
+    )
+    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 8
+
+
+strict_varlen_fwd.register_autograd(_varlen_backward, setup_context=_varlen_setup)
+
+
+@torch.library.custom_op("white_matter::strict_decode", mutates_args=())
+def strict_decode(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    query_start: torch.Tensor | None,
+    query_start_value: int,
+    kv_lengths: torch.Tensor | None,
+    key_mask: torch.Tensor | None,
+    use_dummy: bool,
+    scale: float,
+    num_splits: int,
+) -> torch.Tensor:
+    """One query token per row over the KV pool; output (B, 1, H, D) bf16."""
+    q, k, v = (_kernels.operand(t) for t in (query, key, value))
+    batch, heads, _, dim = q.shape
+    out = torch.empty(batch, 1, heads, dim, device=q.device, dtype=torch.bfloat16)
+    _kernels.decode(
+        q,
+        k,
+        v,
+        out[:, 0],
+        query_start=query_start_value if query_start is None else query_start,
+        kv_lengths=kv_lengths,
+        key_mask=None if key_mask is None else key_mask.contiguous().view(torch.uint8),
+        use_dummy=use_dummy,
+        scale=scale,
+        num_splits=num_splits,
+    )
+    return out
+
+
+@strict_decode.register_fake
+def _(query, *args):
+    batch, heads, _, dim = query.shape
+    return query.new_empty(batch, 1, heads, dim, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("white_matter::flash_attention_decode", mutates_args=())
+def flash_attention_decode(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    lengths: torch.Tensor,
+    scale: float,
+    causal: bool,
+    num_splits: int = 0,
+) -> torch.Tensor:
+    """The reference's decode op (flash_attention.py:15-36) on the HIP kernel:
+    query (B, 1, H, D), key/value caches (B, N, Hkv, D), ``lengths`` visible
+    slots per row. A single query sees every visible slot, so ``causal`` does
+    not change the result."""
+    q = _kernels.operand(query.transpose(1, 2))
+    k = _kernels.operand(key.transpose(1, 2))
+    v = _kernels.operand(value.transpose(1, 2))
+    batch, heads, _, dim = q.shape
+    out = torch.empty(batch, 1, heads, dim, device=q.device, dtype=torch.bfloat16)
+    _kernels.decode(
+        q, k, v, out[:, 0], query_start=lengths, kv_lengths=None, key_mask=None,
+        use_dummy=False, scale=scale, num_splits=num_splits,
+    )
+    return out.to(query.dtype)
+
+
+@flash_attention_decode.register_fake
+def _(query, key, value, lengths, scale, causal, num_splits=0):
+    return query.new_empty(query.shape)
+
+
+# ------------------------------------------------------------ public API ----
+def _zeros_linked(query, key, value, batch, length, heads, dim):
+    zero = (query[..., :0, :].sum() + key[..., :0, :].sum() + value[..., :0, :].sum()).to(query.dtype)
+    return query.new_zeros(batch, length, heads, dim) + zero
+
+
+def _unsupported(dim: int) -> RuntimeError:
+    return RuntimeError(f"the gfx950 attention kernels: this path does not support head_dim {dim} (maximum 128)")
+
+
+def _hip_attention(query, key, value, query_start, kv_lengths, use_dummy_token, metadata, key_mask, scale, num_splits):
+    batch, heads, length, dim = query.shape
+    padded = _kernels.kernel_head_dim(dim)
+    if padded is None:
+        raise _unsupported(dim)
+    dtype = query.dtype
+    q, k, v = (_kernels.pad_head_dim(t, padded) for t in (query, key, value))
+    offset = int(use_dummy_token)
+    differentiable = torch.is_grad_enabled() and any(t.requires_grad for t in (query, key, value))
+    if metadata is None and length == 1 and not differentiable:
+        tensor_start = query_start if isinstance(query_start, torch.Tensor) else None
+        out = strict_decode(
+            q, k, v, tensor_start, 0 if tensor_start is not None else int(query_start), kv_lengths,
+            key_mask, use_dummy_token, scale, num_splits,
+        )
+    elif metadata is not None:
+        if metadata.query_indices.numel() == 0:
+            return _zeros_linked(query, key, value, batch, length, heads, dim)
+        max_q, max_k, unique, top_q, top_k = _schedule_facts(metadata)
+        if metadata.max_queries != length or top_q >= batch * length or top_k >= batch * key.shape[2]:
+            raise ValueError("metadata was prepared for other query/key shapes")
+        out, _ = strict_varlen_fwd(
+            q, k, v, metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
+            max_q, max_k, unique, scale,
+        )
+    else:
+        row_offset = row_limit = None
+        if isinstance(query_start, torch.Tensor):
+            row_offset = (query_start.to(query.device).expand(batch) + (offset - 1)).to(torch.int32)
+            query_offset = 0
+        else:
+            query_offset = int(query_start) + offset - 1
+        if kv_lengths is not None:
+            row_limit = (kv_lengths.to(query.device) + (offset - 1)).to(torch.int32)
+        out, _ = strict_dense_fwd(q, k, v, query_offset, row_offset, row_limit, key_mask, use_dummy_token, scale)
+    return out[..., :dim].to(dtype)
+
+
+def strict_causal_attention(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    *,
+    query_start: int | torch.Tensor = 0,
+    kv_lengths: torch.Tensor | None = None,
+    use_dummy_token: bool = False,
+    metadata: StrictCausalMetadata | None = None,
+    key_mask: torch.Tensor | None = None,
+    softmax_scale: float | None = None,
+    backend: Literal["auto", "reference", "torch_flash", "flash_attention_2"] = "auto",
+    num_splits: int = 0,
+    static_cache: bool = False,
+) -> torch.Tensor:
+    """Attend only to earlier real tokens, plus an optional leading dummy
+    (reference strict_causal_attention.py:158-322).
+
+    Q/K/V use (B,H,T,D); output uses (B,T,H,D). query_start and kv_lengths
+    count real tokens, excluding the dummy slot. K/V may hold current tokens
+    or unused cache capacity (even NaN); neither is read outside the
+    strict-past bound. Inputs are never mutated. Rows with nothing visible
+    return zero. key_mask is boolean (B,N). On ROCm devices "auto",
+    "torch_flash" and "flash_attention_2" run the HIP kernels; num_splits sets
+    the decode split count; static_cache is accepted for compatibility.
+    """
+    if backend not in _BACKENDS:
+        raise ValueError(f"unsupported strict causal backend: {backend!r}")
+    if type(use_dummy_token) is not bool:
+        raise ValueError("use_dummy_token must be boolean")
+    if any(t.ndim != 4 for t in (query, key, value)) or key.shape != value.shape:
+        raise ValueError("Q/K/V require (B,H,T,D) tensors with matching K/V")
+    batch, heads, length, dim = query.shape
+    if key.shape[0] != batch or key.shape[-1] != dim or heads % key.shape[1]:
+        raise ValueError("Q/K/V require matching batch/head_dim and divisible heads")
+    if any(t.device != query.device for t in (key, value)):
+        raise ValueError("Q/K/V must share a device")
+    offset = int(use_dummy_token)
+    if key.shape[-2] - offset < 0:
+        raise ValueError("dummy-enabled K/V must contain the leading dummy slot")
+    if kv_lengths is not None and (kv_lengths.shape != (batch,) or kv_lengths.dtype not in (torch.int32, torch.int64)):
+        raise ValueError("kv_lengths must be integer (B,)")
+    if isinstance(query_start, torch.Tensor) and (
+        query_start.shape != (batch,) or query_start.dtype not in (torch.int32, torch.int64)
+    ):
+        raise ValueError("query_start must be an integer or integer (B,) tensor")
+    if metadata is not None and key_mask is not None:
+        raise ValueError("metadata and key_mask are mutually exclusive")
+    if key_mask is not None and (key_mask.shape != (batch, key.shape[-2]) or key_mask.dtype != torch.bool):
+        raise ValueError("key_mask must be boolean (B,N)")
+    if metadata is not None:
+        metadata = metadata.with_key_extent(key.shape[-2])
+    scale = dim**-0.5 if softmax_scale is None else softmax_scale
+    if not length or not key.shape[-2]:
+        return _zeros_linked(query, key, value, batch, length, heads, dim)
+    if backend == "auto":
+        backend = "hip" if query.is_cuda else "reference"
+    if backend == "reference":
+        return portable.strict_causal_attention_portable(
+            query, key, value, query_start=query_start, kv_lengths=kv_lengths, use_dummy_token=use_dummy_token,
+            metadata=metadata, key_mask=key_mask, scale=scale,
+        )
+    if not query.is_cuda:
+        raise ValueError("FlashAttention requires CUDA")
+    if key_mask is not None and length != 1:
+        raise ValueError("FlashAttention key_mask requires a single query; use document metadata for prefill")
+    return _hip_attention(query, key, value, query_start, kv_lengths, use_dummy_token, metadata, key_mask, scale, num_splits)

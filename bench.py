@@ -1,0 +1,356 @@
+"""Benchmark of WhiteMatter's attention hot path on one MI355X.
+
+Headline ("C2"): bf16 strict_causal_attention in
+Jacobi mode, Q/K/V (8, 16, 2048, 128) ~ N(0,1)/sqrt(D), use_dummy_token=False,
+packed documents per row with geometric lengths (mean 512, clipped to
+[16, 2048], filled to exactly T), metadata from prepare_strict_causal_metadata,
+forward + backward of sum(output). One step = one forward and one backward
+of the attention operator on resident inputs; the metadata is prepared once
+outside the timed region (the reference builds it once per model forward).
+
+value = 14 * D * Hq * P / step time, P = visible (query, key) pairs counted
+exactly from the metadata (the reference's FLOP convention,
+benchmarks/_flop_counter.py:33-34). Per-kernel averages come from HIP events
+on the launch stream; the dominant kernel gives the roofline object.
+Secondary fields: C4 KV-pool decode GB/s and C3 cyclic fwd+bwd TFLOP/s.
+The CPU baseline times the oracle (float32, dense mask) on a bounded sample.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import sys
+import time
+
+import numpy as np
+import torch
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
+PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+METRIC = "attn fwd+bwd TFLOP/s (bf16, T=2048) and % MFMA peak; decode GB/s"
+
+
+def geometric_documents(batch: int, length: int, seed: int, mean: int = 512, lo: int = 16, hi: int = 2048):
+    """Per-row document ids: lengths ~ Geometric(1/mean) clipped to [lo, hi],
+    appended until the row holds `length` tokens; the last is truncated to
+    fill exactly, and a remainder below `lo` is merged into the previous one."""
+    rng = np.random.default_rng(seed)
+    rows = []
+    for _ in range(batch):
+        sizes = []
+        while sum(sizes) < length:
+            sizes.append(int(np.clip(rng.geometric(1.0 / mean), lo, hi)))
+        sizes[-1] -= sum(sizes) - length
+        if sizes[-1] < lo and len(sizes) > 1:
+            sizes[-2] += sizes.pop()
+        rows.append(np.repeat(np.arange(len(sizes)), sizes))
+    return torch.from_numpy(np.stack(rows)).long()
+
+
+def visible_pairs(metadata) -> int:
+    """Visible (query, key) pairs of a varlen schedule: segment s with nq queries
+    and nk keys is bottom-right causal, so query i sees nk - nq + i + 1 keys."""
+    total = 0
+    for qs, qe, ks, ke in metadata.segments:
+        nq, nk = qe - qs, ke - ks
+        total += nq * (nk - nq) + nq * (nq + 1) // 2
+    return total
+
+
+class Timer:
+    """HIP-event timing on the current stream."""
+
+    def __init__(self):
+        self.start = torch.cuda.Event(enable_timing=True)
+        self.stop = torch.cuda.Event(enable_timing=True)
+
+    def __call__(self, fn, reps: int) -> float:
+        torch.cuda.synchronize()
+        self.start.record()
+        for _ in range(reps):
+            fn()
+        self.stop.record()
+        torch.cuda.synchronize()
+        return self.start.elapsed_time(self.stop) / reps
+
+
+def strict_jacobi_setup(device, seed=0, batch=8, heads=16, length=2048, dim=128):
+    from white_matter_amd import prepare_strict_causal_metadata
+
+    gen = torch.Generator().manual_seed(seed)
+    scale = dim**-0.5
+    q, k, v = (
+        (torch.randn(batch, heads, length, dim, generator=gen) * scale).to(device, torch.bfloat16)
+        for _ in range(3)
+    )
+    docs = geometric_documents(batch, length, seed).to(device)
+    t0 = time.perf_counter()
+    metadata = prepare_strict_causal_metadata(docs, length)
+    meta_ms = (time.perf_counter() - t0) * 1e3
+    return q, k, v, docs, metadata, meta_ms
+
+
+def kernel_times(q, k, v, metadata, reps):
+    """Average duration (ms) of each kernel of one forward+backward, launched
+    alone through the C ABI between HIP events on the current stream."""
+    from white_matter_amd import _kernels, _native
+    from white_matter_amd.strict_causal_attention import _schedule_facts
+
+    batch, heads, length, dim = q.shape
+    max_q, max_k, unique, _, _ = _schedule_facts(metadata)
+    varlen = _kernels.Varlen(
+        metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
+        metadata.cu_queries.numel() - 1, max_q, max_k, length, k.shape[2], unique,
+    )
+    vis = _kernels.Visibility(varlen=varlen)
+    out = torch.zeros(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
+    o = out.transpose(1, 2)
+    lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
+    dout = torch.ones_like(o)
+    dq, dk, dv = (torch.zeros_like(t) for t in (q, k, v))
+    delta = torch.empty_like(lse)
+    args = _kernels._base_args(q, k, v, o, lse, dim**-0.5, vis, length)
+    args.dout, args.delta = dout.data_ptr(), delta.data_ptr()
+    args.do_stride = _kernels._strides(dout)
+    args.dq, args.dk, args.dv = dq.data_ptr(), dk.data_ptr(), dv.data_ptr()
+    args.dq_stride, args.dk_stride, args.dv_stride = (_kernels._strides(t) for t in (dq, dk, dv))
+    need = _native.attn_bwd_workspace_size(args)
+    workspace = torch.empty(max(need, 16), device=q.device, dtype=torch.uint8)
+    args.workspace, args.workspace_bytes = workspace.data_ptr(), need
+    dev = q.device
+    timer = Timer()
+    calls = {
+        "attn_fwd": lambda: _native.attn_fwd(args, dev),
+        "bwd_delta": lambda: _native.attn_bwd_preprocess(args, dev),
+        "bwd_dq": lambda: _native.attn_bwd_dq(args, dev),
+        "bwd_dkv": lambda: _native.attn_bwd_dkv(args, dev),
+    }
+    result = {}
+    for name, fn in calls.items():
+        fn()
+        result[name] = timer(fn, reps)
+    del workspace
+    return result
+
+
+def decode_setup(device, seed=1, batch=32, heads=16, kv_heads=16, dim=128, capacity=8192):
+    gen = torch.Generator().manual_seed(seed)
+    q = (torch.randn(batch, heads, 1, dim, generator=gen) * dim**-0.5).to(device, torch.bfloat16)
+    k = torch.empty(batch, kv_heads, capacity, dim, device=device, dtype=torch.bfloat16).normal_(0, dim**-0.5)
+    v = torch.empty_like(k).normal_(0, dim**-0.5)
+    lengths = torch.from_numpy(np.random.default_rng(seed).integers(512, 8192, size=batch, endpoint=True)).to(device)
+    return q, k, v, lengths
+
+
+def cpu_baseline(q, k, v, metadata, budget_s: float):
+    """The oracle (float32 dense-mask softmax, forward + backward) on single rows
+    of the C2 batch, on this host's CPU threads, until `budget_s` has passed."""
+    from oracle import attention as ref
+
+    threads = torch.get_num_threads()
+    batch, heads, length, dim = q.shape
+    qi = metadata.query_indices.cpu().numpy()
+    cq = metadata.cu_queries.cpu().numpy()
+    keep_all = None
+    done_pairs, elapsed, rows = 0, 0.0, 0
+    meta_np = {
+        "query_indices": qi,
+        "key_indices": metadata.key_indices.cpu().numpy(),
+        "cu_queries": cq,
+        "cu_keys": metadata.cu_keys.cpu().numpy(),
+        "key_extent": metadata.key_extent,
+    }
+    keep_all = ref.schedule_keep(meta_np, batch, length, k.shape[2])
+    while elapsed < budget_s and rows < batch:
+        b = rows
+        qb, kb, vb = (t[b : b + 1].float().cpu().requires_grad_() for t in (q, k, v))
+        keep = keep_all[b : b + 1, None]
+        t0 = time.perf_counter()
+        out = ref.masked_attention(qb, kb, vb, keep, dim**-0.5, dtype=torch.float32)
+        out.sum().backward()
+        elapsed += time.perf_counter() - t0
+        done_pairs += int(keep.sum())
+        rows += 1
+    flops = 14 * dim * heads * done_pairs
+    return {
+        "value": flops / elapsed / 1e12,
+        "unit": "TFLOP/s",
+        "cores": threads,
+        "kind": "port",
+        "sample": f"{rows} of {batch} rows of the C2 batch (all {heads} heads, T={length}), fp32, "
+        f"{elapsed:.1f} s; visible-pair FLOPs as the GPU value",
+    }
+
+
+def main(argv=None) -> int:
+    parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    parser.add_argument("--gpus", type=int, default=1)
+    parser.add_argument("--steps", type=int, default=20)
+    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--kernel-reps", type=int, default=20)
+    parser.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    parser.add_argument("--no-cpu-baseline", action="store_true")
+    parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
+    args = parser.parse_args(argv)
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
+        print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
+        return 2
+    if not torch.cuda.is_available():
+        print("bench.py needs a ROCm GPU", file=sys.stderr)
+        return 2
+
+    from white_matter_amd import strict_causal_attention
+
+    device = torch.device("cuda:0")
+    q, k, v, docs, metadata, meta_ms = strict_jacobi_setup(device)
+    batch, heads, length, dim = q.shape
+    pairs = visible_pairs(metadata)
+    dense_pairs = batch * length * (length - 1) // 2
+    flops = 14 * dim * heads * pairs
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+
+    def step():
+        out = strict_causal_attention(*leaves, metadata=metadata)
+        torch.autograd.grad(out, leaves, torch.ones_like(out))
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    timer = Timer()
+    ms = timer(step, args.steps)
+    value = flops / (ms * 1e-3) / 1e12
+
+    kernels = kernel_times(q, k, v, metadata, args.kernel_reps)
+    algorithmic = {  # FLOPs per launch credited to each kernel (10*D bwd = 8*D dkv + 2*D dq)
+        "attn_fwd": 4 * dim * heads * pairs,
+        "bwd_dq": 2 * dim * heads * pairs,
+        "bwd_dkv": 8 * dim * heads * pairs,
+        "bwd_delta": 0,
+    }
+    dominant = max(kernels, key=kernels.get)
+    dom_achieved = algorithmic[dominant] / (kernels[dominant] * 1e-3) / 1e12
+    roofline = {
+        "bound": "mfma",
+        "kernel": dominant,
+        "achieved": round(dom_achieved, 2),
+        "peak": PEAK_BF16_TFLOPS,
+        "unit": "TFLOP/s",
+        "frac": round(dom_achieved / PEAK_BF16_TFLOPS, 4),
+        "traffic": None,
+        "avg_ms": round(kernels[dominant], 4),
+    }
+    line = {
+        "metric": METRIC,
+        "value": round(value, 2),
+        "unit": "TFLOP/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {
+            "workload": "C2 strict_causal_attention Jacobi, packed geometric documents, fwd+bwd",
+            "batch": batch,
+            "heads": heads,
+            "seq_len": length,
+            "head_dim": dim,
+            "documents": int(sum(int(docs[b].max()) + 1 for b in range(batch))),
+            "visible_pairs": pairs,
+            "dense_causal_pairs": dense_pairs,
+            "dense_equivalent_tflops": round(14 * dim * heads * dense_pairs / (ms * 1e-3) / 1e12, 2),
+            "metadata_ms": round(meta_ms, 3),
+        },
+        "roofline": roofline,
+        "kernels": {
+            name: {
+                "avg_ms": round(t, 4),
+                "algorithmic_tflops": round(algorithmic[name] / (t * 1e-3) / 1e12, 2),
+            }
+            for name, t in kernels.items()
+        },
+        "frac_of_peak_step": round(value / PEAK_BF16_TFLOPS, 4),
+    }
+
+    if not args.no_secondary:
+        line["decode"] = decode_line(device)
+        line["cyclic"] = cyclic_line(device)
+
+    if not args.no_cpu_baseline:
+        line["cpu_baseline"] = cpu_baseline(q, k, v, metadata, args.cpu_budget)
+    print(json.dumps(line), flush=True)
+    return 0
+
+
+def decode_line(device):
+    """C4 decode: B=32, H=Hkv=16, D=128, kv lengths ~ U{512..8192}, one token per row."""
+    from white_matter_amd import strict_causal_attention
+
+    q, k, v, lengths = decode_setup(device)
+    batch, kv_heads, capacity, dim = k.shape
+    with torch.no_grad():
+        fn = lambda: strict_causal_attention(q, k, v, query_start=lengths)  # noqa: E731
+        for _ in range(3):
+            fn()
+        ms = Timer()(fn, 50)
+    kv_bytes = int(lengths.sum()) * 2 * kv_heads * dim * 2
+    other = q.numel() * 2 * 2 + batch * 8
+    gbps = (kv_bytes + other) / (ms * 1e-3) / 1e9
+    return {
+        "workload": "C4 decode B=32 H=Hkv=16 D=128 kv_len~U[512,8192]",
+        "ms": round(ms, 4),
+        "gbps": round(gbps, 1),
+        "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
+        "bytes": kv_bytes + other,
+    }
+
+
+def cyclic_line(device, stride=4):
+    """C3: cyclic fwd+bwd over a full pass of `stride` residues, no dummy
+    (strict_past=True), packed documents from prepare_feedback_metadata."""
+    from white_matter_amd import cyclic_attention, prepare_feedback_metadata
+
+    batch, heads, length, dim = 8, 16, 2048, 128
+    gen = torch.Generator().manual_seed(3)
+    docs = geometric_documents(batch, length, 3).to(device)
+    groups = [torch.arange(r, length, stride, device=device) for r in range(stride)]
+    metas = prepare_feedback_metadata(docs, groups, length, use_dummy_token=False)
+    k, v = ((torch.randn(batch, heads, length, dim, generator=gen) * dim**-0.5).to(device, torch.bfloat16) for _ in range(2))
+    qs = [(torch.randn(batch, heads, g.numel(), dim, generator=gen) * dim**-0.5).to(device, torch.bfloat16) for g in groups]
+    kl, vl = k.clone().requires_grad_(), v.clone().requires_grad_()
+    ql = [t.clone().requires_grad_() for t in qs]
+
+    def full_pass():
+        for r in range(stride):
+            out = cyclic_attention(ql[r], kl, vl, query_stride=stride, query_offset=r, strict_past=True,
+                                   metadata=metas[r], backend="tilelang")
+            torch.autograd.grad(out, (ql[r], kl, vl), torch.ones_like(out))
+
+    for _ in range(2):
+        full_pass()
+    ms = Timer()(full_pass, 10)
+    # visible pairs of a full pass: strict document-causal pairs, sum of L(L-1)/2
+    pairs = 0
+    for b in range(batch):
+        _, counts = torch.unique_consecutive(docs[b].cpu(), return_counts=True)
+        pairs += int((counts * (counts - 1) // 2).sum())
+    tflops = 14 * dim * heads * pairs / (ms * 1e-3) / 1e12
+    return {
+        "workload": f"C3 cyclic stride {stride} full pass, strict_past, geometric documents, fwd+bwd",
+        "ms_per_pass": round(ms, 4),
+        "tflops": round(tflops, 2),
+        "frac_mfma": round(tflops / PEAK_BF16_TFLOPS, 4),
+    }
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -176,6 +176,13 @@ int64_t wmx_attn_bwd_workspace_size(const wmx_attn_args* args);
  * which the caller zero-fills. */
 int wmx_attn_bwd(const wmx_attn_args* args, void* stream);
 
+/* The two halves of wmx_attn_bwd, for callers that schedule or time them
+ * separately; both read the delta that wmx_attn_bwd_preprocess wrote.
+ * wmx_attn_bwd_dq writes dq (query-parallel); wmx_attn_bwd_dkv writes dk/dv
+ * (key-parallel). */
+int wmx_attn_bwd_dq(const wmx_attn_args* args, void* stream);
+int wmx_attn_bwd_dkv(const wmx_attn_args* args, void* stream);
+
 /* Workspace bytes wmx_decode needs, and the split count it will use. */
 int64_t wmx_decode_workspace_size(const wmx_decode_args* args);
 int32_t wmx_decode_num_splits(const wmx_decode_args* args);

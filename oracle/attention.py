@@ -15,10 +15,11 @@ import numpy as np
 import torch
 
 
-def masked_attention(q, k, v, keep, scale):
+def masked_attention(q, k, v, keep, scale, dtype=torch.float64):
     """q (B,Hq,Tq,D), k/v (B,Hkv,Tk,D), keep broadcastable to (B,Hq,Tq,Tk).
-    Query head h reads KV head h // (Hq // Hkv). Returns float64 (B,Hq,Tq,D)."""
-    q, k, v = q.double(), k.double(), v.double()
+    Query head h reads KV head h // (Hq // Hkv). Computes and returns `dtype`
+    (float64 for parity checks; float32 is the reference's CPU precision)."""
+    q, k, v = q.to(dtype), k.to(dtype), v.to(dtype)
     group = q.shape[1] // k.shape[1]
     k = k.repeat_interleave(group, dim=1)
     v = v.repeat_interleave(group, dim=1)

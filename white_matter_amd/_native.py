@@ -114,6 +114,8 @@ EXPORTS = (
     "wmx_attn_bwd_preprocess",
     "wmx_attn_bwd_workspace_size",
     "wmx_attn_bwd",
+    "wmx_attn_bwd_dq",
+    "wmx_attn_bwd_dkv",
     "wmx_decode_workspace_size",
     "wmx_decode_num_splits",
     "wmx_decode",
@@ -136,7 +138,7 @@ def load() -> ctypes.CDLL:
     lib.wmx_attn_args_size.restype = ctypes.c_size_t
     lib.wmx_decode_args_size.restype = ctypes.c_size_t
     lib.wmx_last_error.restype = ctypes.c_char_p
-    for name in ("wmx_attn_fwd", "wmx_attn_bwd_preprocess", "wmx_attn_bwd"):
+    for name in ("wmx_attn_fwd", "wmx_attn_bwd_preprocess", "wmx_attn_bwd", "wmx_attn_bwd_dq", "wmx_attn_bwd_dkv"):
         getattr(lib, name).argtypes = [ctypes.POINTER(AttnArgs), _vp]
         getattr(lib, name).restype = ctypes.c_int
     lib.wmx_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnArgs)]
@@ -195,6 +197,16 @@ def attn_bwd_workspace_size(args: AttnArgs) -> int:
 def attn_bwd(args: AttnArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_attn_bwd(ctypes.byref(args), _stream(device)), "wmx_attn_bwd")
+
+
+def attn_bwd_dq(args: AttnArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_attn_bwd_dq(ctypes.byref(args), _stream(device)), "wmx_attn_bwd_dq")
+
+
+def attn_bwd_dkv(args: AttnArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_attn_bwd_dkv(ctypes.byref(args), _stream(device)), "wmx_attn_bwd_dkv")
 
 
 def decode_workspace_size(args: DecodeArgs) -> int:

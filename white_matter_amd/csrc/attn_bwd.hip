@@ -532,46 +532,64 @@ int64_t bwd_workspace_size(const wmx_attn_args& a) {
 }
 
 template <int D, int MODE>
-static int launch_bwd_t(const wmx_attn_args& a, hipStream_t stream) {
-  dim3 gq, gk;
+static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
+  dim3 grid;
   if (MODE == kVarlen) {
     if (a.num_segments <= 0) return WMX_OK;
-    gq = dim3((unsigned)(((a.max_queries + 127) / 128) * (int64_t)a.num_segments), a.q_heads, 1);
-    gk = dim3((unsigned)(((a.max_keys + 127) / 128) * (int64_t)a.num_segments), a.kv_heads, 1);
+    grid = dim3((unsigned)(((a.max_queries + 127) / 128) * (int64_t)a.num_segments), a.q_heads, 1);
   } else {
-    gq = dim3((a.q_len + 127) / 128, a.q_heads, a.batch);
-    gk = dim3((a.kv_len + 127) / 128, a.kv_heads, a.batch);
+    grid = dim3((a.q_len + 127) / 128, a.q_heads, a.batch);
   }
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), gq, dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), grid, dim3(256), 0, stream, a);
+  return WMX_OK;
+}
+
+template <int D, int MODE>
+static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
+  dim3 grid;
+  if (MODE == kVarlen) {
+    if (a.num_segments <= 0) return WMX_OK;
+    grid = dim3((unsigned)(((a.max_keys + 127) / 128) * (int64_t)a.num_segments), a.kv_heads, 1);
+  } else {
+    grid = dim3((a.kv_len + 127) / 128, a.kv_heads, a.batch);
+  }
   if (MODE == kVarlen && !a.keys_unique) {
     const int64_t n = bwd_workspace_size(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,
                        (float*)a.workspace, n);
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true>), gk, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true>), grid, dim3(256), 0, stream, a);
     const int64_t total = n / 2;
     hipLaunchKernelGGL(acc_to_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false>), gk, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false>), grid, dim3(256), 0, stream, a);
   }
   return WMX_OK;
 }
 
 template <int MODE>
-static int launch_bwd_mode(const wmx_attn_args& a, hipStream_t stream) {
+static int launch_part(const wmx_attn_args& a, hipStream_t stream, bool dq) {
   switch (a.head_dim) {
-    case 64: return launch_bwd_t<64, MODE>(a, stream);
-    case 96: return launch_bwd_t<96, MODE>(a, stream);
-    case 128: return launch_bwd_t<128, MODE>(a, stream);
+    case 64: return dq ? launch_dq_t<64, MODE>(a, stream) : launch_dkv_t<64, MODE>(a, stream);
+    case 96: return dq ? launch_dq_t<96, MODE>(a, stream) : launch_dkv_t<96, MODE>(a, stream);
+    case 128: return dq ? launch_dq_t<128, MODE>(a, stream) : launch_dkv_t<128, MODE>(a, stream);
     default: return WMX_E_UNSUPPORTED;
   }
 }
 
+static int launch_bwd_part(const wmx_attn_args& a, hipStream_t stream, bool dq) {
+  if (a.query_indices) return launch_part<kVarlen>(a, stream, dq);
+  if (a.q_seg) return launch_part<kDoc>(a, stream, dq);
+  return launch_part<kDense>(a, stream, dq);
+}
+
+int launch_bwd_dq(const wmx_attn_args& a, hipStream_t stream) { return launch_bwd_part(a, stream, true); }
+int launch_bwd_dkv(const wmx_attn_args& a, hipStream_t stream) { return launch_bwd_part(a, stream, false); }
+
 int launch_bwd(const wmx_attn_args& a, hipStream_t stream) {
   int rc = launch_bwd_preprocess(a, stream);
-  if (rc != WMX_OK) return rc;
-  if (a.query_indices) return launch_bwd_mode<kVarlen>(a, stream);
-  if (a.q_seg) return launch_bwd_mode<kDoc>(a, stream);
-  return launch_bwd_mode<kDense>(a, stream);
+  if (rc == WMX_OK) rc = launch_bwd_dq(a, stream);
+  if (rc == WMX_OK) rc = launch_bwd_dkv(a, stream);
+  return rc;
 }
 
 }  // namespace wmx

@@ -124,6 +124,20 @@ int wmx_attn_bwd(const wmx_attn_args* args, void* stream) {
   return launched(wmx::launch_bwd(*args, (hipStream_t)stream));
 }
 
+int wmx_attn_bwd_dq(const wmx_attn_args* args, void* stream) {
+  int rc = check_common(args, true);
+  if (rc != WMX_OK) return rc;
+  if (args->batch == 0 || args->q_len == 0) return WMX_OK;
+  return launched(wmx::launch_bwd_dq(*args, (hipStream_t)stream));
+}
+
+int wmx_attn_bwd_dkv(const wmx_attn_args* args, void* stream) {
+  int rc = check_common(args, true);
+  if (rc != WMX_OK) return rc;
+  if (args->batch == 0 || args->q_len == 0) return WMX_OK;
+  return launched(wmx::launch_bwd_dkv(*args, (hipStream_t)stream));
+}
+
 int64_t wmx_decode_workspace_size(const wmx_decode_args* args) {
   return args ? wmx::decode_workspace_size(*args) : 0;
 }

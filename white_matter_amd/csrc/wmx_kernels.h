@@ -18,6 +18,8 @@ int launch_fwd(const wmx_attn_args& a, hipStream_t stream);
 int launch_bwd_preprocess(const wmx_attn_args& a, hipStream_t stream);
 int64_t bwd_workspace_size(const wmx_attn_args& a);
 int launch_bwd(const wmx_attn_args& a, hipStream_t stream);
+int launch_bwd_dq(const wmx_attn_args& a, hipStream_t stream);
+int launch_bwd_dkv(const wmx_attn_args& a, hipStream_t stream);
 int64_t decode_workspace_size(const wmx_decode_args& a);
 int decode_num_splits(const wmx_decode_args& a);
 int launch_decode(const wmx_decode_args& a, hipStream_t stream);

@@ -1,0 +1,78 @@
+"""The C-ABI library on the CPU: it loads, exports every function that
+include/wmx_attn.h declares, its argument structs match the ctypes binding,
+and argument checks fail with error codes before anything reaches a GPU."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from white_matter_amd import _native
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "wmx_attn.h"
+
+
+def _declared_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"^\s*(?:int|int32_t|int64_t|size_t|const char\*)\s+(wmx_\w+)\s*\(", text, re.M)))
+
+
+def test_header_declares_the_exported_entry_points():
+    declared = _declared_functions()
+    assert set(declared) == set(_native.EXPORTS)
+
+
+def test_library_loads_and_exports_every_declared_symbol():
+    lib = _native.load()
+    for name in _declared_functions():
+        assert hasattr(lib, name), name
+    assert lib.wmx_abi_version() == _native.ABI_VERSION
+    assert lib.wmx_attn_args_size() == ctypes.sizeof(_native.AttnArgs)
+    assert lib.wmx_decode_args_size() == ctypes.sizeof(_native.DecodeArgs)
+
+
+def test_argument_checks_return_errors_without_launching():
+    lib = _native.load()
+    assert lib.wmx_attn_fwd(None, None) == -1
+    assert b"NULL" in lib.wmx_last_error()
+    args = _native.AttnArgs()
+    args.head_dim = 80
+    assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -2
+    assert b"head_dim" in lib.wmx_last_error()
+    args.head_dim, args.batch, args.q_heads, args.kv_heads, args.query_stride = 128, 1, 3, 2, 1
+    assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -1
+    assert b"kv_heads" in lib.wmx_last_error()
+    args.q_heads = 4
+    args.q = args.k = args.v = args.o = args.lse = 0x1008  # misaligned pointer is rejected before use
+    assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -1
+    assert b"aligned" in lib.wmx_last_error()
+    dec = _native.DecodeArgs()
+    dec.head_dim, dec.batch, dec.q_heads, dec.kv_heads = 128, 1, 6, 2
+    assert lib.wmx_decode(ctypes.byref(dec), None) == -2
+    assert b"{1,2,4,8}" in lib.wmx_last_error()
+
+
+def test_workspace_sizes():
+    lib = _native.load()
+    args = _native.AttnArgs()
+    args.head_dim, args.batch, args.kv_heads, args.key_extent = 128, 2, 4, 100
+    assert lib.wmx_attn_bwd_workspace_size(ctypes.byref(args)) == 0
+    args.query_indices = 0x1000
+    args.keys_unique = 0
+    assert lib.wmx_attn_bwd_workspace_size(ctypes.byref(args)) == 2 * 2 * 100 * 4 * 128 * 4
+    dec = _native.DecodeArgs()
+    dec.batch, dec.q_heads, dec.kv_heads, dec.capacity, dec.head_dim, dec.num_splits = 2, 4, 4, 1000, 64, 3
+    assert lib.wmx_decode_num_splits(ctypes.byref(dec)) == 3
+    assert lib.wmx_decode_workspace_size(ctypes.byref(dec)) == 2 * 4 * 3 * (64 + 2) * 4
+
+
+def test_missing_library_fails_loudly(monkeypatch, tmp_path):
+    monkeypatch.setenv("WMX_ATTN_LIBRARY", str(tmp_path / "absent.so"))
+    _native.load.cache_clear()
+    try:
+        with pytest.raises(RuntimeError, match="not found"):
+            _native.load()
+    finally:
+        monkeypatch.delenv("WMX_ATTN_LIBRARY")
+        _native.load.cache_clear()

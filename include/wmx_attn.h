@@ -118,6 +118,9 @@ typedef struct wmx_attn_args {
   int32_t max_keys;           /* largest segment key count */
   int32_t query_extent;       /* T: row width of flat query indices */
   int32_t key_extent;         /* N: row width of flat key indices */
+  int32_t segment_layout;     /* varlen bit 0: each segment's queries are consecutive
+                                 slots of one row; bit 1: its keys 1.. are consecutive
+                                 slots following key 1 (key 0 may be the dummy) */
   float softmax_scale;
 } wmx_attn_args;
 

@@ -44,6 +44,9 @@ def test_argument_checks_return_errors_without_launching():
     assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -1
     assert b"kv_heads" in lib.wmx_last_error()
     args.q_heads = 4
+    assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -2
+    assert b"softmax_scale" in lib.wmx_last_error()
+    args.softmax_scale = 0.125
     args.q = args.k = args.v = args.o = args.lse = 0x1008  # misaligned pointer is rejected before use
     assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -1
     assert b"aligned" in lib.wmx_last_error()

@@ -70,6 +70,7 @@ class Varlen:
     query_extent: int
     key_extent: int
     keys_unique: bool
+    segment_layout: int = 0  # bit 0 consecutive queries, bit 1 consecutive keys from key 1
 
 
 @dataclass
@@ -108,6 +109,7 @@ class Visibility:
             args.query_extent = s.query_extent
             args.key_extent = s.key_extent
             args.keys_unique = int(s.keys_unique)
+            args.segment_layout = s.segment_layout
 
 
 def _base_args(q, k, v, o, lse, scale: float, vis: Visibility, q_len: int) -> _native.AttnArgs:

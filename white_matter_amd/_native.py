@@ -73,6 +73,7 @@ class AttnArgs(ctypes.Structure):
         ("max_keys", ctypes.c_int32),
         ("query_extent", ctypes.c_int32),
         ("key_extent", ctypes.c_int32),
+        ("segment_layout", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float),
     ]
 

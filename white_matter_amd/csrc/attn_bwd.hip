@@ -19,9 +19,7 @@
 // Varlen schedules whose key rows repeat across segments (the shared dummy
 // slot, capped histories) accumulate dK/dV in fp32 workspace rows with
 // atomics and convert once at the end.
-#include <climits>
-
-#include "wmx_kernels.h"
+#include "attn_tiles.h"
 
 namespace wmx {
 
@@ -54,29 +52,9 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const wmx_attn_args a, i
   if (r < rows && l16 == 0) a.delta[r] = acc;
 }
 
-// ------------------------------------------------------------ visibility --
-// The bound lim(i) = clamp(min(offset + stride * i, limit), -1, nk - 1).
-struct Bound {
-  int64_t offset, limit, stride;
-  int nk;
-  __device__ __forceinline__ int operator()(int i) const {
-    int64_t l = offset + stride * (int64_t)i;
-    l = l < limit ? l : limit;
-    l = l < (int64_t)nk - 1 ? l : (int64_t)nk - 1;
-    return (int)(l < -1 ? -1 : l);
-  }
-  // Smallest query row whose bound reaches key j (nq when none does).
-  __device__ __forceinline__ int first_row(int j, int nq) const {
-    if (j > nk - 1 || limit < j) return nq;
-    const int64_t need = (int64_t)j - offset;
-    int64_t m = need <= 0 ? 0 : (need + stride - 1) / stride;
-    return m < nq ? (int)m : nq;
-  }
-};
-
 // ------------------------------------------------------------------- dQ ----
 template <int D, int MODE>
-__global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const wmx_attn_args a) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args a) {
   constexpr int BM = 128, BN = 64;
   constexpr int KLD = D + 8, TLD = BN + 8;
   constexpr int KS = D / 16, DB = D / 32;
@@ -89,66 +67,47 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const wmx_attn_args a)
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int h = blockIdx.y;
-  const int hk = h / (a.q_heads / a.kv_heads);
 
-  int b = 0, nq, nk, q0, qs = 0, ks = 0;
-  Bound bound;
-  if constexpr (MODE == kVarlen) {
-    const int qtiles = (a.max_queries + BM - 1) / BM;
-    const int seg = blockIdx.x / qtiles;
-    const int tile = qtiles - 1 - (int)(blockIdx.x % qtiles);
-    qs = a.cu_queries[seg];
-    nq = a.cu_queries[seg + 1] - qs;
-    ks = a.cu_keys[seg];
-    nk = a.cu_keys[seg + 1] - ks;
-    q0 = tile * BM;
-    if (q0 >= nq) return;
-    bound = Bound{nk - nq, INT_MAX, 1, nk};
-  } else {
-    b = blockIdx.z;
-    nq = a.q_len;
-    nk = a.kv_len;
-    q0 = (gridDim.x - 1 - blockIdx.x) * BM;
-    bound = Bound{a.row_offset ? a.row_offset[b] : a.query_offset, a.row_limit ? a.row_limit[b] : INT_MAX,
-                  a.query_stride, nk};
-  }
+  const int qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
+  const unsigned outer = MODE == kVarlen ? (unsigned)a.num_segments : (unsigned)a.batch;
+  unsigned unit;
+  if (!logical_unit((unsigned)qtiles * outer * a.q_heads, unit)) return;
+  const int q0 = (qtiles - 1 - (int)(unit % qtiles)) * BM;
+  const unsigned rest = unit / qtiles;
+  const int h = MODE == kVarlen ? (int)(rest / outer) : (int)(rest % a.q_heads);
+  const int grp = MODE == kVarlen ? (int)(rest % outer) : (int)(rest / a.q_heads);
+  const int hk = h / (a.q_heads / a.kv_heads);
+  Problem<MODE> pb;
+  pb.init(a, grp);
+  const int b = pb.b, nq = pb.nq, nk = pb.nk;
+  if (q0 >= nq) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
-  const int lim_max_wg = bound(min(q0 + BM, nq) - 1);
+  const int lim_max_wg = pb.bound.lim(min(q0 + BM, nq) - 1);
   const int i = q0 + wave * 32 + col;
   const bool valid_q = i < nq;
-  const int lim_i = bound(i);
+  const int lim_i = pb.bound.lim(i);
   const int wave_first = q0 + wave * 32;
   const bool wave_live = wave_first < nq;
-  const int lim_min_wave = bound(wave_first);
-  const int lim_max_wave = bound(min(wave_first + 31, nq - 1));
+  const int lim_min_wave = pb.bound.lim(wave_first);
+  const int lim_max_wave = pb.bound.lim(min(wave_first + 31, nq - 1));
 
-  int qb = b, qt = i;
-  if constexpr (MODE == kVarlen) {
-    if (valid_q) split_flat(a.query_indices[qs + i], a.query_extent, qb, qt);
-  }
+  int qb, qt;
+  pb.query_loc(valid_q ? i : q0, qb, qt);
   bf16x8 qf[KS], gf[KS];
-  float lse2 = kPosInf, delta = 0.f;
+  float lse2, delta;
   {
-    const bf16* qrow = (const bf16*)a.q + (int64_t)qb * a.q_stride[0] + (int64_t)h * a.q_stride[1] +
-                       (int64_t)qt * a.q_stride[2];
-    const bf16* grow = (const bf16*)a.dout + (int64_t)qb * a.do_stride[0] + (int64_t)h * a.do_stride[1] +
-                       (int64_t)qt * a.do_stride[2];
+    const bf16* qrow = row_at(a.q, a.q_stride, qb, h, qt) + 8 * half;
+    const bf16* grow = row_at(a.dout, a.do_stride, qb, h, qt) + 8 * half;
+    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      u32x4 wq = {0u, 0u, 0u, 0u}, wg = {0u, 0u, 0u, 0u};
-      if (valid_q) {
-        wq = load16(qrow + 16 * s + 8 * half);
-        wg = load16(grow + 16 * s + 8 * half);
-      }
-      qf[s] = as_bf16x8(wq);
-      gf[s] = as_bf16x8(wg);
+      const u32x4 wq = load16(qrow + 16 * s), wg = load16(grow + 16 * s);
+      qf[s] = as_bf16x8(valid_q ? wq : z);
+      gf[s] = as_bf16x8(valid_q ? wg : z);
     }
-    if (valid_q) {
-      const int64_t r = ((int64_t)qb * a.q_heads + h) * a.q_len + qt;
-      lse2 = a.lse[r] * kLog2e;
-      delta = a.delta[r];
-    }
+    const int64_t r = ((int64_t)qb * a.q_heads + h) * a.q_len + qt;
+    lse2 = valid_q ? a.lse[r] * kLog2e : kPosInf;
+    delta = valid_q ? a.delta[r] : 0.f;
   }
 
   int qseg_i = 0, qstart_i = 0, kt_begin_main = 0;
@@ -172,12 +131,12 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const wmx_attn_args a)
   const int ntiles = gap ? 1 + max(0, kt_end - first_main) : kt_end;
   auto tile_of = [&](int it) { return gap ? (it == 0 ? 0 : first_main + it - 1) : it; };
 
-  auto key_ptr = [&](const void* base, const int64_t* st, int j) -> const bf16* {
-    if (j >= nk || !(j <= lim_max_wg || (slot0 && j == 0))) return nullptr;
-    if (MODE == kDense && a.key_mask && !a.key_mask[(int64_t)b * a.key_mask_stride + j]) return nullptr;
-    int kb = b, kt = j;
-    if constexpr (MODE == kVarlen) split_flat(a.key_indices[ks + j], a.key_extent, kb, kt);
-    return (const bf16*)base + (int64_t)kb * st[0] + (int64_t)hk * st[1] + (int64_t)kt * st[2];
+  auto key_ptr = [&](const void* base, const int64_t* st, int j, bool& ok) -> const bf16* {
+    ok = j < nk && (j <= lim_max_wg || (slot0 && j == 0));
+    if (MODE == kDense && a.key_mask) ok = ok && a.key_mask[(int64_t)b * a.key_mask_stride + min(j, nk - 1)] != 0;
+    int kb, kt;
+    pb.key_loc(ok ? j : 0, kb, kt);
+    return row_at(base, st, kb, hk, kt);
   };
 
   PairTile<BN, D> ktile, vtile;
@@ -187,8 +146,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const wmx_attn_args a)
   const float sl2 = a.softmax_scale * kLog2e;
 
   auto load = [&](int n0) {
-    ktile.load(tid, [&](int r) { return key_ptr(a.k, a.k_stride, n0 + r); });
-    vtile.load(tid, [&](int r) { return key_ptr(a.v, a.v_stride, n0 + r); });
+    ktile.load(tid, [&](int r, bool& ok) { return key_ptr(a.k, a.k_stride, n0 + r, ok); });
+    vtile.load(tid, [&](int r, bool& ok) { return key_ptr(a.v, a.v_stride, n0 + r, ok); });
   };
   if (ntiles > 0) load(tile_of(0) * BN);
   for (int it = 0; it < ntiles; ++it) {
@@ -245,7 +204,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const wmx_attn_args a)
             keep = keep && j < nk && ((ksg == qseg_i && j >= qstart_i) || ksg == -1) && (i < kqend_lds[jl]);
           }
         }
-        const float p = keep ? __builtin_amdgcn_exp2f(sacc[nb][r] * sl2 - lse2) : 0.f;
+        const float p = keep ? __builtin_amdgcn_exp2f(fmaf(sacc[nb][r], sl2, -lse2)) : 0.f;
         sacc[nb][r] = p * (pacc[nb][r] - delta);
       }
     }
@@ -257,7 +216,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dq_kernel(const wmx_attn_args a)
     }
   }
   if (!valid_q) return;
-  bf16* dqrow = (bf16*)a.dq + (int64_t)qb * a.dq_stride[0] + (int64_t)h * a.dq_stride[1] + (int64_t)qt * a.dq_stride[2];
+  bf16* dqrow = (bf16*)row_at(a.dq, a.dq_stride, qb, h, qt);
   store_acc_row<DB>(dqrow, dqacc, a.softmax_scale, half);
 }
 
@@ -279,41 +238,29 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int hk = blockIdx.y;
   const int group = a.q_heads / a.kv_heads;
 
-  int b = 0, nq, nk, n0, qs = 0, ks = 0;
-  Bound bound;
-  if constexpr (MODE == kVarlen) {
-    const int ktiles = (a.max_keys + BNK - 1) / BNK;
-    const int seg = blockIdx.x / ktiles;
-    const int tile = (int)(blockIdx.x % ktiles);
-    qs = a.cu_queries[seg];
-    nq = a.cu_queries[seg + 1] - qs;
-    ks = a.cu_keys[seg];
-    nk = a.cu_keys[seg + 1] - ks;
-    n0 = tile * BNK;
-    if (n0 >= nk) return;
-    bound = Bound{nk - nq, INT_MAX, 1, nk};
-  } else {
-    b = blockIdx.z;
-    nq = a.q_len;
-    nk = a.kv_len;
-    n0 = blockIdx.x * BNK;
-    bound = Bound{a.row_offset ? a.row_offset[b] : a.query_offset, a.row_limit ? a.row_limit[b] : INT_MAX,
-                  a.query_stride, nk};
-  }
+  const int ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + BNK - 1) / BNK;
+  const unsigned outer = MODE == kVarlen ? (unsigned)a.num_segments : (unsigned)a.batch;
+  unsigned unit;
+  if (!logical_unit((unsigned)ktiles * outer * a.kv_heads, unit)) return;
+  const int n0 = (int)(unit % ktiles) * BNK;  // low key tiles are read by the most queries
+  const unsigned rest = unit / ktiles;
+  const int hk = MODE == kVarlen ? (int)(rest / outer) : (int)(rest % a.kv_heads);
+  const int grp = MODE == kVarlen ? (int)(rest % outer) : (int)(rest / a.kv_heads);
+  Problem<MODE> pb;
+  pb.init(a, grp);
+  const int b = pb.b, nq = pb.nq, nk = pb.nk;
+  if (n0 >= nk) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
 
   // this lane's key
   const int n = n0 + wave * 32 + col;
   const bool valid_k = n < nk;
-  bool k_masked_out = false;
-  if (MODE == kDense && a.key_mask && valid_k) k_masked_out = !a.key_mask[(int64_t)b * a.key_mask_stride + n];
-  int kb = b, kslot = n;
-  if constexpr (MODE == kVarlen) {
-    if (valid_k) split_flat(a.key_indices[ks + n], a.key_extent, kb, kslot);
-  }
+  bool k_live = valid_k;
+  if (MODE == kDense && a.key_mask) k_live = k_live && a.key_mask[(int64_t)b * a.key_mask_stride + min(n, nk - 1)] != 0;
+  int kb, kslot;
+  pb.key_loc(valid_k ? n : n0, kb, kslot);
   int kseg_n = 0, kqend_n = 0;
   if constexpr (MODE == kDoc) {
     if (valid_k) {
@@ -321,9 +268,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
       kqend_n = a.k_qend[(int64_t)b * a.kv_len + n];
     }
   }
-  // first query row that can see any key of the workgroup / of this wave
-  const int wg_first_key = n0;
-  int m_begin = (slot0 && wg_first_key == 0) ? 0 : bound.first_row(wg_first_key, nq);
+  // query rows that can see any key of the workgroup / of this wave
+  int m_begin = (slot0 && n0 == 0) ? 0 : pb.bound.first_row(n0, nq);
   int m_end = nq;
   if constexpr (MODE == kDoc) {
     int v = valid_k ? kqend_n : 0;
@@ -335,24 +281,18 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   }
   const int wave_key0 = n0 + wave * 32;
   const bool wave_live = wave_key0 < nk;
-  const int wave_m_begin = (slot0 && wave_key0 == 0) ? 0 : bound.first_row(wave_key0, nq);
+  const int wave_m_begin = (slot0 && wave_key0 == 0) ? 0 : pb.bound.first_row(wave_key0, nq);
 
   bf16x8 kf[KS], vf[KS];
   {
-    const bool live = valid_k && !k_masked_out;
-    const bf16* krow = (const bf16*)a.k + (int64_t)kb * a.k_stride[0] + (int64_t)hk * a.k_stride[1] +
-                       (int64_t)kslot * a.k_stride[2];
-    const bf16* vrow = (const bf16*)a.v + (int64_t)kb * a.v_stride[0] + (int64_t)hk * a.v_stride[1] +
-                       (int64_t)kslot * a.v_stride[2];
+    const bf16* krow = row_at(a.k, a.k_stride, kb, hk, kslot) + 8 * half;
+    const bf16* vrow = row_at(a.v, a.v_stride, kb, hk, kslot) + 8 * half;
+    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      u32x4 wk = {0u, 0u, 0u, 0u}, wv = {0u, 0u, 0u, 0u};
-      if (live) {
-        wk = load16(krow + 16 * s + 8 * half);
-        wv = load16(vrow + 16 * s + 8 * half);
-      }
-      kf[s] = as_bf16x8(wk);
-      vf[s] = as_bf16x8(wv);
+      const u32x4 wk = load16(krow + 16 * s), wv = load16(vrow + 16 * s);
+      kf[s] = as_bf16x8(k_live ? wk : z);
+      vf[s] = as_bf16x8(k_live ? wv : z);
     }
   }
 
@@ -364,39 +304,30 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   }
   const float sl2 = a.softmax_scale * kLog2e;
   PairTile<BMQ, D> qtile, gtile;
+  const int m_first = (m_begin / BMQ) * BMQ;
 
   for (int hq = hk * group; hq < (hk + 1) * group; ++hq) {
-    for (int m0 = (m_begin / BMQ) * BMQ; m0 < m_end; m0 += BMQ) {
-      auto qloc = [&](int m, int& rb, int& rt) -> bool {
-        if (m >= nq) return false;
-        rb = b;
-        rt = m;
-        if constexpr (MODE == kVarlen) split_flat(a.query_indices[qs + m], a.query_extent, rb, rt);
-        return true;
+    for (int m0 = m_first; m0 < m_end; m0 += BMQ) {
+      auto qrow_ptr = [&](const void* base, const int64_t* st, int r, bool& ok) -> const bf16* {
+        const int m = m0 + r;
+        ok = m < nq;
+        int rb, rt;
+        pb.query_loc(ok ? m : m0, rb, rt);
+        return row_at(base, st, rb, hq, rt);
       };
-      qtile.load(tid, [&](int r) -> const bf16* {
-        int rb, rt;
-        if (!qloc(m0 + r, rb, rt)) return nullptr;
-        return (const bf16*)a.q + (int64_t)rb * a.q_stride[0] + (int64_t)hq * a.q_stride[1] + (int64_t)rt * a.q_stride[2];
-      });
-      gtile.load(tid, [&](int r) -> const bf16* {
-        int rb, rt;
-        if (!qloc(m0 + r, rb, rt)) return nullptr;
-        return (const bf16*)a.dout + (int64_t)rb * a.do_stride[0] + (int64_t)hq * a.do_stride[1] +
-               (int64_t)rt * a.do_stride[2];
-      });
+      qtile.load(tid, [&](int r, bool& ok) { return qrow_ptr(a.q, a.q_stride, r, ok); });
+      gtile.load(tid, [&](int r, bool& ok) { return qrow_ptr(a.dout, a.do_stride, r, ok); });
       float lse_v = kPosInf, delta_v = 0.f;
       int qseg_v = INT_MIN, qstart_v = INT_MAX;
-      if (tid < BMQ) {
+      if (tid < BMQ && m0 + tid < nq) {
         int rb, rt;
-        if (qloc(m0 + tid, rb, rt)) {
-          const int64_t r = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
-          lse_v = a.lse[r] * kLog2e;
-          delta_v = a.delta[r];
-          if constexpr (MODE == kDoc) {
-            qseg_v = a.q_seg[(int64_t)b * a.q_len + m0 + tid];
-            qstart_v = a.q_start[(int64_t)b * a.q_len + m0 + tid];
-          }
+        pb.query_loc(m0 + tid, rb, rt);
+        const int64_t r = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
+        lse_v = a.lse[r] * kLog2e;
+        delta_v = a.delta[r];
+        if constexpr (MODE == kDoc) {
+          qseg_v = a.q_seg[(int64_t)b * a.q_len + m0 + tid];
+          qstart_v = a.q_start[(int64_t)b * a.q_len + m0 + tid];
         }
       }
       __syncthreads();
@@ -424,6 +355,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
           pacc[mb] = mfma32(lds_row_operand(g_lds, QLD, mb * 32 + col, s, half), vf[s], pacc[mb]);
         }
       }
+      const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= wave_m_begin &&
+                        m0 + BMQ <= nq && pb.bound.lim(m0) >= wave_key0 + 31;
 #pragma unroll
       for (int mb = 0; mb < BMQ / 32; ++mb) {
 #pragma unroll
@@ -435,12 +368,15 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
           for (int e = 0; e < 4; ++e) {
             const int r = 4 * g + e;
             const int m = m0 + ml + e;
-            bool keep = valid_k && !k_masked_out && m < nq && ((n <= bound(m)) || (slot0 && n == 0));
-            if constexpr (MODE == kDoc) {
-              const int qsg = qseg_lds[ml + e];
-              keep = keep && ((qsg == kseg_n && n >= qstart_lds[ml + e]) || kseg_n == -1) && (m < kqend_n);
+            bool keep = true;
+            if (!full) {
+              keep = k_live && m < nq && ((n <= pb.bound.lim(m)) || (slot0 && n == 0));
+              if constexpr (MODE == kDoc) {
+                const int qsg = qseg_lds[ml + e];
+                keep = keep && ((qsg == kseg_n && n >= qstart_lds[ml + e]) || kseg_n == -1) && (m < kqend_n);
+              }
             }
-            const float p = keep ? __builtin_amdgcn_exp2f(sacc[mb][r] * sl2 - l4[e]) : 0.f;
+            const float p = keep ? __builtin_amdgcn_exp2f(fmaf(sacc[mb][r], sl2, -l4[e])) : 0.f;
             sacc[mb][r] = p;
             pacc[mb][r] = p * (pacc[mb][r] - d4[e]);
           }
@@ -461,7 +397,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
 
   if (!valid_k) return;
   if constexpr (ATOMIC) {
-    // fp32 accumulators laid out [key_indices row][kv head][D]
+    // fp32 accumulators laid out [key row][kv head][D]
     const int64_t row = (int64_t)kb * a.key_extent + kslot;
     float* acck = (float*)a.workspace + (row * a.kv_heads + hk) * D;
     float* accv = acck + (int64_t)a.batch * a.key_extent * a.kv_heads * D;
@@ -475,10 +411,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
       }
     }
   } else {
-    bf16* dkrow = (bf16*)a.dk + (int64_t)kb * a.dk_stride[0] + (int64_t)hk * a.dk_stride[1] + (int64_t)kslot * a.dk_stride[2];
-    bf16* dvrow = (bf16*)a.dv + (int64_t)kb * a.dv_stride[0] + (int64_t)hk * a.dv_stride[1] + (int64_t)kslot * a.dv_stride[2];
-    store_acc_row<DB>(dkrow, dkacc, a.softmax_scale, half);
-    store_acc_row<DB>(dvrow, dvacc, 1.f, half);
+    store_acc_row<DB>((bf16*)row_at(a.dk, a.dk_stride, kb, hk, kslot), dkacc, a.softmax_scale, half);
+    store_acc_row<DB>((bf16*)row_at(a.dv, a.dv_stride, kb, hk, kslot), dvacc, 1.f, half);
   }
 }
 
@@ -533,26 +467,19 @@ int64_t bwd_workspace_size(const wmx_attn_args& a) {
 
 template <int D, int MODE>
 static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
-  dim3 grid;
-  if (MODE == kVarlen) {
-    if (a.num_segments <= 0) return WMX_OK;
-    grid = dim3((unsigned)(((a.max_queries + 127) / 128) * (int64_t)a.num_segments), a.q_heads, 1);
-  } else {
-    grid = dim3((a.q_len + 127) / 128, a.q_heads, a.batch);
-  }
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), grid, dim3(256), 0, stream, a);
+  const int64_t qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + 127) / 128;
+  const int64_t units = qtiles * (MODE == kVarlen ? a.num_segments : a.batch) * a.q_heads;
+  if (units <= 0) return WMX_OK;
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)logical_grid(units)), dim3(256), 0, stream, a);
   return WMX_OK;
 }
 
 template <int D, int MODE>
 static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
-  dim3 grid;
-  if (MODE == kVarlen) {
-    if (a.num_segments <= 0) return WMX_OK;
-    grid = dim3((unsigned)(((a.max_keys + 127) / 128) * (int64_t)a.num_segments), a.kv_heads, 1);
-  } else {
-    grid = dim3((a.kv_len + 127) / 128, a.kv_heads, a.batch);
-  }
+  const int64_t ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + 127) / 128;
+  const int64_t units = ktiles * (MODE == kVarlen ? a.num_segments : a.batch) * a.kv_heads;
+  if (units <= 0) return WMX_OK;
+  const dim3 grid((unsigned)logical_grid(units));
   if (MODE == kVarlen && !a.keys_unique) {
     const int64_t n = bwd_workspace_size(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,

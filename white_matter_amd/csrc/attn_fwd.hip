@@ -1,47 +1,42 @@
 // Flash-style attention forward for gfx950 (CDNA4), bf16 in, fp32 accumulate.
 //
-// One workgroup = 4 wave64s = 128 query rows of one (batch, query head);
-// each wave owns 32 query rows. Key/value tiles of 64 rows are staged in
-// LDS (K row-major, V transposed) and shared by the 4 waves.
+// One workgroup = 4 wave64s = 128 query rows of one (batch or segment,
+// query head); each wave owns 32 query rows. Key/value tiles of 64 rows are
+// staged through registers into LDS (K row-major, V transposed and
+// swizzled) and shared by the 4 waves; the next tile's global loads are in
+// flight while the current tile is computed.
 //
 // Each wave computes S^T = K Q^T so that a lane owns one query column: the
-// softmax row statistics are then per-lane scalars plus one exchange with
+// softmax row statistics are per-lane scalars plus one exchange with
 // lane ^ 32, and the output accumulator O^T = V^T P^T is rescaled by a
-// per-lane factor. P never leaves registers (see the k-order note in
-// wmx_device.h). Masking (strided causal bound, per-row offset/limit,
-// key mask, documents, varlen segments) is evaluated only on tiles that
-// can contain a masked pair; tiles nobody in the workgroup can see are
-// never loaded (tile skipping), and rows beyond the workgroup's reach are
-// zero-filled on load so that NaN in unused cache capacity cannot leak.
+// per-lane factor (skipped for the whole wave when no row maximum moved).
+// P never leaves registers (see the k-order note in wmx_device.h). Masks
+// (strided causal bound, per-row offset/limit, key mask, documents, varlen
+// segments) are evaluated only on tiles that can contain a masked pair;
+// tiles nobody in the workgroup can see are never loaded, and rows beyond
+// the workgroup's reach are zero-filled so NaN in unused cache capacity
+// cannot leak.
 //
 // Semantics follow the reference's portable path
 // (src/white_matter/ops/cyclic_attention/reference.py:10-42,
-//  src/white_matter/ops/strict_causal_attention.py:279-322) and its
-// numerics contract (exp2 online softmax with the rescale-by-exactly-one
-// guard, natural-log LSE, zero rows for empty visibility).
-#include <climits>
-
-#include "wmx_kernels.h"
+//  src/white_matter/ops/strict_causal_attention.py:279-322) with the
+// accelerated path's numerics contract (exp2 online softmax with the
+// rescale-by-exactly-one guard, natural-log LSE, zero rows for empty
+// visibility; _tilelang/forward.py:99-131).
+#include "attn_tiles.h"
 
 namespace wmx {
 
-template <int D>
-struct FwdTile {
-  static constexpr int BM = 128;
-  static constexpr int BN = 64;
-  static constexpr int KLD = D + 8;   // K tile row stride (elements)
-  static constexpr int VLD = BN + 8;  // V^T tile row stride (elements)
-};
+constexpr int kFwdBM = 128;  // query rows per workgroup
+constexpr int kFwdBN = 64;   // keys per tile
 
 template <int D, int MODE>
-__global__ __launch_bounds__(256) void attn_fwd_kernel(const wmx_attn_args a) {
-  using Tl = FwdTile<D>;
-  constexpr int BM = Tl::BM, BN = Tl::BN, KLD = Tl::KLD, VLD = Tl::VLD;
-  constexpr int KS = D / 16;          // MFMA k-steps over head_dim
-  constexpr int DB = D / 32;          // 32-row blocks of O^T
-  constexpr int CPR = D / 8;          // 16-byte chunks per row
-  constexpr int KCH = BN * CPR / 256; // K chunks per thread
-  constexpr int VCH = (BN / 2 * CPR + 255) / 256;  // V row-pair chunks per thread
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a) {
+  constexpr int BM = kFwdBM, BN = kFwdBN;
+  constexpr int KLD = D + 8;  // K tile row stride (elements)
+  constexpr int VLD = BN + 8; // V^T tile row stride (elements)
+  constexpr int KS = D / 16;  // MFMA k-steps over head_dim
+  constexpr int DB = D / 32;  // 32-row blocks of O^T
 
   __shared__ __attribute__((aligned(16))) bf16 k_lds[BN * KLD];
   __shared__ __attribute__((aligned(16))) bf16 vt_lds[D * VLD];
@@ -51,43 +46,24 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const wmx_attn_args a) {
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int half = lane >> 5, col = lane & 31;
-  const int h = blockIdx.y;
-  const int hk = h / (a.q_heads / a.kv_heads);
 
   // ---- resolve the problem this workgroup works on ----
-  int b = 0, nq, nk, q0, qs = 0, ks = 0;
-  int64_t offset, limit, qstride;
-  if constexpr (MODE == kVarlen) {
-    const int qtiles = (a.max_queries + BM - 1) / BM;
-    const int seg = blockIdx.x / qtiles;
-    const int tile = qtiles - 1 - (int)(blockIdx.x % qtiles);
-    qs = a.cu_queries[seg];
-    nq = a.cu_queries[seg + 1] - qs;
-    ks = a.cu_keys[seg];
-    nk = a.cu_keys[seg + 1] - ks;
-    q0 = tile * BM;
-    if (q0 >= nq) return;
-    offset = nk - nq;
-    limit = INT_MAX;
-    qstride = 1;
-  } else {
-    b = blockIdx.z;
-    nq = a.q_len;
-    nk = a.kv_len;
-    q0 = (gridDim.x - 1 - blockIdx.x) * BM;
-    offset = a.row_offset ? a.row_offset[b] : a.query_offset;
-    limit = a.row_limit ? a.row_limit[b] : INT_MAX;
-    qstride = a.query_stride;
-  }
-  auto lim_of = [&](int i) -> int {
-    int64_t l = offset + qstride * (int64_t)i;
-    l = l < limit ? l : limit;
-    l = l < (int64_t)nk - 1 ? l : (int64_t)nk - 1;
-    return (int)(l < -1 ? -1 : l);
-  };
-  const int q_last = min(q0 + BM, nq) - 1;
-  const int lim_max_wg = lim_of(q_last);
+  const int qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
+  const unsigned outer = MODE == kVarlen ? (unsigned)a.num_segments : (unsigned)a.batch;
+  unsigned unit;
+  if (!logical_unit((unsigned)qtiles * outer * a.q_heads, unit)) return;
+  const int q0 = (qtiles - 1 - (int)(unit % qtiles)) * BM;
+  const unsigned rest = unit / qtiles;
+  const int h = MODE == kVarlen ? (int)(rest / outer) : (int)(rest % a.q_heads);
+  const int grp = MODE == kVarlen ? (int)(rest % outer) : (int)(rest / a.q_heads);
+  const int hk = h / (a.q_heads / a.kv_heads);
+  Problem<MODE> pb;
+  pb.init(a, grp);
+  const int b = pb.b, nq = pb.nq, nk = pb.nk;
+  if (q0 >= nq) return;
+  auto lim_of = [&](int i) { return pb.bound.lim(i); };
   const bool slot0 = a.keep_slot0 && nk > 0;
+  const int lim_max_wg = lim_of(min(q0 + BM, nq) - 1);
 
   // ---- this lane's query row ----
   const int i = q0 + wave * 32 + col;
@@ -98,24 +74,21 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const wmx_attn_args a) {
   const int lim_min_wave = lim_of(wave_first);
   const int lim_max_wave = lim_of(min(wave_first + 31, nq - 1));
 
-  int qb = b, qt = i;
-  if constexpr (MODE == kVarlen) {
-    if (valid_q) split_flat(a.query_indices[qs + i], a.query_extent, qb, qt);
-  }
-  const RowSource qsrc{(const bf16*)a.q, a.q_stride[0], a.q_stride[1], a.q_stride[2]};
+  int qb, qt;
+  pb.query_loc(valid_q ? i : q0, qb, qt);
   bf16x8 qf[KS];
   {
-    const bf16* qrow = row_ptr(qsrc, qb, h, qt);
+    const bf16* qrow = (const bf16*)a.q + (int64_t)qb * a.q_stride[0] + (int64_t)h * a.q_stride[1] +
+                       (int64_t)qt * a.q_stride[2] + 8 * half;
+    const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (valid_q) w = load16(qrow + 16 * s + 8 * half);
-      qf[s] = as_bf16x8(w);
+      const u32x4 w = load16(qrow + 16 * s);
+      qf[s] = as_bf16x8(valid_q ? w : z);
     }
   }
 
-  int qseg_i = 0, qstart_i = 0;
-  int kt_begin_main = 0;
+  int qseg_i = 0, qstart_i = 0, kt_begin_main = 0;
   if constexpr (MODE == kDoc) {
     if (valid_q) {
       qseg_i = a.q_seg[(int64_t)b * a.q_len + i];
@@ -131,7 +104,7 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const wmx_attn_args a) {
     kt_begin_main = v < 0 ? 0 : v / BN;
   }
 
-  // ---- key tile range ----
+  // ---- key tile range: tile 0 stays when it holds the shared dummy ----
   int kt_end = (lim_max_wg + 1 + BN - 1) / BN;
   if (slot0 && kt_end < 1) kt_end = 1;
   const int first_main = kt_begin_main > 1 ? kt_begin_main : 1;
@@ -139,77 +112,33 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const wmx_attn_args a) {
   const int ntiles = gap ? 1 + max(0, kt_end - first_main) : kt_end;
   auto tile_of = [&](int it) { return gap ? (it == 0 ? 0 : first_main + it - 1) : it; };
 
-  const RowSource ksrc{(const bf16*)a.k, a.k_stride[0], a.k_stride[1], a.k_stride[2]};
-  const RowSource vsrc{(const bf16*)a.v, a.v_stride[0], a.v_stride[1], a.v_stride[2]};
-  auto key_row_valid = [&](int j) -> bool {
-    if (j >= nk) return false;
-    if (!(j <= lim_max_wg || (slot0 && j == 0))) return false;
-    if (MODE == kDense && a.key_mask) return a.key_mask[(int64_t)b * a.key_mask_stride + j] != 0;
-    return true;
-  };
-  auto key_loc = [&](int j, int& kb, int& kt) {
-    if constexpr (MODE == kVarlen) {
-      split_flat(a.key_indices[ks + j], a.key_extent, kb, kt);
-    } else {
-      kb = b;
-      kt = j;
-    }
+  // key row j of this problem as a global pointer into K (or V)
+  auto key_ptr = [&](const void* base, const int64_t* st, int j, bool& ok) -> const bf16* {
+    ok = j < nk && (j <= lim_max_wg || (slot0 && j == 0));
+    if (MODE == kDense && a.key_mask) ok = ok && a.key_mask[(int64_t)b * a.key_mask_stride + min(j, nk - 1)] != 0;
+    int kb, kt;
+    pb.key_loc(ok ? j : 0, kb, kt);
+    return row_at(base, st, kb, hk, kt);
   };
 
-  u32x4 kreg[KCH];
-  u32x4 vreg[VCH][2];
+  PairTile<BN, D> ktile, vtile;
   auto load_tile = [&](int n0) {
-#pragma unroll
-    for (int r = 0; r < KCH; ++r) {
-      const int c = tid + 256 * r;
-      const int row = c / CPR, cc = c % CPR;
-      const int j = n0 + row;
-      u32x4 w = {0u, 0u, 0u, 0u};
-      if (key_row_valid(j)) {
-        int kb, kt;
-        key_loc(j, kb, kt);
-        w = load16(row_ptr(ksrc, kb, hk, kt) + 8 * cc);
-      }
-      kreg[r] = w;
-    }
-#pragma unroll
-    for (int r = 0; r < VCH; ++r) {
-      const int c = tid + 256 * r;
-      const int p = c / CPR, cc = c % CPR;
-#pragma unroll
-      for (int u = 0; u < 2; ++u) {
-        const int j = n0 + 2 * p + u;
-        u32x4 w = {0u, 0u, 0u, 0u};
-        if (c < BN / 2 * CPR && key_row_valid(j)) {
-          int kb, kt;
-          key_loc(j, kb, kt);
-          w = load16(row_ptr(vsrc, kb, hk, kt) + 8 * cc);
-        }
-        vreg[r][u] = w;
-      }
-    }
+    ktile.load(tid, [&](int r, bool& ok) { return key_ptr(a.k, a.k_stride, n0 + r, ok); });
+    vtile.load(tid, [&](int r, bool& ok) { return key_ptr(a.v, a.v_stride, n0 + r, ok); });
   };
-  auto store_tile = [&](int n0) {
+
+  f32x16 oacc[DB];
 #pragma unroll
-    for (int r = 0; r < KCH; ++r) {
-      const int c = tid + 256 * r;
-      const int row = c / CPR, cc = c % CPR;
-      *reinterpret_cast<u32x4*>(&k_lds[row * KLD + 8 * cc]) = kreg[r];
-    }
-#pragma unroll
-    for (int r = 0; r < VCH; ++r) {
-      const int c = tid + 256 * r;
-      if (c < BN / 2 * CPR) {
-        const int p = c / CPR, cc = c % CPR;
-        const u32x4 x = vreg[r][0], y = vreg[r][1];
-        uint32_t* dst = reinterpret_cast<uint32_t*>(&vt_lds[(8 * cc) * VLD + 2 * p]);
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          dst[(2 * e) * (VLD / 2)] = (x[e] & 0xffffu) | (y[e] << 16);
-          dst[(2 * e + 1) * (VLD / 2)] = (x[e] >> 16) | (y[e] & 0xffff0000u);
-        }
-      }
-    }
+  for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
+  float m_run = kNegInf, l_run = 0.f;
+  const float sl2 = a.softmax_scale * kLog2e;  // > 0 (checked on the host)
+
+  if (ntiles > 0) load_tile(tile_of(0) * BN);
+  for (int it = 0; it < ntiles; ++it) {
+    const int n0 = tile_of(it) * BN;
+    __syncthreads();
+    ktile.store_rows(tid, k_lds, KLD);
+    vtile.store_cols(tid, vt_lds, VLD);
     if constexpr (MODE == kDoc) {
       if (tid < BN) {
         const int j = n0 + tid;
@@ -222,19 +151,6 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const wmx_attn_args a) {
         kseg_lds[tid] = j < nk ? (int)a.key_mask[(int64_t)b * a.key_mask_stride + j] : 0;
       }
     }
-  };
-
-  f32x16 oacc[DB];
-#pragma unroll
-  for (int d = 0; d < DB; ++d) oacc[d] = f32x16{};
-  float m_run = kNegInf, l_run = 0.f;
-  const float sl2 = a.softmax_scale * kLog2e;
-
-  if (ntiles > 0) load_tile(tile_of(0) * BN);
-  for (int it = 0; it < ntiles; ++it) {
-    const int n0 = tile_of(it) * BN;
-    __syncthreads();
-    store_tile(n0);
     __syncthreads();
     if (it + 1 < ntiles) load_tile(tile_of(it + 1) * BN);
 
@@ -245,22 +161,24 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const wmx_attn_args a) {
 #pragma unroll
     for (int nb = 0; nb < BN / 32; ++nb) {
       sacc[nb] = f32x16{};
-      const bf16* krow = &k_lds[(nb * 32 + col) * KLD + 8 * half];
 #pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        sacc[nb] = mfma32(as_bf16x8(*reinterpret_cast<const u32x4*>(krow + 16 * s)), qf[s], sacc[nb]);
-      }
+      for (int s = 0; s < KS; ++s)
+        sacc[nb] = mfma32(lds_row_operand(k_lds, KLD, nb * 32 + col, s, half), qf[s], sacc[nb]);
     }
 
     const bool full = (MODE != kDoc) && !(MODE == kDense && a.key_mask) && (n0 + BN - 1 <= lim_min_wave) &&
                       (n0 + BN <= nk);
     float rmax = kNegInf;
+    if (full) {
 #pragma unroll
-    for (int nb = 0; nb < BN / 32; ++nb) {
+      for (int nb = 0; nb < BN / 32; ++nb)
 #pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        float x = sacc[nb][r] * sl2;
-        if (!full) {
+        for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, sacc[nb][r]);
+    } else {
+#pragma unroll
+      for (int nb = 0; nb < BN / 32; ++nb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
           const int jl = nb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
           const int j = n0 + jl;
           bool keep = (j <= lim_i) || (slot0 && j == 0);
@@ -271,86 +189,61 @@ __global__ __launch_bounds__(256) void attn_fwd_kernel(const wmx_attn_args a) {
             const int ksg = kseg_lds[jl];
             keep = keep && j < nk && ((ksg == qseg_i && j >= qstart_i) || ksg == -1) && (i < kqend_lds[jl]);
           }
-          x = keep ? x : kNegInf;
+          const float x = keep ? sacc[nb][r] : kNegInf;
+          sacc[nb][r] = x;
+          rmax = fmaxf(rmax, x);
         }
-        sacc[nb][r] = x;
-        rmax = fmaxf(rmax, x);
       }
     }
     rmax = fmaxf(rmax, xor32(rmax));
-    const float m_new = fmaxf(m_run, rmax);
+    const float m_new = fmaxf(m_run, rmax * sl2);
     const float m_use = fmaxf(m_new, kMaxFloor);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     float rsum = 0.f;
 #pragma unroll
     for (int nb = 0; nb < BN / 32; ++nb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(sacc[nb][r] - m_use);
+        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[nb][r], sl2, -m_use));
         sacc[nb][r] = p;
         rsum += p;
       }
     }
     rsum += xor32(rsum);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
     l_run = l_run * alpha + rsum;
     m_run = m_new;
+    if (__any(alpha != 1.f)) {
 #pragma unroll
-    for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+    }
 
 #pragma unroll
     for (int s = 0; s < BN / 16; ++s) {
-      const f32x16& src = sacc[s >> 1];
-      const int base = 8 * (s & 1);
-      u32x4 pw;
-      pw[0] = pack_bf16x2(src[base + 0], src[base + 1]);
-      pw[1] = pack_bf16x2(src[base + 2], src[base + 3]);
-      pw[2] = pack_bf16x2(src[base + 4], src[base + 5]);
-      pw[3] = pack_bf16x2(src[base + 6], src[base + 7]);
-      const bf16x8 pb = as_bf16x8(pw);
+      const bf16x8 pb = acc_kperm_operand(sacc[s >> 1], s);
 #pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        const bf16* vrow = &vt_lds[(d * 32 + col) * VLD + 16 * s + 4 * half];
-        const u32x2 lo = *reinterpret_cast<const u32x2*>(vrow);
-        const u32x2 hi = *reinterpret_cast<const u32x2*>(vrow + 8);
-        const u32x4 va = {lo[0], lo[1], hi[0], hi[1]};
-        oacc[d] = mfma32(as_bf16x8(va), pb, oacc[d]);
-      }
+      for (int d = 0; d < DB; ++d) oacc[d] = mfma32(lds_kperm_operand(vt_lds, VLD, d * 32 + col, s, half), pb, oacc[d]);
     }
   }
 
   if (!valid_q) return;
   const float inv = l_run > 0.f ? 1.f / l_run : 0.f;
-  int ob = b, ot = i;
-  if constexpr (MODE == kVarlen) { ob = qb; ot = qt; }
-  bf16* orow = (bf16*)a.o + (int64_t)ob * a.o_stride[0] + (int64_t)h * a.o_stride[1] + (int64_t)ot * a.o_stride[2];
-#pragma unroll
-  for (int d = 0; d < DB; ++d) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x2 w;
-      w[0] = pack_bf16x2(oacc[d][4 * g + 0] * inv, oacc[d][4 * g + 1] * inv);
-      w[1] = pack_bf16x2(oacc[d][4 * g + 2] * inv, oacc[d][4 * g + 3] * inv);
-      store8(orow + d * 32 + 8 * g + 4 * half, w);
-    }
-  }
+  bf16* orow = (bf16*)a.o + (int64_t)qb * a.o_stride[0] + (int64_t)h * a.o_stride[1] + (int64_t)qt * a.o_stride[2];
+  store_acc_row<DB>(orow, oacc, inv, half);
   if (half == 0) {
     const float lse = l_run > 0.f ? (m_run + __log2f(l_run)) * kLn2 : kPosInf;
-    a.lse[((int64_t)ob * a.q_heads + h) * a.q_len + ot] = lse;
+    a.lse[((int64_t)qb * a.q_heads + h) * a.q_len + qt] = lse;
   }
 }
 
 template <int D, int MODE>
 static int launch_fwd_t(const wmx_attn_args& a, hipStream_t stream) {
-  constexpr int BM = FwdTile<D>::BM;
-  dim3 grid;
-  if (MODE == kVarlen) {
-    if (a.num_segments <= 0 || a.max_queries <= 0) return WMX_OK;
-    const int64_t qtiles = (a.max_queries + BM - 1) / BM;
-    grid = dim3((unsigned)(qtiles * a.num_segments), a.q_heads, 1);
-  } else {
-    grid = dim3((a.q_len + BM - 1) / BM, a.q_heads, a.batch);
-  }
-  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), grid, dim3(256), 0, stream, a);
+  const int64_t qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + kFwdBM - 1) / kFwdBM;
+  const int64_t outer = MODE == kVarlen ? a.num_segments : a.batch;
+  const int64_t units = qtiles * outer * a.q_heads;
+  if (units <= 0) return WMX_OK;
+  const int64_t blocks = logical_grid(units);
+  if (blocks > INT_MAX) return WMX_E_UNSUPPORTED;
+  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
   return WMX_OK;
 }
 

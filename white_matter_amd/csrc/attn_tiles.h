@@ -1,0 +1,98 @@
+// Per-workgroup problem resolution shared by the attention kernels.
+//
+// A workgroup owns either 128 query rows (forward, dQ) or 128 key rows (dK/dV)
+// of one (batch row or varlen segment, head). These structs decode its
+// logical index (XCD-aware: consecutive units share one XCD's L2, heavy query
+// tiles first), locate its rows, and evaluate the visibility bound
+//   lim(i) = clamp(min(offset + stride * i, limit), -1, nk - 1)
+// of wmx_attn_args.
+#pragma once
+
+#include <climits>
+
+#include "wmx_kernels.h"
+
+namespace wmx {
+
+// Workgroups are dispatched round-robin over the 8 XCDs: blockIdx.x % 8 picks
+// the XCD. Consecutive logical units are mapped to one XCD.
+__device__ __forceinline__ bool logical_unit(unsigned total, unsigned& unit) {
+  const unsigned per_xcd = gridDim.x >> 3;
+  unit = (blockIdx.x & 7u) * per_xcd + (blockIdx.x >> 3);
+  return unit < total;
+}
+
+// Launch size for `units` logical units (a multiple of 8 workgroups).
+inline int64_t logical_grid(int64_t units) { return (units + 7) / 8 * 8; }
+
+struct Bounds {
+  int64_t offset, limit, stride;
+  int nk;
+  __device__ __forceinline__ int lim(int i) const {
+    int64_t l = offset + stride * (int64_t)i;
+    l = l < limit ? l : limit;
+    l = l < (int64_t)nk - 1 ? l : (int64_t)nk - 1;
+    return (int)(l < -1 ? -1 : l);
+  }
+  // Smallest query row whose bound reaches key j (nq when none does).
+  __device__ __forceinline__ int first_row(int j, int nq) const {
+    if (j > nk - 1 || limit < j) return nq;
+    const int64_t need = (int64_t)j - offset;
+    const int64_t m = need <= 0 ? 0 : (need + stride - 1) / stride;
+    return m < nq ? (int)m : nq;
+  }
+};
+
+// The rows of one problem (a batch row of a dense call, or a varlen segment).
+template <int MODE>
+struct Problem {
+  int b;        // batch row (dense / documents)
+  int nq, nk;   // query and key rows
+  Bounds bound;
+  SegmentRows qrows, krows;  // varlen only
+
+  // grp = batch row or segment index. Returns false for an empty segment side.
+  __device__ __forceinline__ void init(const wmx_attn_args& a, int grp) {
+    b = grp;
+    if constexpr (MODE == kVarlen) {
+      const int qs = a.cu_queries[grp], ks = a.cu_keys[grp];
+      nq = a.cu_queries[grp + 1] - qs;
+      nk = a.cu_keys[grp + 1] - ks;
+      if (nq > 0)
+        qrows.init(a.query_indices + qs, nq, a.query_extent, a.segment_layout & kQueriesConsecutive,
+                   a.segment_layout & kQueriesOneRow, false);
+      if (nk > 0)
+        krows.init(a.key_indices + ks, nk, a.key_extent, a.segment_layout & kKeysConsecutive,
+                   a.segment_layout & kKeysOneRow, true);
+      bound = Bounds{nk - nq, INT_MAX, 1, nk};
+    } else {
+      nq = a.q_len;
+      nk = a.kv_len;
+      bound = Bounds{a.row_offset ? a.row_offset[b] : a.query_offset, a.row_limit ? a.row_limit[b] : INT_MAX,
+                     a.query_stride, nk};
+    }
+  }
+  // (row, slot) of query row i and key row j (both must be in range)
+  __device__ __forceinline__ void query_loc(int i, int& qb, int& qt) const {
+    if constexpr (MODE == kVarlen) {
+      qrows.locate(i, qb, qt);
+    } else {
+      qb = b;
+      qt = i;
+    }
+  }
+  __device__ __forceinline__ void key_loc(int j, int& kb, int& kt) const {
+    if constexpr (MODE == kVarlen) {
+      krows.locate(j, kb, kt);
+    } else {
+      kb = b;
+      kt = j;
+    }
+  }
+};
+
+__device__ __forceinline__ const bf16* row_at(const void* base, const int64_t* st, int b, int h, int t) {
+  return (const bf16*)base + (int64_t)b * st[0] + (int64_t)h * st[1] + (int64_t)t * st[2];
+}
+
+}  // namespace wmx

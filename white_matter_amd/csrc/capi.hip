@@ -39,7 +39,7 @@ int check_common(const wmx_attn_args* a, bool backward) {
     return fail(WMX_E_INVALID, "negative or zero shape");
   if (a->q_heads % a->kv_heads != 0) return fail(WMX_E_INVALID, "q_heads %% kv_heads != 0");
   if (a->query_stride < 1) return fail(WMX_E_INVALID, "query_stride must be >= 1");
-  if (!(a->softmax_scale == a->softmax_scale)) return fail(WMX_E_INVALID, "softmax_scale is NaN");
+  if (!(a->softmax_scale > 0.f)) return fail(WMX_E_UNSUPPORTED, "softmax_scale must be positive and finite");
   if (!a->q || !a->k || !a->v || !a->o || !a->lse) return fail(WMX_E_INVALID, "q/k/v/o/lse pointer is NULL");
   if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v))
     return fail(WMX_E_INVALID, "q/k/v must be 16-byte aligned");

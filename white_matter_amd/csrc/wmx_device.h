@@ -75,10 +75,60 @@ __device__ __forceinline__ void split_flat(int64_t flat, int extent, int& b, int
   t = (int)(flat - (int64_t)b * extent);
 }
 
+// segment_layout bits of wmx_attn_args
+constexpr int kQueriesConsecutive = 1;  // query i of a segment sits at slot t0 + i of one row
+constexpr int kKeysConsecutive = 2;     // key j >= 1 sits at slot t1 + j - 1 of one row
+constexpr int kQueriesOneRow = 4;       // every query of a segment is in the row of its first
+constexpr int kKeysOneRow = 8;          // every key of a segment is in the row of its first
+
+// Where the rows of one varlen segment live: one division per workgroup,
+// then per-row slots by addition (consecutive layout) or by subtracting the
+// row base from the gathered flat index (one row); the general case divides.
+struct SegmentRows {
+  const int64_t* idx;  // the segment's first flat index
+  int extent;
+  int layout;          // consecutive / one-row bits for this side
+  bool from_one;       // consecutive from element 1 (keys: element 0 may be the dummy)
+  int row;
+  int64_t row_base;    // row * extent
+  int slot0, slot1;    // slots of elements 0 and 1
+
+  __device__ void init(const int64_t* first, int count, int extent_, bool consecutive, bool one_row, bool from_one_) {
+    idx = first;
+    extent = extent_;
+    layout = (consecutive ? 1 : 0) | (one_row ? 2 : 0);
+    from_one = from_one_;
+    int t0 = 0;
+    split_flat(first[0], extent, row, t0);
+    row_base = (int64_t)row * extent;
+    slot0 = t0;
+    slot1 = count > 1 ? (int)(first[1] - row_base) : t0 + 1;
+  }
+  __device__ __forceinline__ void locate(int j, int& b, int& t) const {
+    if (layout & 1) {
+      b = row;
+      t = from_one ? (j == 0 ? slot0 : slot1 + j - 1) : slot0 + j;
+    } else if (layout & 2) {
+      b = row;
+      t = (int)(idx[j] - row_base);
+    } else {
+      split_flat(idx[j], extent, b, t);
+    }
+  }
+};
+
+// Transposed LDS tiles t[d][n] are XOR-swizzled in groups of four elements:
+// element (d, n) lives at d * ld + (n ^ tswz(d)). Groups of four stay
+// contiguous (8-byte operand reads), and the 16 lanes that store one column
+// chunk of a row pair hit 16 distinct banks instead of 2.
+__device__ __forceinline__ int tswz(int d) { return ((d >> 3) & 7) << 2; }
+
 // A [ROWS x D] bf16 tile staged through registers, read as row pairs so the
 // same registers can be written to LDS row-major, transposed, or both.
-// rp(r) returns the global row pointer of tile row r, or nullptr for a row
-// that must read as zeros (outside the problem or beyond every reader's reach).
+// rp(r, ok) returns a dereferenceable global pointer for tile row r and sets
+// ok = false for a row that must read as zeros (outside the problem or beyond
+// every reader's reach); such rows are loaded from a valid row and zeroed, so
+// the loads are branch-free.
 template <int ROWS, int D, int NT = 256>
 struct PairTile {
   static constexpr int CPR = D / 8;
@@ -91,16 +141,15 @@ struct PairTile {
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
       const int c = tid + NT * r;
-      u32x4 wx = {0u, 0u, 0u, 0u}, wy = {0u, 0u, 0u, 0u};
-      if (c < N) {
-        const int p = c / CPR, cc = c % CPR;
-        const bf16* ra = rp(2 * p);
-        const bf16* rb = rp(2 * p + 1);
-        if (ra) wx = load16(ra + 8 * cc);
-        if (rb) wy = load16(rb + 8 * cc);
-      }
-      x[r] = wx;
-      y[r] = wy;
+      const int cl = c < N ? c : N - 1;
+      const int p = cl / CPR, cc = cl % CPR;
+      bool oka, okb;
+      const bf16* ra = rp(2 * p, oka);
+      const bf16* rb = rp(2 * p + 1, okb);
+      const u32x4 wx = load16(ra + 8 * cc), wy = load16(rb + 8 * cc);
+      const u32x4 z = {0u, 0u, 0u, 0u};
+      x[r] = oka ? wx : z;
+      y[r] = okb ? wy : z;
     }
   }
   // lds[row * ld + d]
@@ -115,18 +164,20 @@ struct PairTile {
       }
     }
   }
-  // lds[d * ld + row]; ld must be even
+  // lds[d * ld + (row ^ tswz(d))]; ld even, ROWS a multiple of 32
   __device__ __forceinline__ void store_cols(int tid, bf16* lds, int ld) const {
 #pragma unroll
     for (int r = 0; r < PER; ++r) {
       const int c = tid + NT * r;
       if (c < N) {
         const int p = c / CPR, cc = c % CPR;
-        uint32_t* dst = reinterpret_cast<uint32_t*>(lds + (8 * cc) * ld + 2 * p);
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          dst[(2 * e) * (ld / 2)] = (x[r][e] & 0xffffu) | (y[r][e] << 16);
-          dst[(2 * e + 1) * (ld / 2)] = (x[r][e] >> 16) | (y[r][e] & 0xffff0000u);
+          const int d0 = 8 * cc + 2 * e;
+          uint32_t* lo = reinterpret_cast<uint32_t*>(lds + d0 * ld + ((2 * p) ^ tswz(d0)));
+          uint32_t* hi = reinterpret_cast<uint32_t*>(lds + (d0 + 1) * ld + ((2 * p) ^ tswz(d0 + 1)));
+          *lo = (x[r][e] & 0xffffu) | (y[r][e] << 16);
+          *hi = (x[r][e] >> 16) | (y[r][e] & 0xffff0000u);
         }
       }
     }
@@ -134,11 +185,12 @@ struct PairTile {
 };
 
 // MFMA operand whose k order follows an accumulator's row order, read from a
-// transposed LDS tile t[row * ld + k]: k = {16s + 4h + [0,4), 16s + 8 + 4h + [0,4)}.
+// transposed, swizzled LDS tile: k = {16s + 4h + [0,4), 16s + 8 + 4h + [0,4)}.
 __device__ __forceinline__ bf16x8 lds_kperm_operand(const bf16* t, int ld, int row, int s, int half) {
-  const bf16* p = t + row * ld + 16 * s + 4 * half;
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(p);
-  const u32x2 hi = *reinterpret_cast<const u32x2*>(p + 8);
+  const bf16* base = t + row * ld;
+  const int sw = tswz(row);
+  const u32x2 lo = *reinterpret_cast<const u32x2*>(base + ((16 * s + 4 * half) ^ sw));
+  const u32x2 hi = *reinterpret_cast<const u32x2*>(base + ((16 * s + 8 + 4 * half) ^ sw));
   const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
   return as_bf16x8(v);
 }

@@ -58,20 +58,23 @@ class StrictCausalMetadata:
         """Address the same key slots in storage rows of width ``key_extent``."""
         if key_extent == self.key_extent:
             return self
-        row, slot = torch.div(self.key_indices, self.key_extent, rounding_mode="floor"), self.key_indices % self.key_extent
-        remapped = StrictCausalMetadata(
-            self.query_indices,
-            row * key_extent + slot,
-            self.cu_queries,
-            self.cu_keys,
-            self.max_queries,
-            self.max_keys,
-            key_extent,
-            self.segments,
-        )
-        facts = getattr(self, "_facts", None)
-        if facts is not None:
-            object.__setattr__(remapped, "_facts", facts)
+        # one remapped schedule per storage width, so its host facts are computed once
+        remapped_by_extent = self.__dict__.setdefault("_remapped", {})
+        remapped = remapped_by_extent.get(key_extent)
+        if remapped is None:
+            row = torch.div(self.key_indices, self.key_extent, rounding_mode="floor")
+            slot = self.key_indices % self.key_extent
+            remapped = StrictCausalMetadata(
+                self.query_indices,
+                row * key_extent + slot,
+                self.cu_queries,
+                self.cu_keys,
+                self.max_queries,
+                self.max_keys,
+                key_extent,
+                self.segments,
+            )
+            remapped_by_extent[key_extent] = remapped
         return remapped
 
 
@@ -161,10 +164,30 @@ def prepare_strict_causal_metadata(
 
 
 # ---------------------------------------------------------------- schedules --
-def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int, int]:
+def _segment_layout(indices: torch.Tensor, cu: torch.Tensor, extent: int, skip_first: bool) -> tuple[bool, bool]:
+    """(consecutive, one_row) over all segments: element e of a segment sits at
+    slot first + e (from element 1 on when skip_first), and every element of a
+    segment lies in the row of its first element."""
+    n = indices.numel()
+    if n == 0:
+        return True, True
+    owner = torch.repeat_interleave(torch.arange(cu.numel() - 1, device=indices.device), cu.diff().long())
+    local = torch.arange(n, device=indices.device) - cu.long()[owner]
+    start = indices[cu.long()[owner]]
+    rows_ok = bool((torch.div(indices, extent, rounding_mode="floor") == torch.div(start, extent, rounding_mode="floor")).all())
+    if skip_first:
+        second = indices[(cu.long()[owner] + 1).clamp_max(n - 1)]
+        expected = torch.where(local == 0, indices, second + local - 1)
+    else:
+        expected = start + local
+    return bool((indices == expected).all()) and rows_ok, rows_ok
+
+
+def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int, int, int]:
     """Host facts the kernels need, computed once per metadata object and kept
     on it: largest segment (queries, keys), whether key rows repeat across
-    segments, and the largest query and key index (for bounds checks)."""
+    segments, the largest query and key index (for bounds checks), and the
+    segment layout bits of wmx_attn_args (consecutive / one-row slots)."""
     facts = getattr(metadata, "_facts", None)
     if facts is None:
         segments = metadata.segments
@@ -179,7 +202,10 @@ def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int
         top_k = int(ki.max()) if n else -1
         if (qi.numel() and int(qi.min()) < 0) or (n and int(ki.min()) < 0):
             raise ValueError("metadata indices must be nonnegative")
-        facts = (max_q, max_k, unique, top_q, top_k)
+        q_consecutive, q_one_row = _segment_layout(qi, metadata.cu_queries, metadata.max_queries, False)
+        k_consecutive, k_one_row = _segment_layout(ki, metadata.cu_keys, metadata.key_extent, True)
+        layout = (1 if q_consecutive else 0) | (2 if k_consecutive else 0) | (4 if q_one_row else 0) | (8 if k_one_row else 0)
+        facts = (max_q, max_k, unique, top_q, top_k, layout)
         object.__setattr__(metadata, "_facts", facts)
     return facts
 
@@ -289,7 +315,16 @@ def _dense_backward(ctx, dout, dlse):
 strict_dense_fwd.register_autograd(_dense_backward, setup_context=_dense_setup)
 
 
-def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, max_k, keys_unique):
+_KEYS_UNIQUE = 16  # schedule_flags bit above the four segment-layout bits
+
+
+def _schedule_flags(metadata: StrictCausalMetadata) -> tuple[int, int, int]:
+    """(max_queries, max_keys, flags) passed to the varlen operators."""
+    max_q, max_k, unique, _, _, layout = _schedule_facts(metadata)
+    return max_q, max_k, layout | (_KEYS_UNIQUE if unique else 0)
+
+
+def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, max_k, flags):
     return _kernels.Varlen(
         query_indices=query_indices.contiguous(),
         key_indices=key_indices.contiguous(),
@@ -300,7 +335,8 @@ def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, 
         max_keys=max_k,
         query_extent=query.shape[2],
         key_extent=key.shape[2],
-        keys_unique=keys_unique,
+        keys_unique=bool(flags & _KEYS_UNIQUE),
+        segment_layout=flags & 15,
     )
 
 
@@ -315,7 +351,7 @@ def strict_varlen_fwd(
     cu_keys: torch.Tensor,
     max_queries: int,
     max_keys: int,
-    keys_unique: bool,
+    schedule_flags: int,
     scale: float,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Packed-segment attention read straight from (B, H, T, D) storage;
@@ -325,7 +361,7 @@ def strict_varlen_fwd(
     out = torch.zeros(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
     lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
     vis = _kernels.Visibility(
-        varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, keys_unique)
+        varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags)
     )
     _kernels.forward(q, k, v, out.transpose(1, 2), lse, scale, vis)
     return out, lse
@@ -354,7 +390,7 @@ def strict_varlen_bwd(
     cu_keys: torch.Tensor,
     max_queries: int,
     max_keys: int,
-    keys_unique: bool,
+    schedule_flags: int,
     scale: float,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     q, k, v = (_kernels.operand(t) for t in (query, key, value))
@@ -364,7 +400,7 @@ def strict_varlen_bwd(
     dk = torch.zeros(k.shape, device=q.device, dtype=torch.bfloat16)
     dv = torch.zeros(v.shape, device=q.device, dtype=torch.bfloat16)
     vis = _kernels.Visibility(
-        varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, keys_unique)
+        varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags)
     )
     _kernels.backward(q, k, v, o, lse, g, dq, dk, dv, scale, vis)
     return dq, dk, dv
@@ -380,7 +416,7 @@ def _(query, key, value, *args):
 
 
 def _varlen_setup(ctx, inputs, output):
-    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.unique, ctx.scale = inputs
+    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale = inputs
     ctx.dtypes = (query.dtype, key.dtype, value.dtype)
     ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck)
 
@@ -388,7 +424,7 @@ def _varlen_setup(ctx, inputs, output):
 def _varlen_backward(ctx, dout, dlse):
     query, key, value, out, lse, qi, ki, cq, ck = ctx.saved_tensors
     dq, dk, dv = strict_varlen_bwd(
-        query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.unique, ctx.scale
+        query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale
     )
     return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 8
 
@@ -480,6 +516,8 @@ def _hip_attention(query, key, value, query_start, kv_lengths, use_dummy_token, 
     padded = _kernels.kernel_head_dim(dim)
     if padded is None:
         raise _unsupported(dim)
+    if not scale > 0:
+        raise RuntimeError(f"the gfx950 attention kernels: this path does not support softmax_scale {scale}")
     dtype = query.dtype
     q, k, v = (_kernels.pad_head_dim(t, padded) for t in (query, key, value))
     offset = int(use_dummy_token)
@@ -493,12 +531,13 @@ def _hip_attention(query, key, value, query_start, kv_lengths, use_dummy_token, 
     elif metadata is not None:
         if metadata.query_indices.numel() == 0:
             return _zeros_linked(query, key, value, batch, length, heads, dim)
-        max_q, max_k, unique, top_q, top_k = _schedule_facts(metadata)
+        _, _, _, top_q, top_k, _ = _schedule_facts(metadata)
+        max_q, max_k, flags = _schedule_flags(metadata)
         if metadata.max_queries != length or top_q >= batch * length or top_k >= batch * key.shape[2]:
             raise ValueError("metadata was prepared for other query/key shapes")
         out, _ = strict_varlen_fwd(
             q, k, v, metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
-            max_q, max_k, unique, scale,
+            max_q, max_k, flags, scale,
         )
     else:
         row_offset = row_limit = None

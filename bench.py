@@ -197,6 +197,11 @@ def main(argv=None) -> int:
     parser.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
+    parser.add_argument(
+        "--copy-calibration",
+        action="store_true",
+        help="first run one device copy of 256 MiB, the known-size kernel that scales FETCH_SIZE/WRITE_SIZE",
+    )
     args = parser.parse_args(argv)
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
@@ -208,6 +213,12 @@ def main(argv=None) -> int:
     from white_matter_amd import strict_causal_attention
 
     device = torch.device("cuda:0")
+    if args.copy_calibration:
+        src = torch.ones(256 << 20, dtype=torch.uint8, device=device)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
     q, k, v, docs, metadata, meta_ms = strict_jacobi_setup(device)
     batch, heads, length, dim = q.shape
     pairs = visible_pairs(metadata)

@@ -65,7 +65,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   __shared__ int kqend_lds[BN];
   __shared__ int red_lds[4];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
 
   const int qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
@@ -236,7 +236,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   __shared__ __attribute__((aligned(16))) int qstart_lds[BMQ];
   __shared__ int red_lds[4];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
   const int group = a.q_heads / a.kv_heads;
 

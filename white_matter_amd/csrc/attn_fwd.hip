@@ -33,18 +33,18 @@ constexpr int kFwdBN = 64;   // keys per tile
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a) {
   constexpr int BM = kFwdBM, BN = kFwdBN;
-  constexpr int KLD = D + 8;  // K tile row stride (elements)
-  constexpr int VLD = BN + 8; // V^T tile row stride (elements)
+  constexpr int KLD = D + 8;     // K tile row stride (elements): per-row 16-byte operand reads
+  constexpr int VLD = tr_ld(D);  // V tile row stride (elements): transpose reads
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
   constexpr int DB = D / 32;  // 32-row blocks of O^T
 
   __shared__ __attribute__((aligned(16))) bf16 k_lds[BN * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 vt_lds[D * VLD];
+  __shared__ __attribute__((aligned(16))) bf16 v_lds[BN * VLD];
   __shared__ int kseg_lds[BN];
   __shared__ int kqend_lds[BN];
   __shared__ int red_lds[4];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
 
   // ---- resolve the problem this workgroup works on ----
@@ -103,6 +103,16 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
     v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
     kt_begin_main = v < 0 ? 0 : v / BN;
   }
+  // document of this wave's rows when they all share one (ids are sorted)
+  int qseg_w = 0, qstart_w = 0;
+  bool q_uniform = false;
+  if constexpr (MODE == kDoc) {
+    qseg_w = __builtin_amdgcn_readfirstlane(qseg_i);
+    q_uniform = __all(!valid_q || qseg_i == qseg_w);
+    int v = valid_q ? qstart_i : INT_MIN;
+    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    qstart_w = __builtin_amdgcn_readfirstlane(v);  // largest document start of the wave's rows
+  }
 
   // ---- key tile range: tile 0 stays when it holds the shared dummy ----
   int kt_end = (lim_max_wg + 1 + BN - 1) / BN;
@@ -120,11 +130,38 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
     pb.key_loc(ok ? j : 0, kb, kt);
     return row_at(base, st, kb, hk, kt);
   };
+  // Affine key rows (dense rows, or a varlen segment whose keys 1.. are
+  // consecutive slots of one row): slot(j) = first + j for j >= 1 and key 0
+  // at slot0, read from a per-workgroup slice base.
+  const bool affine = MODE != kVarlen || (a.segment_layout & kKeysConsecutive);
+  int kb0 = b, kslot0 = 0, kfirst = 0;
+  if (nk > 0) {
+    pb.key_loc(0, kb0, kslot0);
+    if (nk > 1) {
+      int kb1, kslot1;
+      pb.key_loc(1, kb1, kslot1);
+      kfirst = kslot1 - 1;
+    } else {
+      kfirst = kslot0;
+    }
+  }
+  const bf16* kslice = row_at(a.k, a.k_stride, kb0, hk, 0);
+  const bf16* vslice = row_at(a.v, a.v_stride, kb0, hk, 0);
+  const int64_t kst = a.k_stride[2], vst = a.v_stride[2];
+  // a tile whose rows are all in range and inside the workgroup's reach
+  auto tile_full = [&](int n0) {
+    return affine && !(MODE == kDense && a.key_mask) && n0 + BN <= nk && n0 + BN - 1 <= lim_max_wg && n0 > 0;
+  };
 
   PairTile<BN, D> ktile, vtile;
   auto load_tile = [&](int n0) {
-    ktile.load(tid, [&](int r, bool& ok) { return key_ptr(a.k, a.k_stride, n0 + r, ok); });
-    vtile.load(tid, [&](int r, bool& ok) { return key_ptr(a.v, a.v_stride, n0 + r, ok); });
+    if (tile_full(n0)) {
+      ktile.load(tid, [&](int r, bool& ok) { ok = true; return kslice + (int64_t)(kfirst + n0 + r) * kst; });
+      vtile.load(tid, [&](int r, bool& ok) { ok = true; return vslice + (int64_t)(kfirst + n0 + r) * vst; });
+    } else {
+      ktile.load(tid, [&](int r, bool& ok) { return key_ptr(a.k, a.k_stride, n0 + r, ok); });
+      vtile.load(tid, [&](int r, bool& ok) { return key_ptr(a.v, a.v_stride, n0 + r, ok); });
+    }
   };
 
   f32x16 oacc[DB];
@@ -133,12 +170,79 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
   float m_run = kNegInf, l_run = 0.f;
   const float sl2 = a.softmax_scale * kLog2e;  // > 0 (checked on the host)
 
+  // One key tile of this wave's online softmax and PV product.
+  auto tile_step = [&](int n0, bool masked) {
+    f32x16 sacc[BN / 32];
+#pragma unroll
+    for (int nb = 0; nb < BN / 32; ++nb) {
+      sacc[nb] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s)
+        sacc[nb] = mfma32(lds_row_operand(k_lds, KLD, nb * 32 + col, s, half), qf[s], sacc[nb]);
+    }
+
+    if (masked) {
+      // keeps this block a real (wave-uniform) branch instead of selects
+      __asm__ volatile("");
+#pragma unroll
+      for (int nb = 0; nb < BN / 32; ++nb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int jl = nb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const int j = n0 + jl;
+          bool keep = (j <= lim_i) || (slot0 && j == 0);
+          if constexpr (MODE == kDense) {
+            if (a.key_mask) keep = keep && kseg_lds[jl] != 0;
+          }
+          if constexpr (MODE == kDoc) {
+            const int ksg = kseg_lds[jl];
+            keep = keep && j < nk && ((ksg == qseg_i && j >= qstart_i) || ksg == -1) && (i < kqend_lds[jl]);
+          }
+          sacc[nb][r] = keep ? sacc[nb][r] : kNegInf;
+        }
+      }
+    }
+    float rmax = kNegInf;
+#pragma unroll
+    for (int nb = 0; nb < BN / 32; ++nb)
+#pragma unroll
+      for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, sacc[nb][r]);
+    rmax = max_halves(rmax);
+    const float m_new = fmaxf(m_run, rmax * sl2);
+    const float m_use = fmaxf(m_new, kMaxFloor);
+    float rsum = 0.f;
+#pragma unroll
+    for (int nb = 0; nb < BN / 32; ++nb) {
+#pragma unroll
+      for (int r = 0; r < 16; ++r) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[nb][r], sl2, -m_use));
+        sacc[nb][r] = p;
+        rsum += p;
+      }
+    }
+    rsum = sum_halves(rsum);
+    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
+    l_run = l_run * alpha + rsum;
+    m_run = m_new;
+    if (__any(alpha != 1.f)) {
+#pragma unroll
+      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
+    }
+
+#pragma unroll
+    for (int s = 0; s < BN / 16; ++s) {
+      const bf16x8 pb = acc_kperm_operand(sacc[s >> 1], s);
+#pragma unroll
+      for (int d = 0; d < DB; ++d) oacc[d] = mfma32(lds_tr_operand(v_lds, VLD, d * 32, s, lane), pb, oacc[d]);
+    }
+  };
+
   if (ntiles > 0) load_tile(tile_of(0) * BN);
   for (int it = 0; it < ntiles; ++it) {
     const int n0 = tile_of(it) * BN;
     __syncthreads();
     ktile.store_rows(tid, k_lds, KLD);
-    vtile.store_cols(tid, vt_lds, VLD);
+    vtile.store_rows(tid, v_lds, VLD);
     if constexpr (MODE == kDoc) {
       if (tid < BN) {
         const int j = n0 + tid;
@@ -157,72 +261,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
     const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
     if (!wave_sees) continue;
 
-    f32x16 sacc[BN / 32];
-#pragma unroll
-    for (int nb = 0; nb < BN / 32; ++nb) {
-      sacc[nb] = f32x16{};
-#pragma unroll
-      for (int s = 0; s < KS; ++s)
-        sacc[nb] = mfma32(lds_row_operand(k_lds, KLD, nb * 32 + col, s, half), qf[s], sacc[nb]);
+    // Per-element masks are needed on the causal diagonal, at document
+    // boundaries and under a key mask; the wave decides uniformly.
+    bool masked = !((n0 + BN - 1 <= lim_min_wave) && (n0 + BN <= nk));
+    if constexpr (MODE == kDense) masked = masked || a.key_mask != nullptr;
+    if constexpr (MODE == kDoc) {
+      // a tile is document-interior for this wave when all 32 query ids and
+      // all 64 key ids equal one id: the document rule then keeps every pair
+      // (with n0 >= every row's document start and every key's query end past
+      // the wave's last row, all three parts of the document rule hold)
+      const int i_last = min(wave_first + 31, nq - 1);
+      masked = masked || !(q_uniform && n0 >= qstart_w && __all(kseg_lds[lane] == qseg_w && kqend_lds[lane] > i_last));
     }
-
-    const bool full = (MODE != kDoc) && !(MODE == kDense && a.key_mask) && (n0 + BN - 1 <= lim_min_wave) &&
-                      (n0 + BN <= nk);
-    float rmax = kNegInf;
-    if (full) {
-#pragma unroll
-      for (int nb = 0; nb < BN / 32; ++nb)
-#pragma unroll
-        for (int r = 0; r < 16; ++r) rmax = fmaxf(rmax, sacc[nb][r]);
-    } else {
-#pragma unroll
-      for (int nb = 0; nb < BN / 32; ++nb) {
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int jl = nb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const int j = n0 + jl;
-          bool keep = (j <= lim_i) || (slot0 && j == 0);
-          if constexpr (MODE == kDense) {
-            if (a.key_mask) keep = keep && kseg_lds[jl] != 0;
-          }
-          if constexpr (MODE == kDoc) {
-            const int ksg = kseg_lds[jl];
-            keep = keep && j < nk && ((ksg == qseg_i && j >= qstart_i) || ksg == -1) && (i < kqend_lds[jl]);
-          }
-          const float x = keep ? sacc[nb][r] : kNegInf;
-          sacc[nb][r] = x;
-          rmax = fmaxf(rmax, x);
-        }
-      }
-    }
-    rmax = fmaxf(rmax, xor32(rmax));
-    const float m_new = fmaxf(m_run, rmax * sl2);
-    const float m_use = fmaxf(m_new, kMaxFloor);
-    float rsum = 0.f;
-#pragma unroll
-    for (int nb = 0; nb < BN / 32; ++nb) {
-#pragma unroll
-      for (int r = 0; r < 16; ++r) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[nb][r], sl2, -m_use));
-        sacc[nb][r] = p;
-        rsum += p;
-      }
-    }
-    rsum += xor32(rsum);
-    const float alpha = __builtin_amdgcn_exp2f(m_run - m_use);
-    l_run = l_run * alpha + rsum;
-    m_run = m_new;
-    if (__any(alpha != 1.f)) {
-#pragma unroll
-      for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
-    }
-
-#pragma unroll
-    for (int s = 0; s < BN / 16; ++s) {
-      const bf16x8 pb = acc_kperm_operand(sacc[s >> 1], s);
-#pragma unroll
-      for (int d = 0; d < DB; ++d) oacc[d] = mfma32(lds_kperm_operand(vt_lds, VLD, d * 32 + col, s, half), pb, oacc[d]);
-    }
+    tile_step(n0, masked);
   }
 
   if (!valid_q) return;

@@ -56,8 +56,19 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_b
 __device__ __forceinline__ u32x4 load16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void store8(bf16* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
 
-// Swap values between lane l and lane l ^ 32 (the two halves of a wave).
-__device__ __forceinline__ float xor32(float x) { return __shfl_xor(x, 32); }
+// Reductions across the two halves of a wave (lane l with lane l ^ 32),
+// with v_permlane32_swap: the two results hold x[l] and x[l ^ 32] in some order.
+__device__ __forceinline__ float max_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float sum_halves(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Wave index as a scalar, so that values derived from it stay wave-uniform.
+__device__ __forceinline__ int wave_id() { return __builtin_amdgcn_readfirstlane(threadIdx.x >> 6); }
 
 // Row-addressing of one operand: dense (b fixed, row t) or varlen (flat index).
 struct RowSource {
@@ -226,5 +237,43 @@ __device__ __forceinline__ void store_acc_row(bf16* row, const f32x16 (&acc)[DB]
     }
   }
 }
+
+}  // namespace wmx
+
+namespace wmx {
+
+// ds_read_b64_tr_b16 (gfx950): within each group of 16 lanes, lane li
+// receives element li % 4 of the 8-byte chunks addressed by lanes li / 4 + 4k,
+// k = 0..3 (checked on the device). If lane s of a group addresses
+// t[(n0 + s / 4) * ld + d0 + 4 * (s % 4)], lane li receives
+// t[(n0 + k) * ld + d0 + li] for k = 0..3: four consecutive rows of one column
+// of a row-major tile, which is half of an MFMA operand whose contraction runs
+// over the tile's rows.
+__device__ __forceinline__ u32x2 lds_read_tr4(const bf16* p) {
+  typedef short i16x4 __attribute__((ext_vector_type(4)));
+  typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
+  const i16x4 v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((lds_i16x4*)(p));
+  return __builtin_bit_cast(u32x2, v);
+}
+
+// MFMA operand (row index = lane % 32 of a 32-row block starting at column
+// c0 of a row-major LDS tile t[n][c], contraction over the tile rows n in the
+// accumulator k-order of k-step s): lane half h receives rows
+// {16s + 4h + [0,4)} and {16s + 8 + 4h + [0,4)} of column c0 + lane % 32.
+__device__ __forceinline__ bf16x8 lds_tr_operand(const bf16* t, int ld, int c0, int s, int lane) {
+  const int li = lane & 15, g = lane >> 4;  // 16-lane group
+  const int h = g >> 1;
+  const int col = c0 + 16 * (g & 1) + 4 * (li & 3);
+  const int row = 16 * s + 4 * h + (li >> 2);
+  const u32x2 lo = lds_read_tr4(t + row * ld + col);
+  const u32x2 hi = lds_read_tr4(t + (row + 8) * ld + col);
+  const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
+  return as_bf16x8(v);
+}
+
+// Row stride (elements) of a row-major tile read with lds_tr_operand: the 32
+// lanes of one LDS pass read 4 rows x 16 dwords, so rows sit 16 (mod 64)
+// dwords apart.
+constexpr int tr_ld(int d) { return ((d / 2) % 64 == 16 || (d / 2) % 64 == 48) ? d : tr_ld(d + 8); }
 
 }  // namespace wmx

@@ -1,21 +1,21 @@
 // Flash-style attention forward for gfx950 (CDNA4), bf16 in, fp32 accumulate.
 //
-// One workgroup = 4 wave64s = 128 query rows of one (batch or segment,
-// query head); each wave owns 32 query rows. Key/value tiles of 64 rows are
-// staged through registers into LDS (K row-major, V transposed and
-// swizzled) and shared by the 4 waves; the next tile's global loads are in
-// flight while the current tile is computed.
+// One workgroup = 4 wave64s = 128 query rows of one (batch row or varlen
+// segment, query head); each wave owns 32 query rows. Key/value tiles of 64
+// rows go from global memory straight into double-buffered LDS (direct-to-LDS
+// loads, no staging registers): the next tile streams in while the current
+// one is computed. Rows outside the problem or past the workgroup's reach
+// arrive as zeros, so NaN in unused cache capacity cannot leak.
 //
 // Each wave computes S^T = K Q^T so that a lane owns one query column: the
 // softmax row statistics are per-lane scalars plus one exchange with
 // lane ^ 32, and the output accumulator O^T = V^T P^T is rescaled by a
 // per-lane factor (skipped for the whole wave when no row maximum moved).
-// P never leaves registers (see the k-order note in wmx_device.h). Masks
-// (strided causal bound, per-row offset/limit, key mask, documents, varlen
-// segments) are evaluated only on tiles that can contain a masked pair;
-// tiles nobody in the workgroup can see are never loaded, and rows beyond
-// the workgroup's reach are zero-filled so NaN in unused cache capacity
-// cannot leak.
+// P never leaves registers (see the k-order note in wmx_device.h); V^T is
+// read from the row-major V tile with transpose reads. Masks (strided causal
+// bound, per-row offset/limit, key mask, documents, varlen segments) are
+// evaluated only on tiles that can contain a masked pair; tiles nobody in the
+// workgroup can see are never loaded.
 //
 // Semantics follow the reference's portable path
 // (src/white_matter/ops/cyclic_attention/reference.py:10-42,
@@ -23,6 +23,8 @@
 // accelerated path's numerics contract (exp2 online softmax with the
 // rescale-by-exactly-one guard, natural-log LSE, zero rows for empty
 // visibility; _tilelang/forward.py:99-131).
+#include <type_traits>
+
 #include "attn_tiles.h"
 
 namespace wmx {
@@ -33,15 +35,19 @@ constexpr int kFwdBN = 64;   // keys per tile
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a) {
   constexpr int BM = kFwdBM, BN = kFwdBN;
-  constexpr int KLD = D + 8;     // K tile row stride (elements): per-row 16-byte operand reads
-  constexpr int VLD = tr_ld(D);  // V tile row stride (elements): transpose reads
+  static_assert(BN == kTileRows, "one LDS tile per key tile");
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
   constexpr int DB = D / 32;  // 32-row blocks of O^T
 
-  __shared__ __attribute__((aligned(16))) bf16 k_lds[BN * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 v_lds[BN * VLD];
-  __shared__ int kseg_lds[BN];
-  __shared__ int kqend_lds[BN];
+  // Two buffers indexed by compile-time constants only (the tile loop is
+  // unrolled by two): the compiler then sees that loads streaming into one
+  // buffer never alias reads of the other and does not wait for the prefetch
+  // before computing, and buffer offsets fold into instruction immediates.
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 v_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 v_lds1[kTileElems];
+  __shared__ int meta_lds[2][2][BN];  // per buffer: key ids (or key mask), key query ends
   __shared__ int red_lds[4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -101,7 +107,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
     if (lane == 0) red_lds[wave] = v;
     __syncthreads();
     v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
-    kt_begin_main = v < 0 ? 0 : v / BN;
+    kt_begin_main = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v / BN);  // uniform: keeps the tile loop scalar
   }
   // document of this wave's rows when they all share one (ids are sorted)
   int qseg_w = 0, qstart_w = 0;
@@ -122,45 +128,26 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
   const int ntiles = gap ? 1 + max(0, kt_end - first_main) : kt_end;
   auto tile_of = [&](int it) { return gap ? (it == 0 ? 0 : first_main + it - 1) : it; };
 
-  // key row j of this problem as a global pointer into K (or V)
-  auto key_ptr = [&](const void* base, const int64_t* st, int j, bool& ok) -> const bf16* {
-    ok = j < nk && (j <= lim_max_wg || (slot0 && j == 0));
-    if (MODE == kDense && a.key_mask) ok = ok && a.key_mask[(int64_t)b * a.key_mask_stride + min(j, nk - 1)] != 0;
-    int kb, kt;
-    pb.key_loc(ok ? j : 0, kb, kt);
-    return row_at(base, st, kb, hk, kt);
-  };
-  // Affine key rows (dense rows, or a varlen segment whose keys 1.. are
-  // consecutive slots of one row): slot(j) = first + j for j >= 1 and key 0
-  // at slot0, read from a per-workgroup slice base.
-  const bool affine = MODE != kVarlen || (a.segment_layout & kKeysConsecutive);
-  int kb0 = b, kslot0 = 0, kfirst = 0;
-  if (nk > 0) {
-    pb.key_loc(0, kb0, kslot0);
-    if (nk > 1) {
-      int kb1, kslot1;
-      pb.key_loc(1, kb1, kslot1);
-      kfirst = kslot1 - 1;
-    } else {
-      kfirst = kslot0;
+  // ---- key/value tiles: keys [0, reach) are visible to some row of the workgroup ----
+  TileDMA<D> dma;
+  dma.init(wave, lane);
+  KeyTiles<MODE, D> keys;
+  keys.init(a, pb, hk, slot0 ? max(lim_max_wg + 1, 1) : lim_max_wg + 1, dma);
+  // masking metadata of a key tile, loaded into a register while the tile
+  // streams in and stored to LDS once the previous buffer is free
+  auto load_meta = [&](int n0) -> int {
+    const int j = n0 + (tid & 63);
+    if constexpr (MODE == kDoc) {
+      if (tid < 64) return j < nk ? a.k_seg[(int64_t)b * a.kv_len + j] : INT_MIN;
+      if (tid < 128) return j < nk ? a.k_qend[(int64_t)b * a.kv_len + j] : 0;
+    } else if constexpr (MODE == kDense) {
+      if (a.key_mask && tid < 64) return j < nk ? (int)a.key_mask[(int64_t)b * a.key_mask_stride + j] : 0;
     }
-  }
-  const bf16* kslice = row_at(a.k, a.k_stride, kb0, hk, 0);
-  const bf16* vslice = row_at(a.v, a.v_stride, kb0, hk, 0);
-  const int64_t kst = a.k_stride[2], vst = a.v_stride[2];
-  // a tile whose rows are all in range and inside the workgroup's reach
-  auto tile_full = [&](int n0) {
-    return affine && !(MODE == kDense && a.key_mask) && n0 + BN <= nk && n0 + BN - 1 <= lim_max_wg && n0 > 0;
+    return 0;
   };
-
-  PairTile<BN, D> ktile, vtile;
-  auto load_tile = [&](int n0) {
-    if (tile_full(n0)) {
-      ktile.load(tid, [&](int r, bool& ok) { ok = true; return kslice + (int64_t)(kfirst + n0 + r) * kst; });
-      vtile.load(tid, [&](int r, bool& ok) { ok = true; return vslice + (int64_t)(kfirst + n0 + r) * vst; });
-    } else {
-      ktile.load(tid, [&](int r, bool& ok) { return key_ptr(a.k, a.k_stride, n0 + r, ok); });
-      vtile.load(tid, [&](int r, bool& ok) { return key_ptr(a.v, a.v_stride, n0 + r, ok); });
+  auto store_meta = [&](int buf, int v) {
+    if (MODE == kDoc || (MODE == kDense && a.key_mask)) {
+      if (tid < 128) meta_lds[buf][tid >> 6][tid & 63] = v;
     }
   };
 
@@ -171,14 +158,19 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
   const float sl2 = a.softmax_scale * kLog2e;  // > 0 (checked on the host)
 
   // One key tile of this wave's online softmax and PV product.
-  auto tile_step = [&](int n0, bool masked) {
+  RowReads<KS> krd;
+  krd.init(col, half);
+  TrReads<DB> vrd;
+  vrd.init(lane);
+  auto tile_step = [&](int n0, int buf, const bf16* kt, const bf16* vt, bool masked) __attribute__((always_inline)) {
+    krd.refresh();
+    vrd.refresh();
     f32x16 sacc[BN / 32];
 #pragma unroll
     for (int nb = 0; nb < BN / 32; ++nb) {
       sacc[nb] = f32x16{};
 #pragma unroll
-      for (int s = 0; s < KS; ++s)
-        sacc[nb] = mfma32(lds_row_operand(k_lds, KLD, nb * 32 + col, s, half), qf[s], sacc[nb]);
+      for (int s = 0; s < KS; ++s) sacc[nb] = mfma32(krd.get(kt, s, nb), qf[s], sacc[nb]);
     }
 
     if (masked) {
@@ -190,13 +182,14 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
         for (int r = 0; r < 16; ++r) {
           const int jl = nb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
           const int j = n0 + jl;
-          bool keep = (j <= lim_i) || (slot0 && j == 0);
+          // bitwise forms: every term is evaluated, no per-lane branches
+          bool keep = (j <= lim_i) | (slot0 & (j == 0));
           if constexpr (MODE == kDense) {
-            if (a.key_mask) keep = keep && kseg_lds[jl] != 0;
+            if (a.key_mask) keep = keep & (meta_lds[buf][0][jl] != 0);
           }
           if constexpr (MODE == kDoc) {
-            const int ksg = kseg_lds[jl];
-            keep = keep && j < nk && ((ksg == qseg_i && j >= qstart_i) || ksg == -1) && (i < kqend_lds[jl]);
+            const int ksg = meta_lds[buf][0][jl], kqe = meta_lds[buf][1][jl];
+            keep = keep & (j < nk) & (((ksg == qseg_i) & (j >= qstart_i)) | (ksg == -1)) & (i < kqe);
           }
           sacc[nb][r] = keep ? sacc[nb][r] : kNegInf;
         }
@@ -233,47 +226,56 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
     for (int s = 0; s < BN / 16; ++s) {
       const bf16x8 pb = acc_kperm_operand(sacc[s >> 1], s);
 #pragma unroll
-      for (int d = 0; d < DB; ++d) oacc[d] = mfma32(lds_tr_operand(v_lds, VLD, d * 32, s, lane), pb, oacc[d]);
+      for (int d = 0; d < DB; ++d) oacc[d] = mfma32(vrd.get(vt, d, s), pb, oacc[d]);
     }
   };
 
-  if (ntiles > 0) load_tile(tile_of(0) * BN);
-  for (int it = 0; it < ntiles; ++it) {
+  // One iteration of the tile loop on buffer B (tile `it` resident there),
+  // prefetching tile it + 1 into the other buffer.
+  auto iteration = [&](auto bufc, int it) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    bf16* const kcur = B ? k_lds1 : k_lds0;
+    bf16* const vcur = B ? v_lds1 : v_lds0;
+    bf16* const knext = B ? k_lds0 : k_lds1;
+    bf16* const vnext = B ? v_lds0 : v_lds1;
     const int n0 = tile_of(it) * BN;
-    __syncthreads();
-    ktile.store_rows(tid, k_lds, KLD);
-    vtile.store_rows(tid, v_lds, VLD);
-    if constexpr (MODE == kDoc) {
-      if (tid < BN) {
-        const int j = n0 + tid;
-        kseg_lds[tid] = j < nk ? a.k_seg[(int64_t)b * a.kv_len + j] : INT_MIN;
-        kqend_lds[tid] = j < nk ? a.k_qend[(int64_t)b * a.kv_len + j] : 0;
-      }
-    } else if constexpr (MODE == kDense) {
-      if (a.key_mask && tid < BN) {
-        const int j = n0 + tid;
-        kseg_lds[tid] = j < nk ? (int)a.key_mask[(int64_t)b * a.key_mask_stride + j] : 0;
-      }
+    // tile `it` (and its metadata) has landed; every wave is done with the other buffer
+    dma_barrier();
+    const bool more = it + 1 < ntiles;
+    int next_meta = 0;
+    if (more) {
+      const int n1 = tile_of(it + 1) * BN;
+      keys.issue(a, pb, dma, n1, knext, vnext, wave);
+      next_meta = load_meta(n1);
     }
-    __syncthreads();
-    if (it + 1 < ntiles) load_tile(tile_of(it + 1) * BN);
-
     const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
-    if (!wave_sees) continue;
-
-    // Per-element masks are needed on the causal diagonal, at document
-    // boundaries and under a key mask; the wave decides uniformly.
-    bool masked = !((n0 + BN - 1 <= lim_min_wave) && (n0 + BN <= nk));
-    if constexpr (MODE == kDense) masked = masked || a.key_mask != nullptr;
-    if constexpr (MODE == kDoc) {
-      // a tile is document-interior for this wave when all 32 query ids and
-      // all 64 key ids equal one id: the document rule then keeps every pair
-      // (with n0 >= every row's document start and every key's query end past
-      // the wave's last row, all three parts of the document rule hold)
-      const int i_last = min(wave_first + 31, nq - 1);
-      masked = masked || !(q_uniform && n0 >= qstart_w && __all(kseg_lds[lane] == qseg_w && kqend_lds[lane] > i_last));
+    if (wave_sees) {
+      // Per-element masks are needed on the causal diagonal, at document
+      // boundaries and under a key mask; the wave decides uniformly.
+      bool masked = !((n0 + BN - 1 <= lim_min_wave) && (n0 + BN <= nk));
+      if constexpr (MODE == kDense) masked = masked || a.key_mask != nullptr;
+      if constexpr (MODE == kDoc) {
+        // a tile is document-interior for this wave when all 32 query ids and
+        // all 64 key ids equal one id: the document rule then keeps every pair
+        // (with n0 >= every row's document start and every key's query end
+        // past the wave's last row, all three parts of the document rule hold)
+        const int i_last = min(wave_first + 31, nq - 1);
+        masked = masked || !(q_uniform && n0 >= qstart_w &&
+                             __all(meta_lds[B][0][lane] == qseg_w && meta_lds[B][1][lane] > i_last));
+      }
+      tile_step(n0, B, kcur, vcur, masked);
     }
-    tile_step(n0, masked);
+    if (more) store_meta(B ^ 1, next_meta);
+  };
+
+  if (ntiles > 0) {
+    const int n0 = tile_of(0) * BN;
+    keys.issue(a, pb, dma, n0, k_lds0, v_lds0, wave);
+    store_meta(0, load_meta(n0));
+  }
+  for (int it = 0; it < ntiles; it += 2) {
+    iteration(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntiles) iteration(std::integral_constant<int, 1>{}, it + 1);
   }
 
   if (!valid_q) return;

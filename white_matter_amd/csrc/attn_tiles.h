@@ -10,6 +10,7 @@
 
 #include <climits>
 
+#include "lds_tiles.h"
 #include "wmx_kernels.h"
 
 namespace wmx {
@@ -94,5 +95,79 @@ struct Problem {
 __device__ __forceinline__ const bf16* row_at(const void* base, const int64_t* st, int b, int h, int t) {
   return (const bf16*)base + (int64_t)b * st[0] + (int64_t)h * st[1] + (int64_t)t * st[2];
 }
+
+// The key (and value) rows of one problem and kv head as 64-row LDS tiles.
+// Keys [0, reach) are loaded, later rows read as zeros. Where the keys sit at
+// a fixed stride in one row (dense rows; a varlen segment with consecutive
+// slots from key 1 on) a tile is a strided load from a per-tile base;
+// otherwise, and under a key mask (masked-out slots may hold anything), each
+// row is located and gathered.
+template <int MODE, int D>
+struct KeyTiles {
+  const bf16 *kslice, *vslice;  // slot 0 of the keys' row, kv head hk
+  int64_t kst, vst;             // slot strides (elements)
+  int kfirst;                   // strided: key j at slot kfirst + j
+  int reach;
+  bool strided;
+  unsigned koff[4], voff[4];
+  int b, hk, nk;
+
+  __device__ __forceinline__ void init(const wmx_attn_args& a, const Problem<MODE>& pb, int hk_, int reach_,
+                                       const TileDMA<D>& dma) {
+    b = pb.b;
+    hk = hk_;
+    nk = pb.nk;
+    reach = reach_;
+    int kb0 = b, kslot0 = 0;
+    kfirst = 0;
+    if constexpr (MODE == kVarlen) {
+      if (nk > 0) {
+        pb.key_loc(0, kb0, kslot0);
+        if (nk > 1) {
+          int kb1, kslot1;
+          pb.key_loc(1, kb1, kslot1);
+          kfirst = kslot1 - 1;
+        }
+      }
+    }
+    kslice = row_at(a.k, a.k_stride, kb0, hk, 0);
+    vslice = row_at(a.v, a.v_stride, kb0, hk, 0);
+    kst = a.k_stride[2];
+    vst = a.v_stride[2];
+    const bool layout_ok = MODE != kVarlen || (a.segment_layout & kKeysConsecutive);
+    const bool mask_free = !(MODE == kDense && a.key_mask);
+    // rows must not overlap (zero rows past the buffer end) and 64 rows must
+    // fit 32-bit offsets
+    const bool stride_ok = kst >= D && vst >= D && kst < (1 << 23) && vst < (1 << 23);
+    strided = layout_ok && mask_free && stride_ok;
+    dma.strided_offsets(strided ? (int)kst * 2 : 0, koff);
+    dma.strided_offsets(strided ? (int)vst * 2 : 0, voff);
+  }
+
+  template <class Args>
+  __device__ __forceinline__ void issue(const Args& a, const Problem<MODE>& pb, const TileDMA<D>& dma, int n0,
+                                        bf16* ktile, bf16* vtile, int wave) const {
+    if (strided && (MODE != kVarlen || n0 > 0)) {
+      const int nvalid = min(max(reach - n0, 0), kTileRows);
+      const int64_t slot = (int64_t)kfirst + n0;
+      const rsrc_t rk = make_rsrc(kslice + slot * kst, nvalid * (int)kst * 2);
+      const rsrc_t rv = make_rsrc(vslice + slot * vst, nvalid * (int)vst * 2);
+      TileDMA<D>::issue_strided(rk, ktile, wave, koff);
+      TileDMA<D>::issue_strided(rv, vtile, wave, voff);
+    } else {
+      dma.issue_gathered2(ktile, vtile, wave, [&](int tr, bool& ok, const bf16*& kp, const bf16*& vp) {
+        const int j = n0 + tr;
+        ok = j < reach;
+        if constexpr (MODE == kDense) {
+          if (a.key_mask) ok = ok && a.key_mask[(int64_t)b * a.key_mask_stride + min(j, nk - 1)] != 0;
+        }
+        int kb, kt;
+        pb.key_loc(ok ? j : 0, kb, kt);
+        kp = row_at(a.k, a.k_stride, kb, hk, kt);
+        vp = row_at(a.v, a.v_stride, kb, hk, kt);
+      });
+    }
+  }
+};
 
 }  // namespace wmx

@@ -1,0 +1,193 @@
+// 64-row bf16 tiles in LDS, filled by direct-to-LDS loads (16 bytes per lane
+// from global memory straight into LDS, no staging registers, no ds_write).
+//
+// Layout: a tile row holds 16 chunks of 16 bytes (up to 128 bf16; chunks past
+// head_dim/8 are padding that no reader touches). Chunk c of row r is stored
+// at chunk c ^ swz(r), swz(r) = 4 (r % 4) + (r / 4) % 4. With 64 banks of
+// 4 bytes this keeps both read patterns of the kernels free of bank conflicts:
+//   row operands - 16 lanes read 16 B of 16 different rows, same chunk;
+//   tr operands  - 32 lanes read 8 B of 4 consecutive rows x 4 chunks
+//                  (ds_read_b64_tr_b16, see wmx_device.h).
+// One wave instruction fills 1 KB = 4 rows: lane l writes LDS bytes
+// base + 16 l, i.e. physical chunk l % 16 of row l / 16, so the lane loads
+// the logical chunk (l % 16) ^ swz(row).
+//
+// Two ways to fill a tile:
+//   strided - rows at a fixed byte stride from a per-tile base, through a
+//             buffer resource whose size ends at the last row to load: the
+//             rows past it (outside the problem or past every reader's
+//             reach) read as zeros, so NaN in unused cache capacity never
+//             reaches the products;
+//   gathered - one global address per row, zeros (from a zero chunk) for a
+//             row that must not be read.
+#pragma once
+
+#include "wmx_device.h"
+
+namespace wmx {
+
+constexpr int kTileRows = 64;
+constexpr int kRowElems = 128;
+constexpr int kTileElems = kTileRows * kRowElems;  // 16 KB
+constexpr unsigned kOutOfRange = 0x80000000u;      // past every tile buffer's size
+
+__device__ __forceinline__ int tile_swz(int r) { return 4 * (r & 3) + ((r >> 2) & 3); }
+__device__ __forceinline__ int tile_elem(int r, int c) { return r * kRowElems + 8 * (c ^ tile_swz(r)); }
+
+// Row operand of k-step s (k = head_dim): row r, elements 16 s + 8 half .. + 8.
+__device__ __forceinline__ bf16x8 tile_row_operand(const bf16* t, int r, int s, int half) {
+  return as_bf16x8(*reinterpret_cast<const u32x4*>(t + tile_elem(r, 2 * s + half)));
+}
+
+// Transposed operand (contraction over tile rows, accumulator k-order of
+// k-step s) for the 32 columns c0 .. c0 + 31, as lds_tr_operand.
+__device__ __forceinline__ bf16x8 tile_tr_operand(const bf16* t, int c0, int s, int lane) {
+  const int li = lane & 15, g = lane >> 4;
+  const int col = c0 + 16 * (g & 1) + 4 * (li & 3);
+  const int row = 16 * s + 4 * (g >> 1) + (li >> 2);
+  const int within = col & 7;
+  const u32x2 lo = lds_read_tr4(t + tile_elem(row, col >> 3) + within);
+  const u32x2 hi = lds_read_tr4(t + tile_elem(row + 8, col >> 3) + within);
+  const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
+  return as_bf16x8(v);
+}
+
+// Keeps a value in a register as if it changed here: derived addresses are
+// then formed at their use (register + immediate) instead of being hoisted
+// out of the loop as one register per (buffer, k-step).
+template <class T>
+__device__ __forceinline__ void opaque(T& x) {
+  __asm__ volatile("" : "+v"(x));
+}
+
+// This lane's byte offsets for the row operands of a 32-row block: row r
+// (= lane % 32), k-steps s < KS. Row blocks 32 rows apart share the swizzle,
+// so block nb adds the immediate 8192 nb.
+template <int KS>
+struct RowReads {
+  int off[KS];
+  __device__ __forceinline__ void init(int r, int half) {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) off[s] = 2 * tile_elem(r, 2 * s + half);
+  }
+  __device__ __forceinline__ void refresh() {
+#pragma unroll
+    for (int s = 0; s < KS; ++s) opaque(off[s]);
+  }
+  __device__ __forceinline__ bf16x8 get(const bf16* t, int s, int nb) const {
+    return as_bf16x8(*reinterpret_cast<const u32x4*>((const char*)t + off[s] + 8192 * nb));
+  }
+};
+
+// This lane's byte offsets for transposed operands (see tile_tr_operand) of
+// the 32-column blocks d < DB; k-step s adds 16 rows, the immediate 4096 s.
+template <int DB>
+struct TrReads {
+  int lo[DB], hi[DB];
+  __device__ __forceinline__ void init(int lane) {
+    const int li = lane & 15, g = lane >> 4;
+    const int row = 4 * (g >> 1) + (li >> 2);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      const int c = 32 * d + 16 * (g & 1) + 4 * (li & 3);
+      lo[d] = 2 * (tile_elem(row, c >> 3) + (c & 7));
+      hi[d] = 2 * (tile_elem(row + 8, c >> 3) + (c & 7));
+    }
+  }
+  __device__ __forceinline__ void refresh() {
+#pragma unroll
+    for (int d = 0; d < DB; ++d) {
+      opaque(lo[d]);
+      opaque(hi[d]);
+    }
+  }
+  __device__ __forceinline__ bf16x8 get(const bf16* t, int d, int s) const {
+    const char* base = (const char*)t + 4096 * s;
+    const u32x2 l = lds_read_tr4((const bf16*)(base + lo[d]));
+    const u32x2 h = lds_read_tr4((const bf16*)(base + hi[d]));
+    const u32x4 v = {l[0], l[1], h[0], h[1]};
+    return as_bf16x8(v);
+  }
+};
+
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+typedef __attribute__((address_space(3))) void lds_void;
+
+// A raw byte buffer over [base, base + bytes); reads past it return zeros.
+// Both arguments must be wave-uniform; they are moved to scalar registers
+// explicitly so that the compiler never wraps a load in a per-lane loop.
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
+  const uint64_t p = (uint64_t)base;
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)p);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(p >> 32));
+  void* up = (void*)(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(up, (short)0, __builtin_amdgcn_readfirstlane(bytes), 0x00020000);
+}
+
+// Source of the zero rows of gathered tiles.
+static __device__ __attribute__((aligned(16))) const uint32_t kZeroChunk[4] = {0u, 0u, 0u, 0u};
+
+// This thread's four 16-byte slots of a 64-row tile (256 threads = 4 waves,
+// each wave filling 16 rows with 4 instructions).
+template <int D>
+struct TileDMA {
+  int row[4];      // tile row of instruction r
+  int chunk16[4];  // byte offset of the logical chunk in the row, or -1 for padding
+
+  __device__ __forceinline__ void init(int wave, int lane) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      const int tr = (wave * 4 + r) * 4 + (lane >> 4);
+      const int lc = (lane & 15) ^ tile_swz(tr);
+      row[r] = tr;
+      chunk16[r] = lc < D / 8 ? lc * 16 : -1;
+    }
+  }
+  // Per-lane byte offsets of a strided tile with row stride row_bytes
+  // (0 <= row_bytes * 64 < 2^31).
+  __device__ __forceinline__ void strided_offsets(int row_bytes, unsigned (&off)[4]) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) off[r] = chunk16[r] < 0 ? kOutOfRange : (unsigned)(row[r] * row_bytes + chunk16[r]);
+  }
+  static __device__ __forceinline__ void issue_strided(const rsrc_t& rs, bf16* tile, int wave, const unsigned (&off)[4]) {
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + (wave * 4 + r) * 512), 16, off[r], 0, 0, 0);
+  }
+  // rows(tr, ok) returns the address of tile row tr and sets ok = false for a
+  // row that must read as zeros.
+  template <class Rows>
+  __device__ __forceinline__ void issue_gathered(bf16* tile, int wave, Rows rows) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      bool ok;
+      const bf16* p = rows(row[r], ok);
+      const void* src = (ok && chunk16[r] >= 0) ? (const void*)((const char*)p + chunk16[r]) : (const void*)kZeroChunk;
+      __builtin_amdgcn_global_load_lds(src, (lds_void*)(tile + (wave * 4 + r) * 512), 16, 0, 0);
+    }
+  }
+  // Two tiles whose rows are located together: rows(tr, ok, p0, p1).
+  template <class Rows>
+  __device__ __forceinline__ void issue_gathered2(bf16* t0, bf16* t1, int wave, Rows rows) const {
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+      bool ok;
+      const bf16 *p0, *p1;
+      rows(row[r], ok, p0, p1);
+      const bool use = ok && chunk16[r] >= 0;
+      const void* s0 = use ? (const void*)((const char*)p0 + chunk16[r]) : (const void*)kZeroChunk;
+      const void* s1 = use ? (const void*)((const char*)p1 + chunk16[r]) : (const void*)kZeroChunk;
+      __builtin_amdgcn_global_load_lds(s0, (lds_void*)(t0 + (wave * 4 + r) * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(s1, (lds_void*)(t1 + (wave * 4 + r) * 512), 16, 0, 0);
+    }
+  }
+};
+
+// Wait for this wave's outstanding global loads (direct-to-LDS included),
+// then for the whole workgroup.
+__device__ __forceinline__ void dma_barrier() {
+  __builtin_amdgcn_s_waitcnt(0);
+  __syncthreads();
+}
+
+}  // namespace wmx

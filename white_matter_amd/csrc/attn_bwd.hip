@@ -19,6 +19,8 @@
 // Varlen schedules whose key rows repeat across segments (the shared dummy
 // slot, capped histories) accumulate dK/dV in fp32 workspace rows with
 // atomics and convert once at the end.
+#include <type_traits>
+
 #include "attn_tiles.h"
 
 namespace wmx {
@@ -221,19 +223,26 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
 }
 
 // ------------------------------------------------------------------ dKV ----
+// One workgroup = 128 keys of one (batch row or segment, kv head), 32 per
+// wave, held in registers. Query and output-gradient tiles of 64 rows for
+// every query head of the group stream through double-buffered LDS
+// (direct-to-LDS loads, the next tile in flight while the current one is
+// computed); each tile is read row-wise for S = Q K^T and dP = dO V^T and
+// with transpose reads for dV^T = dO^T P and dK^T = Q^T dS.
 template <int D, int MODE, bool ATOMIC>
 __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a) {
   constexpr int BNK = 128, BMQ = 64;
-  constexpr int QLD = D + 8, TLD = BMQ + 8;
+  static_assert(BMQ == kTileRows, "one LDS tile per query tile");
   constexpr int KS = D / 16, DB = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16 q_lds[BMQ * QLD];
-  __shared__ __attribute__((aligned(16))) bf16 g_lds[BMQ * QLD];
-  __shared__ __attribute__((aligned(16))) bf16 qt_lds[D * TLD];
-  __shared__ __attribute__((aligned(16))) bf16 gt_lds[D * TLD];
-  __shared__ __attribute__((aligned(16))) float lse_lds[BMQ];
-  __shared__ __attribute__((aligned(16))) float delta_lds[BMQ];
-  __shared__ __attribute__((aligned(16))) int qseg_lds[BMQ];
-  __shared__ __attribute__((aligned(16))) int qstart_lds[BMQ];
+  // two buffers as distinct arrays with static roles (the loop is unrolled
+  // by two): prefetches into one buffer are then known not to alias reads
+  // of the other, so reads never wait for the prefetch
+  __shared__ __attribute__((aligned(1024))) bf16 q_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 q_lds1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 g_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 g_lds1[kTileElems];
+  __shared__ __attribute__((aligned(16))) float stat_lds[2][2][BMQ];  // lse * log2e, delta
+  __shared__ __attribute__((aligned(16))) int qdoc_lds[2][2][BMQ];    // document id, document start
   __shared__ int red_lds[4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -269,7 +278,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
     }
   }
   // query rows that can see any key of the workgroup / of this wave
-  int m_begin = (slot0 && n0 == 0) ? 0 : pb.bound.first_row(n0, nq);
+  const int m_begin = (slot0 && n0 == 0) ? 0 : pb.bound.first_row(n0, nq);
   int m_end = nq;
   if constexpr (MODE == kDoc) {
     int v = valid_k ? kqend_n : 0;
@@ -277,7 +286,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
     if (lane == 0) red_lds[wave] = v;
     __syncthreads();
     v = max(max(red_lds[0], red_lds[1]), max(red_lds[2], red_lds[3]));
-    m_end = min(m_end, v);
+    m_end = __builtin_amdgcn_readfirstlane(min(m_end, v));  // uniform: keeps the tile loop scalar
   }
   const int wave_key0 = n0 + wave * 32;
   const bool wave_live = wave_key0 < nk;
@@ -303,96 +312,157 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
     dvacc[d] = f32x16{};
   }
   const float sl2 = a.softmax_scale * kLog2e;
-  PairTile<BMQ, D> qtile, gtile;
+
+  // ---- query tiles: (head, first row) pairs over the group's heads ----
   const int m_first = (m_begin / BMQ) * BMQ;
+  const int nqt = m_end > m_first ? (m_end - m_first + BMQ - 1) / BMQ : 0;
+  const int total = nqt * group;
+  TileDMA<D> dma;
+  dma.init(wave, lane);
+  QueryTiles<MODE, D> qrows;
+  qrows.init(a, pb, dma);
+  RowReads<KS> rrd;
+  rrd.init(col, half);
+  TrReads<DB> trd;
+  trd.init(lane);
 
-  for (int hq = hk * group; hq < (hk + 1) * group; ++hq) {
-    for (int m0 = m_first; m0 < m_end; m0 += BMQ) {
-      auto qrow_ptr = [&](const void* base, const int64_t* st, int r, bool& ok) -> const bf16* {
-        const int m = m0 + r;
-        ok = m < nq;
-        int rb, rt;
-        pb.query_loc(ok ? m : m0, rb, rt);
-        return row_at(base, st, rb, hq, rt);
-      };
-      qtile.load(tid, [&](int r, bool& ok) { return qrow_ptr(a.q, a.q_stride, r, ok); });
-      gtile.load(tid, [&](int r, bool& ok) { return qrow_ptr(a.dout, a.do_stride, r, ok); });
-      float lse_v = kPosInf, delta_v = 0.f;
-      int qseg_v = INT_MIN, qstart_v = INT_MAX;
-      if (tid < BMQ && m0 + tid < nq) {
-        int rb, rt;
-        pb.query_loc(m0 + tid, rb, rt);
-        const int64_t r = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
-        lse_v = a.lse[r] * kLog2e;
-        delta_v = a.delta[r];
-        if constexpr (MODE == kDoc) {
-          qseg_v = a.q_seg[(int64_t)b * a.q_len + m0 + tid];
-          qstart_v = a.q_start[(int64_t)b * a.q_len + m0 + tid];
-        }
+  // per-row statistics (and document metadata) of a query tile, loaded into
+  // registers while the tile streams in, stored once the other buffer is free
+  struct RowMeta {
+    float lse2, delta;
+    int seg, start;
+  };
+  auto load_meta = [&](int hq, int m0) {
+    RowMeta r{kPosInf, 0.f, INT_MIN, INT_MAX};
+    const int m = m0 + (tid & 63);
+    if (tid < BMQ && m < nq) {
+      int rb, rt;
+      pb.query_loc(m, rb, rt);
+      const int64_t idx = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
+      r.lse2 = a.lse[idx] * kLog2e;
+      r.delta = a.delta[idx];
+      if constexpr (MODE == kDoc) {
+        r.seg = a.q_seg[(int64_t)b * a.q_len + m];
+        r.start = a.q_start[(int64_t)b * a.q_len + m];
       }
-      __syncthreads();
-      qtile.store_rows(tid, q_lds, QLD);
-      qtile.store_cols(tid, qt_lds, TLD);
-      gtile.store_rows(tid, g_lds, QLD);
-      gtile.store_cols(tid, gt_lds, TLD);
-      if (tid < BMQ) {
-        lse_lds[tid] = lse_v;
-        delta_lds[tid] = delta_v;
-        qseg_lds[tid] = qseg_v;
-        qstart_lds[tid] = qstart_v;
+    }
+    return r;
+  };
+  auto store_meta = [&](auto bufc, const RowMeta& r) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    if (tid < BMQ) {
+      stat_lds[B][0][tid] = r.lse2;
+      stat_lds[B][1][tid] = r.delta;
+      if constexpr (MODE == kDoc) {
+        qdoc_lds[B][0][tid] = r.seg;
+        qdoc_lds[B][1][tid] = r.start;
       }
-      __syncthreads();
-      if (!wave_live || m0 + BMQ <= wave_m_begin) continue;
+    }
+  };
 
-      f32x16 sacc[BMQ / 32], pacc[BMQ / 32];
+  // One query tile against this wave's 32 keys.
+  auto tile_step = [&](auto bufc, int m0) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    const bf16* qt = B ? q_lds1 : q_lds0;
+    const bf16* gt = B ? g_lds1 : g_lds0;
+    rrd.refresh();
+    trd.refresh();
+    f32x16 sacc[BMQ / 32], pacc[BMQ / 32];
+#pragma unroll
+    for (int mb = 0; mb < BMQ / 32; ++mb) {
+      sacc[mb] = f32x16{};
+      pacc[mb] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        sacc[mb] = mfma32(rrd.get(qt, s, mb), kf[s], sacc[mb]);
+        pacc[mb] = mfma32(rrd.get(gt, s, mb), vf[s], pacc[mb]);
+      }
+    }
+    // every pair of the tile is visible to this wave: no per-element mask
+    const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= wave_m_begin &&
+                      m0 + BMQ <= nq && pb.bound.lim(m0) >= wave_key0 + 31;
+    if (!full) {
+      // keeps this block a real (wave-uniform) branch instead of selects
+      __asm__ volatile("");
 #pragma unroll
       for (int mb = 0; mb < BMQ / 32; ++mb) {
-        sacc[mb] = f32x16{};
-        pacc[mb] = f32x16{};
 #pragma unroll
-        for (int s = 0; s < KS; ++s) {
-          sacc[mb] = mfma32(lds_row_operand(q_lds, QLD, mb * 32 + col, s, half), kf[s], sacc[mb]);
-          pacc[mb] = mfma32(lds_row_operand(g_lds, QLD, mb * 32 + col, s, half), vf[s], pacc[mb]);
-        }
-      }
-      const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= wave_m_begin &&
-                        m0 + BMQ <= nq && pb.bound.lim(m0) >= wave_key0 + 31;
-#pragma unroll
-      for (int mb = 0; mb < BMQ / 32; ++mb) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int ml = mb * 32 + 8 * g + 4 * half;
-          const f32x4 l4 = *reinterpret_cast<const f32x4*>(&lse_lds[ml]);
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&delta_lds[ml]);
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const int r = 4 * g + e;
-            const int m = m0 + ml + e;
-            bool keep = true;
-            if (!full) {
-              keep = k_live && m < nq && ((n <= pb.bound.lim(m)) || (slot0 && n == 0));
-              if constexpr (MODE == kDoc) {
-                const int qsg = qseg_lds[ml + e];
-                keep = keep && ((qsg == kseg_n && n >= qstart_lds[ml + e]) || kseg_n == -1) && (m < kqend_n);
-              }
-            }
-            const float p = keep ? __builtin_amdgcn_exp2f(fmaf(sacc[mb][r], sl2, -l4[e])) : 0.f;
-            sacc[mb][r] = p;
-            pacc[mb][r] = p * (pacc[mb][r] - d4[e]);
+        for (int r = 0; r < 16; ++r) {
+          const int ml = mb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const int m = m0 + ml;
+          bool keep = k_live & (m < nq) & ((n <= pb.bound.lim(m)) | (slot0 & (n == 0)));
+          if constexpr (MODE == kDoc) {
+            const int qsg = qdoc_lds[B][0][ml], qst = qdoc_lds[B][1][ml];
+            keep = keep & (((qsg == kseg_n) & (n >= qst)) | (kseg_n == -1)) & (m < kqend_n);
           }
-        }
-      }
-#pragma unroll
-      for (int s = 0; s < BMQ / 16; ++s) {
-        const bf16x8 pop = acc_kperm_operand(sacc[s >> 1], s);
-        const bf16x8 dsop = acc_kperm_operand(pacc[s >> 1], s);
-#pragma unroll
-        for (int d = 0; d < DB; ++d) {
-          dvacc[d] = mfma32(lds_kperm_operand(gt_lds, TLD, d * 32 + col, s, half), pop, dvacc[d]);
-          dkacc[d] = mfma32(lds_kperm_operand(qt_lds, TLD, d * 32 + col, s, half), dsop, dkacc[d]);
+          sacc[mb][r] = keep ? sacc[mb][r] : kNegInf;
         }
       }
     }
+#pragma unroll
+    for (int mb = 0; mb < BMQ / 32; ++mb) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        const int ml = mb * 32 + 8 * g + 4 * half;
+        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&stat_lds[B][0][ml]);
+        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&stat_lds[B][1][ml]);
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int r = 4 * g + e;
+          // a masked score is -inf and gives p = 0 exactly (lse is finite or +inf)
+          const float p = __builtin_amdgcn_exp2f(fmaf(sacc[mb][r], sl2, -l4[e]));
+          sacc[mb][r] = p;
+          pacc[mb][r] = p * (pacc[mb][r] - d4[e]);
+        }
+      }
+    }
+#pragma unroll
+    for (int s = 0; s < BMQ / 16; ++s) {
+      const bf16x8 pop = acc_kperm_operand(sacc[s >> 1], s);
+      const bf16x8 dsop = acc_kperm_operand(pacc[s >> 1], s);
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+        dvacc[d] = mfma32(trd.get(gt, d, s), pop, dvacc[d]);
+        dkacc[d] = mfma32(trd.get(qt, d, s), dsop, dkacc[d]);
+      }
+    }
+  };
+
+  // iteration `it` works on buffer B and prefetches iteration it + 1
+  int hq_cur = hk * group, m_cur = m_first;
+  auto advance = [&](int& hq, int& m0) {
+    m0 += BMQ;
+    if (m0 >= m_end) {
+      m0 = m_first;
+      ++hq;
+    }
+  };
+  auto iteration = [&](auto bufc, int it) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    const int hq = hq_cur, m0 = m_cur;
+    int hn = hq, mn = m0;
+    advance(hn, mn);
+    dma_barrier();
+    const bool more = it + 1 < total;
+    RowMeta next{};
+    if (more) {
+      qrows.issue(a, pb, dma, hn, mn, B ? q_lds0 : q_lds1, B ? g_lds0 : g_lds1, wave);
+      next = load_meta(hn, mn);
+    }
+    (void)hq;
+    if (wave_live && m0 + BMQ > wave_m_begin) tile_step(bufc, m0);
+    if (more) store_meta(std::integral_constant<int, B ^ 1>{}, next);
+    hq_cur = hn;
+    m_cur = mn;
+  };
+
+  if (total > 0) {
+    qrows.issue(a, pb, dma, hq_cur, m_cur, q_lds0, g_lds0, wave);
+    store_meta(std::integral_constant<int, 0>{}, load_meta(hq_cur, m_cur));
+  }
+  for (int it = 0; it < total; it += 2) {
+    iteration(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < total) iteration(std::integral_constant<int, 1>{}, it + 1);
   }
 
   if (!valid_k) return;

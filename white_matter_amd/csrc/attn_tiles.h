@@ -170,4 +170,59 @@ struct KeyTiles {
   }
 };
 
+// The query and output-gradient rows of one problem as 64-row LDS tiles (Q
+// and dO share the row addressing), for any query head. Rows past nq read as
+// zeros. Dense rows and varlen segments with consecutive query slots are
+// strided loads; other varlen layouts gather each row.
+template <int MODE, int D>
+struct QueryTiles {
+  const bf16 *qslice, *gslice;  // slot 0 of the queries' row, head 0
+  int64_t qst, gst, qhs, ghs;   // slot and head strides (elements)
+  int qfirst;                   // strided: query m at slot qfirst + m
+  int nq;
+  bool strided;
+  unsigned qoff[4], goff[4];
+
+  __device__ __forceinline__ void init(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D>& dma) {
+    nq = pb.nq;
+    int qb0 = pb.b;
+    qfirst = 0;
+    if constexpr (MODE == kVarlen) {
+      if (nq > 0) pb.query_loc(0, qb0, qfirst);
+    }
+    qslice = row_at(a.q, a.q_stride, qb0, 0, 0);
+    gslice = row_at(a.dout, a.do_stride, qb0, 0, 0);
+    qst = a.q_stride[2];
+    gst = a.do_stride[2];
+    qhs = a.q_stride[1];
+    ghs = a.do_stride[1];
+    const bool layout_ok = MODE != kVarlen || (a.segment_layout & kQueriesConsecutive);
+    const bool stride_ok = qst >= D && gst >= D && qst < (1 << 23) && gst < (1 << 23);
+    strided = layout_ok && stride_ok;
+    dma.strided_offsets(strided ? (int)qst * 2 : 0, qoff);
+    dma.strided_offsets(strided ? (int)gst * 2 : 0, goff);
+  }
+
+  __device__ __forceinline__ void issue(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D>& dma,
+                                        int hq, int m0, bf16* qtile, bf16* gtile, int wave) const {
+    if (strided) {
+      const int nvalid = min(max(nq - m0, 0), kTileRows);
+      const int64_t slot = (int64_t)qfirst + m0;
+      const rsrc_t rq = make_rsrc(qslice + hq * qhs + slot * qst, nvalid * (int)qst * 2);
+      const rsrc_t rg = make_rsrc(gslice + hq * ghs + slot * gst, nvalid * (int)gst * 2);
+      TileDMA<D>::issue_strided(rq, qtile, wave, qoff);
+      TileDMA<D>::issue_strided(rg, gtile, wave, goff);
+    } else {
+      dma.issue_gathered2(qtile, gtile, wave, [&](int tr, bool& ok, const bf16*& qp, const bf16*& gp) {
+        const int m = m0 + tr;
+        ok = m < nq;
+        int rb, rt;
+        pb.query_loc(ok ? m : 0, rb, rt);
+        qp = row_at(a.q, a.q_stride, rb, hq, rt);
+        gp = row_at(a.dout, a.do_stride, rb, hq, rt);
+      });
+    }
+  }
+};
+
 }  // namespace wmx

@@ -55,16 +55,21 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const wmx_attn_args a, i
 }
 
 // ------------------------------------------------------------------- dQ ----
+// One workgroup = 128 query rows (4 waves x 32) of one (batch row or segment,
+// query head), Q and dO rows in registers. Key/value tiles of 64 rows stream
+// through double-buffered LDS exactly as in the forward; the K tile is read
+// row-wise for S^T = K Q^T and with transpose reads for dQ^T = K^T dS^T.
 template <int D, int MODE>
 __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args a) {
   constexpr int BM = 128, BN = 64;
-  constexpr int KLD = D + 8, TLD = BN + 8;
+  static_assert(BN == kTileRows, "one LDS tile per key tile");
   constexpr int KS = D / 16, DB = D / 32;
-  __shared__ __attribute__((aligned(16))) bf16 k_lds[BN * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 v_lds[BN * KLD];
-  __shared__ __attribute__((aligned(16))) bf16 kt_lds[D * TLD];
-  __shared__ int kseg_lds[BN];
-  __shared__ int kqend_lds[BN];
+  // two buffers as distinct arrays with static roles (see the forward)
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 v_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 v_lds1[kTileElems];
+  __shared__ int meta_lds[2][2][BN];  // per buffer: key ids (or key mask), key query ends
   __shared__ int red_lds[4];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
@@ -124,7 +129,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
     if (lane == 0) red_lds[wave] = v;
     __syncthreads();
     v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
-    kt_begin_main = v < 0 ? 0 : v / BN;
+    kt_begin_main = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v / BN);  // uniform: keeps the tile loop scalar
   }
   int kt_end = (lim_max_wg + 1 + BN - 1) / BN;
   if (slot0 && kt_end < 1) kt_end = 1;
@@ -133,49 +138,38 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   const int ntiles = gap ? 1 + max(0, kt_end - first_main) : kt_end;
   auto tile_of = [&](int it) { return gap ? (it == 0 ? 0 : first_main + it - 1) : it; };
 
-  auto key_ptr = [&](const void* base, const int64_t* st, int j, bool& ok) -> const bf16* {
-    ok = j < nk && (j <= lim_max_wg || (slot0 && j == 0));
-    if (MODE == kDense && a.key_mask) ok = ok && a.key_mask[(int64_t)b * a.key_mask_stride + min(j, nk - 1)] != 0;
-    int kb, kt;
-    pb.key_loc(ok ? j : 0, kb, kt);
-    return row_at(base, st, kb, hk, kt);
+  TileDMA<D> dma;
+  dma.init(wave, lane);
+  KeyTiles<MODE, D> keys;
+  keys.init(a, pb, hk, slot0 ? max(lim_max_wg + 1, 1) : lim_max_wg + 1, dma);
+  auto load_meta = [&](int n0) -> int {
+    const int j = n0 + (tid & 63);
+    if constexpr (MODE == kDoc) {
+      if (tid < 64) return j < nk ? a.k_seg[(int64_t)b * a.kv_len + j] : INT_MIN;
+      if (tid < 128) return j < nk ? a.k_qend[(int64_t)b * a.kv_len + j] : 0;
+    } else if constexpr (MODE == kDense) {
+      if (a.key_mask && tid < 64) return j < nk ? (int)a.key_mask[(int64_t)b * a.key_mask_stride + j] : 0;
+    }
+    return 0;
+  };
+  auto store_meta = [&](int buf, int v) {
+    if (MODE == kDoc || (MODE == kDense && a.key_mask)) {
+      if (tid < 128) meta_lds[buf][tid >> 6][tid & 63] = v;
+    }
   };
 
-  PairTile<BN, D> ktile, vtile;
   f32x16 dqacc[DB];
 #pragma unroll
   for (int d = 0; d < DB; ++d) dqacc[d] = f32x16{};
   const float sl2 = a.softmax_scale * kLog2e;
+  RowReads<KS> rrd;
+  rrd.init(col, half);
+  TrReads<DB> trd;
+  trd.init(lane);
 
-  auto load = [&](int n0) {
-    ktile.load(tid, [&](int r, bool& ok) { return key_ptr(a.k, a.k_stride, n0 + r, ok); });
-    vtile.load(tid, [&](int r, bool& ok) { return key_ptr(a.v, a.v_stride, n0 + r, ok); });
-  };
-  if (ntiles > 0) load(tile_of(0) * BN);
-  for (int it = 0; it < ntiles; ++it) {
-    const int n0 = tile_of(it) * BN;
-    __syncthreads();
-    ktile.store_rows(tid, k_lds, KLD);
-    ktile.store_cols(tid, kt_lds, TLD);
-    vtile.store_rows(tid, v_lds, KLD);
-    if constexpr (MODE == kDoc) {
-      if (tid < BN) {
-        const int j = n0 + tid;
-        kseg_lds[tid] = j < nk ? a.k_seg[(int64_t)b * a.kv_len + j] : INT_MIN;
-        kqend_lds[tid] = j < nk ? a.k_qend[(int64_t)b * a.kv_len + j] : 0;
-      }
-    } else if constexpr (MODE == kDense) {
-      if (a.key_mask && tid < BN) {
-        const int j = n0 + tid;
-        kseg_lds[tid] = j < nk ? (int)a.key_mask[(int64_t)b * a.key_mask_stride + j] : 0;
-      }
-    }
-    __syncthreads();
-    if (it + 1 < ntiles) load(tile_of(it + 1) * BN);
-
-    const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
-    if (!wave_sees) continue;
-
+  auto tile_step = [&](int n0, int buf, const bf16* kt, const bf16* vt, bool masked) __attribute__((always_inline)) {
+    rrd.refresh();
+    trd.refresh();
     f32x16 sacc[BN / 32], pacc[BN / 32];
 #pragma unroll
     for (int nb = 0; nb < BN / 32; ++nb) {
@@ -183,30 +177,37 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
       pacc[nb] = f32x16{};
 #pragma unroll
       for (int s = 0; s < KS; ++s) {
-        sacc[nb] = mfma32(lds_row_operand(k_lds, KLD, nb * 32 + col, s, half), qf[s], sacc[nb]);
-        pacc[nb] = mfma32(lds_row_operand(v_lds, KLD, nb * 32 + col, s, half), gf[s], pacc[nb]);
+        sacc[nb] = mfma32(rrd.get(kt, s, nb), qf[s], sacc[nb]);
+        pacc[nb] = mfma32(rrd.get(vt, s, nb), gf[s], pacc[nb]);
       }
     }
-    const bool full = (MODE != kDoc) && !(MODE == kDense && a.key_mask) && (n0 + BN - 1 <= lim_min_wave) &&
-                      (n0 + BN <= nk);
+    if (masked) {
+      // keeps this block a real (wave-uniform) branch instead of selects
+      __asm__ volatile("");
+#pragma unroll
+      for (int nb = 0; nb < BN / 32; ++nb) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int jl = nb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          const int j = n0 + jl;
+          bool keep = (j <= lim_i) | (slot0 & (j == 0));
+          if constexpr (MODE == kDense) {
+            if (a.key_mask) keep = keep & (meta_lds[buf][0][jl] != 0);
+          }
+          if constexpr (MODE == kDoc) {
+            const int ksg = meta_lds[buf][0][jl], kqe = meta_lds[buf][1][jl];
+            keep = keep & (j < nk) & (((ksg == qseg_i) & (j >= qstart_i)) | (ksg == -1)) & (i < kqe);
+          }
+          sacc[nb][r] = keep ? sacc[nb][r] : kNegInf;
+        }
+      }
+    }
 #pragma unroll
     for (int nb = 0; nb < BN / 32; ++nb) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
-        bool keep = true;
-        if (!full) {
-          const int jl = nb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const int j = n0 + jl;
-          keep = (j <= lim_i) || (slot0 && j == 0);
-          if constexpr (MODE == kDense) {
-            if (a.key_mask) keep = keep && kseg_lds[jl] != 0;
-          }
-          if constexpr (MODE == kDoc) {
-            const int ksg = kseg_lds[jl];
-            keep = keep && j < nk && ((ksg == qseg_i && j >= qstart_i) || ksg == -1) && (i < kqend_lds[jl]);
-          }
-        }
-        const float p = keep ? __builtin_amdgcn_exp2f(fmaf(sacc[nb][r], sl2, -lse2)) : 0.f;
+        // a masked score is -inf and gives p = 0 exactly (lse is finite or +inf)
+        const float p = __builtin_amdgcn_exp2f(fmaf(sacc[nb][r], sl2, -lse2));
         sacc[nb][r] = p * (pacc[nb][r] - delta);
       }
     }
@@ -214,9 +215,43 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
     for (int s = 0; s < BN / 16; ++s) {
       const bf16x8 ds = acc_kperm_operand(sacc[s >> 1], s);
 #pragma unroll
-      for (int d = 0; d < DB; ++d) dqacc[d] = mfma32(lds_kperm_operand(kt_lds, TLD, d * 32 + col, s, half), ds, dqacc[d]);
+      for (int d = 0; d < DB; ++d) dqacc[d] = mfma32(trd.get(kt, d, s), ds, dqacc[d]);
     }
+  };
+
+  auto iteration = [&](auto bufc, int it) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    const bf16* kcur = B ? k_lds1 : k_lds0;
+    const bf16* vcur = B ? v_lds1 : v_lds0;
+    const int n0 = tile_of(it) * BN;
+    dma_barrier();
+    const bool more = it + 1 < ntiles;
+    int next_meta = 0;
+    if (more) {
+      const int n1 = tile_of(it + 1) * BN;
+      keys.issue(a, pb, dma, n1, B ? k_lds0 : k_lds1, B ? v_lds0 : v_lds1, wave);
+      next_meta = load_meta(n1);
+    }
+    const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    if (wave_sees) {
+      bool masked = !((n0 + BN - 1 <= lim_min_wave) && (n0 + BN <= nk));
+      if constexpr (MODE == kDense) masked = masked || a.key_mask != nullptr;
+      if constexpr (MODE == kDoc) masked = true;
+      tile_step(n0, B, kcur, vcur, masked);
+    }
+    if (more) store_meta(B ^ 1, next_meta);
+  };
+
+  if (ntiles > 0) {
+    const int n0 = tile_of(0) * BN;
+    keys.issue(a, pb, dma, n0, k_lds0, v_lds0, wave);
+    store_meta(0, load_meta(n0));
   }
+  for (int it = 0; it < ntiles; it += 2) {
+    iteration(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntiles) iteration(std::integral_constant<int, 1>{}, it + 1);
+  }
+
   if (!valid_q) return;
   bf16* dqrow = (bf16*)row_at(a.dq, a.dq_stride, qb, h, qt);
   store_acc_row<DB>(dqrow, dqacc, a.softmax_scale, half);

@@ -229,7 +229,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
     int next_meta = 0;
     if (more) {
       const int n1 = tile_of(it + 1) * BN;
-      keys.issue(a, pb, dma, n1, B ? k_lds0 : k_lds1, B ? v_lds0 : v_lds1, wave);
+      keys.issue(a, pb, dma, n1, B ? k_lds0 : k_lds1, B ? v_lds0 : v_lds1);
       next_meta = load_meta(n1);
     }
     const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
@@ -244,7 +244,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
 
   if (ntiles > 0) {
     const int n0 = tile_of(0) * BN;
-    keys.issue(a, pb, dma, n0, k_lds0, v_lds0, wave);
+    keys.issue(a, pb, dma, n0, k_lds0, v_lds0);
     store_meta(0, load_meta(n0));
   }
   for (int it = 0; it < ntiles; it += 2) {
@@ -396,46 +396,44 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   };
 
   // One query tile against this wave's 32 keys.
+  // first query row that sees this lane's key (INT_MAX for a dead key): the
+  // causal/offset rule is then one comparison per score
+  const int m_lo = !k_live ? INT_MAX : (slot0 && n == 0) ? 0 : pb.bound.first_row(n, nq);
+
+  // One query tile against this wave's 32 keys, in two halves of 32 query
+  // rows so that only one half's scores are live at a time.
   auto tile_step = [&](auto bufc, int m0) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
     const bf16* qt = B ? q_lds1 : q_lds0;
     const bf16* gt = B ? g_lds1 : g_lds0;
     rrd.refresh();
     trd.refresh();
-    f32x16 sacc[BMQ / 32], pacc[BMQ / 32];
-#pragma unroll
-    for (int mb = 0; mb < BMQ / 32; ++mb) {
-      sacc[mb] = f32x16{};
-      pacc[mb] = f32x16{};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        sacc[mb] = mfma32(rrd.get(qt, s, mb), kf[s], sacc[mb]);
-        pacc[mb] = mfma32(rrd.get(gt, s, mb), vf[s], pacc[mb]);
-      }
-    }
     // every pair of the tile is visible to this wave: no per-element mask
     const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= wave_m_begin &&
                       m0 + BMQ <= nq && pb.bound.lim(m0) >= wave_key0 + 31;
-    if (!full) {
-      // keeps this block a real (wave-uniform) branch instead of selects
-      __asm__ volatile("");
+    const int lo = m_lo - m0, hi = nq - m0;  // rows ml in [lo, hi) see the key
 #pragma unroll
-      for (int mb = 0; mb < BMQ / 32; ++mb) {
+    for (int mb = 0; mb < BMQ / 32; ++mb) {
+      f32x16 sacc = f32x16{}, pacc = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) {
+        sacc = mfma32(rrd.get(qt, s, mb), kf[s], sacc);
+        pacc = mfma32(rrd.get(gt, s, mb), vf[s], pacc);
+      }
+      if (!full) {
+        // keeps this block a real (wave-uniform) branch instead of selects
+        __asm__ volatile("");
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int ml = mb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const int m = m0 + ml;
-          bool keep = k_live & (m < nq) & ((n <= pb.bound.lim(m)) | (slot0 & (n == 0)));
+          bool keep = (ml >= lo) & (ml < hi);
           if constexpr (MODE == kDoc) {
             const int qsg = qdoc_lds[B][0][ml], qst = qdoc_lds[B][1][ml];
-            keep = keep & (((qsg == kseg_n) & (n >= qst)) | (kseg_n == -1)) & (m < kqend_n);
+            keep = keep & (((qsg == kseg_n) & (n >= qst)) | (kseg_n == -1)) & (m0 + ml < kqend_n);
           }
-          sacc[mb][r] = keep ? sacc[mb][r] : kNegInf;
+          sacc[r] = keep ? sacc[r] : kNegInf;
         }
       }
-    }
-#pragma unroll
-    for (int mb = 0; mb < BMQ / 32; ++mb) {
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int ml = mb * 32 + 8 * g + 4 * half;
@@ -445,20 +443,21 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
         for (int e = 0; e < 4; ++e) {
           const int r = 4 * g + e;
           // a masked score is -inf and gives p = 0 exactly (lse is finite or +inf)
-          const float p = __builtin_amdgcn_exp2f(fmaf(sacc[mb][r], sl2, -l4[e]));
-          sacc[mb][r] = p;
-          pacc[mb][r] = p * (pacc[mb][r] - d4[e]);
+          const float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], sl2, -l4[e]));
+          sacc[r] = p;
+          pacc[r] = p * (pacc[r] - d4[e]);
         }
       }
-    }
 #pragma unroll
-    for (int s = 0; s < BMQ / 16; ++s) {
-      const bf16x8 pop = acc_kperm_operand(sacc[s >> 1], s);
-      const bf16x8 dsop = acc_kperm_operand(pacc[s >> 1], s);
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int s = 2 * mb + h2;
+        const bf16x8 pop = acc_kperm_operand(sacc, s);
+        const bf16x8 dsop = acc_kperm_operand(pacc, s);
 #pragma unroll
-      for (int d = 0; d < DB; ++d) {
-        dvacc[d] = mfma32(trd.get(gt, d, s), pop, dvacc[d]);
-        dkacc[d] = mfma32(trd.get(qt, d, s), dsop, dkacc[d]);
+        for (int d = 0; d < DB; ++d) {
+          dvacc[d] = mfma32(trd.get(gt, d, s), pop, dvacc[d]);
+          dkacc[d] = mfma32(trd.get(qt, d, s), dsop, dkacc[d]);
+        }
       }
     }
   };
@@ -481,7 +480,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
     const bool more = it + 1 < total;
     RowMeta next{};
     if (more) {
-      qrows.issue(a, pb, dma, hn, mn, B ? q_lds0 : q_lds1, B ? g_lds0 : g_lds1, wave);
+      qrows.issue(a, pb, dma, hn, mn, B ? q_lds0 : q_lds1, B ? g_lds0 : g_lds1);
       next = load_meta(hn, mn);
     }
     (void)hq;
@@ -492,7 +491,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   };
 
   if (total > 0) {
-    qrows.issue(a, pb, dma, hq_cur, m_cur, q_lds0, g_lds0, wave);
+    qrows.issue(a, pb, dma, hq_cur, m_cur, q_lds0, g_lds0);
     store_meta(std::integral_constant<int, 0>{}, load_meta(hq_cur, m_cur));
   }
   for (int it = 0; it < total; it += 2) {
@@ -624,4 +623,22 @@ int launch_bwd(const wmx_attn_args& a, hipStream_t stream) {
   return rc;
 }
 
+}  // namespace wmx
+
+// Explicit instantiations of the launched kernels: every launcher above then
+// finds its host stub even where the compiler would not emit one for an
+// instantiation first seen next to a branch it folds away.
+namespace wmx {
+#define WMX_BWD_KERNELS(D)                                                   \
+  template __global__ void attn_bwd_dq_kernel<D, kDense>(const wmx_attn_args);   \
+  template __global__ void attn_bwd_dq_kernel<D, kDoc>(const wmx_attn_args);     \
+  template __global__ void attn_bwd_dq_kernel<D, kVarlen>(const wmx_attn_args);  \
+  template __global__ void attn_bwd_dkv_kernel<D, kDense, false>(const wmx_attn_args); \
+  template __global__ void attn_bwd_dkv_kernel<D, kDoc, false>(const wmx_attn_args);   \
+  template __global__ void attn_bwd_dkv_kernel<D, kVarlen, false>(const wmx_attn_args); \
+  template __global__ void attn_bwd_dkv_kernel<D, kVarlen, true>(const wmx_attn_args);
+WMX_BWD_KERNELS(64)
+WMX_BWD_KERNELS(96)
+WMX_BWD_KERNELS(128)
+#undef WMX_BWD_KERNELS
 }  // namespace wmx

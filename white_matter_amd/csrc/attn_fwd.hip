@@ -245,7 +245,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
     int next_meta = 0;
     if (more) {
       const int n1 = tile_of(it + 1) * BN;
-      keys.issue(a, pb, dma, n1, knext, vnext, wave);
+      keys.issue(a, pb, dma, n1, knext, vnext);
       next_meta = load_meta(n1);
     }
     const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
@@ -270,7 +270,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
 
   if (ntiles > 0) {
     const int n0 = tile_of(0) * BN;
-    keys.issue(a, pb, dma, n0, k_lds0, v_lds0, wave);
+    keys.issue(a, pb, dma, n0, k_lds0, v_lds0);
     store_meta(0, load_meta(n0));
   }
   for (int it = 0; it < ntiles; it += 2) {

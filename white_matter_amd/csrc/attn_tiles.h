@@ -146,16 +146,16 @@ struct KeyTiles {
 
   template <class Args>
   __device__ __forceinline__ void issue(const Args& a, const Problem<MODE>& pb, const TileDMA<D>& dma, int n0,
-                                        bf16* ktile, bf16* vtile, int wave) const {
+                                        bf16* ktile, bf16* vtile) const {
     if (strided && (MODE != kVarlen || n0 > 0)) {
       const int nvalid = min(max(reach - n0, 0), kTileRows);
       const int64_t slot = (int64_t)kfirst + n0;
       const rsrc_t rk = make_rsrc(kslice + slot * kst, nvalid * (int)kst * 2);
       const rsrc_t rv = make_rsrc(vslice + slot * vst, nvalid * (int)vst * 2);
-      TileDMA<D>::issue_strided(rk, ktile, wave, koff);
-      TileDMA<D>::issue_strided(rv, vtile, wave, voff);
+      dma.issue_strided(rk, ktile, koff);
+      dma.issue_strided(rv, vtile, voff);
     } else {
-      dma.issue_gathered2(ktile, vtile, wave, [&](int tr, bool& ok, const bf16*& kp, const bf16*& vp) {
+      dma.issue_gathered2(ktile, vtile, [&](int tr, bool& ok, const bf16*& kp, const bf16*& vp) {
         const int j = n0 + tr;
         ok = j < reach;
         if constexpr (MODE == kDense) {
@@ -181,7 +181,6 @@ struct QueryTiles {
   int qfirst;                   // strided: query m at slot qfirst + m
   int nq;
   bool strided;
-  unsigned qoff[4], goff[4];
 
   __device__ __forceinline__ void init(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D>& dma) {
     nq = pb.nq;
@@ -199,21 +198,19 @@ struct QueryTiles {
     const bool layout_ok = MODE != kVarlen || (a.segment_layout & kQueriesConsecutive);
     const bool stride_ok = qst >= D && gst >= D && qst < (1 << 23) && gst < (1 << 23);
     strided = layout_ok && stride_ok;
-    dma.strided_offsets(strided ? (int)qst * 2 : 0, qoff);
-    dma.strided_offsets(strided ? (int)gst * 2 : 0, goff);
   }
 
   __device__ __forceinline__ void issue(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D>& dma,
-                                        int hq, int m0, bf16* qtile, bf16* gtile, int wave) const {
+                                        int hq, int m0, bf16* qtile, bf16* gtile) const {
     if (strided) {
       const int nvalid = min(max(nq - m0, 0), kTileRows);
       const int64_t slot = (int64_t)qfirst + m0;
       const rsrc_t rq = make_rsrc(qslice + hq * qhs + slot * qst, nvalid * (int)qst * 2);
       const rsrc_t rg = make_rsrc(gslice + hq * ghs + slot * gst, nvalid * (int)gst * 2);
-      TileDMA<D>::issue_strided(rq, qtile, wave, qoff);
-      TileDMA<D>::issue_strided(rg, gtile, wave, goff);
+      dma.issue_strided_rows(rq, qtile, (int)qst * 2);
+      dma.issue_strided_rows(rg, gtile, (int)gst * 2);
     } else {
-      dma.issue_gathered2(qtile, gtile, wave, [&](int tr, bool& ok, const bf16*& qp, const bf16*& gp) {
+      dma.issue_gathered2(qtile, gtile, [&](int tr, bool& ok, const bf16*& qp, const bf16*& gp) {
         const int m = m0 + tr;
         ok = m < nq;
         int rb, rt;

@@ -131,52 +131,59 @@ static __device__ __attribute__((aligned(16))) const uint32_t kZeroChunk[4] = {0
 // each wave filling 16 rows with 4 instructions).
 template <int D>
 struct TileDMA {
-  int row[4];      // tile row of instruction r
-  int chunk16[4];  // byte offset of the logical chunk in the row, or -1 for padding
+  // Instruction r of wave w fills tile row (4 w + r) * 4 + sub, sub = lane / 16,
+  // whose swizzle is 4 sub + r: the lane loads logical chunk lc0 ^ r with
+  // lc0 = (lane % 16) ^ 4 sub. Only these three values are kept; rows and
+  // offsets are formed per use.
+  int wave, sub, lc0;
 
-  __device__ __forceinline__ void init(int wave, int lane) {
-#pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      const int tr = (wave * 4 + r) * 4 + (lane >> 4);
-      const int lc = (lane & 15) ^ tile_swz(tr);
-      row[r] = tr;
-      chunk16[r] = lc < D / 8 ? lc * 16 : -1;
-    }
+  __device__ __forceinline__ void init(int wave_, int lane) {
+    wave = wave_;
+    sub = lane >> 4;
+    lc0 = (lane & 15) ^ (sub << 2);
   }
-  // Per-lane byte offsets of a strided tile with row stride row_bytes
-  // (0 <= row_bytes * 64 < 2^31).
+  __device__ __forceinline__ int row(int r) const { return (wave * 4 + r) * 4 + sub; }
+  // byte offset of this lane's chunk of instruction r in its row, or -1 for padding
+  __device__ __forceinline__ int chunk16(int r) const {
+    const int c = lc0 ^ r;
+    return (D == 128 || c < D / 8) ? 16 * c : -1;
+  }
+  // Per-lane byte offset of instruction r of a strided tile with row stride
+  // row_bytes (0 <= row_bytes * 64 < 2^31).
+  __device__ __forceinline__ unsigned strided_offset(int r, int row_bytes) const {
+    const int c = chunk16(r);
+    return c < 0 ? kOutOfRange : (unsigned)(row(r) * row_bytes + c);
+  }
   __device__ __forceinline__ void strided_offsets(int row_bytes, unsigned (&off)[4]) const {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) off[r] = chunk16[r] < 0 ? kOutOfRange : (unsigned)(row[r] * row_bytes + chunk16[r]);
+    for (int r = 0; r < 4; ++r) off[r] = strided_offset(r, row_bytes);
   }
-  static __device__ __forceinline__ void issue_strided(const rsrc_t& rs, bf16* tile, int wave, const unsigned (&off)[4]) {
+  __device__ __forceinline__ void issue_strided(const rsrc_t& rs, bf16* tile, const unsigned (&off)[4]) const {
 #pragma unroll
     for (int r = 0; r < 4; ++r)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + (wave * 4 + r) * 512), 16, off[r], 0, 0, 0);
   }
-  // rows(tr, ok) returns the address of tile row tr and sets ok = false for a
-  // row that must read as zeros.
-  template <class Rows>
-  __device__ __forceinline__ void issue_gathered(bf16* tile, int wave, Rows rows) const {
+  // Offsets formed at issue time (no registers held between tiles).
+  __device__ __forceinline__ void issue_strided_rows(const rsrc_t& rs, bf16* tile, int row_bytes) const {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
-      bool ok;
-      const bf16* p = rows(row[r], ok);
-      const void* src = (ok && chunk16[r] >= 0) ? (const void*)((const char*)p + chunk16[r]) : (const void*)kZeroChunk;
-      __builtin_amdgcn_global_load_lds(src, (lds_void*)(tile + (wave * 4 + r) * 512), 16, 0, 0);
-    }
+    for (int r = 0; r < 4; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + (wave * 4 + r) * 512), 16,
+                                               strided_offset(r, row_bytes), 0, 0, 0);
   }
-  // Two tiles whose rows are located together: rows(tr, ok, p0, p1).
+  // Two tiles whose rows are located together: rows(tr, ok, p0, p1) returns
+  // the addresses of tile row tr and sets ok = false for a row that must read
+  // as zeros.
   template <class Rows>
-  __device__ __forceinline__ void issue_gathered2(bf16* t0, bf16* t1, int wave, Rows rows) const {
+  __device__ __forceinline__ void issue_gathered2(bf16* t0, bf16* t1, Rows rows) const {
 #pragma unroll
     for (int r = 0; r < 4; ++r) {
       bool ok;
       const bf16 *p0, *p1;
-      rows(row[r], ok, p0, p1);
-      const bool use = ok && chunk16[r] >= 0;
-      const void* s0 = use ? (const void*)((const char*)p0 + chunk16[r]) : (const void*)kZeroChunk;
-      const void* s1 = use ? (const void*)((const char*)p1 + chunk16[r]) : (const void*)kZeroChunk;
+      rows(row(r), ok, p0, p1);
+      const int c = chunk16(r);
+      const bool use = ok && c >= 0;
+      const void* s0 = use ? (const void*)((const char*)p0 + c) : (const void*)kZeroChunk;
+      const void* s1 = use ? (const void*)((const char*)p1 + c) : (const void*)kZeroChunk;
       __builtin_amdgcn_global_load_lds(s0, (lds_void*)(t0 + (wave * 4 + r) * 512), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(s1, (lds_void*)(t1 + (wave * 4 + r) * 512), 16, 0, 0);
     }

@@ -33,6 +33,16 @@ if ROOT not in sys.path:
 
 PEAK_BF16_TFLOPS = 2500.0  # MI355X dense bf16 MFMA
 PEAK_HBM_GBPS = 8000.0  # MI355X HBM3E
+CALIBRATION_BYTES = 256 << 20
+TRAFFIC_PROFILE = os.path.join(ROOT, "profiles", "c2_strict_jacobi_traffic.md")
+KERNEL_NAMES = {  # rocprof kernel name prefix -> bench kernel key
+    "wmx::attn_fwd_kernel": "attn_fwd",
+    "wmx::bwd_delta_kernel": "bwd_delta",
+    "wmx::attn_bwd_dq_kernel": "bwd_dq",
+    "wmx::attn_bwd_dkv_kernel": "bwd_dkv",
+    "wmx::decode_split_kernel": "decode_split",
+    "wmx::decode_combine_kernel": "decode_combine",
+}
 METRIC = "attn fwd+bwd TFLOP/s (bf16, T=2048) and % MFMA peak; decode GB/s"
 
 
@@ -167,8 +177,8 @@ def cpu_baseline(q, k, v, metadata, budget_s: float):
         "key_extent": metadata.key_extent,
     }
     keep_all = ref.schedule_keep(meta_np, batch, length, k.shape[2])
-    while elapsed < budget_s and rows < batch:
-        b = rows
+    while elapsed < budget_s:
+        b = rows % batch  # cycle over the batch rows until the budget is spent
         qb, kb, vb = (t[b : b + 1].float().cpu().requires_grad_() for t in (q, k, v))
         keep = keep_all[b : b + 1, None]
         t0 = time.perf_counter()
@@ -183,9 +193,77 @@ def cpu_baseline(q, k, v, metadata, budget_s: float):
         "unit": "TFLOP/s",
         "cores": threads,
         "kind": "port",
-        "sample": f"{rows} of {batch} rows of the C2 batch (all {heads} heads, T={length}), fp32, "
-        f"{elapsed:.1f} s; visible-pair FLOPs as the GPU value",
+        "sample": f"{rows} single-row passes over the {batch} rows of the C2 batch (all {heads} heads, "
+        f"T={length}), fp32 forward + backward, {elapsed:.1f} s; visible-pair FLOPs as the GPU value",
     }
+
+
+def algorithmic_bytes(q, k, v) -> dict[str, int]:
+    """HBM bytes each kernel must move at least once per launch: its operands
+    read and its results written (bf16 tensors, fp32 LSE and delta)."""
+    t = q.numel() * 2  # Q, O, dO, dQ each
+    kv = k.numel() * 2 + v.numel() * 2
+    rows = q.shape[0] * q.shape[1] * q.shape[2] * 4  # LSE or delta
+    return {
+        "attn_fwd": 2 * t + kv + rows,  # Q, K, V in; O, LSE out
+        "bwd_delta": 2 * t + rows,  # O, dO in; delta out
+        "bwd_dq": 3 * t + kv + 2 * rows,  # Q, dO, K, V, LSE, delta in; dQ out
+        "bwd_dkv": 2 * t + 2 * kv + 2 * rows,  # Q, dO, K, V, LSE, delta in; dK, dV out
+    }
+
+
+def measured_traffic(kernel: str) -> int | None:
+    """HBM bytes per launch of `kernel` (FETCH_SIZE + WRITE_SIZE scaled by the
+    calibration copy) from the JSON block of the committed rocprof summary of
+    this workload, or None when there is none."""
+    try:
+        with open(TRAFFIC_PROFILE) as f:
+            text = f.read()
+        block = text.split("```json", 1)[1].split("```", 1)[0]
+        entry = json.loads(block)["kernels"][kernel]
+        return int(entry["fetch_bytes"] + entry["write_bytes"])
+    except (OSError, IndexError, KeyError, ValueError):
+        return None
+
+
+def pmc_summary(dirs) -> dict:
+    """Per-kernel averages of FETCH_SIZE and WRITE_SIZE (KiB per dispatch,
+    summed over counter dimensions) from rocprofv3 --pmc --output-format csv
+    directories, converted to bytes with the factor the same counters read on
+    the calibration copy (torch.neg over CALIBRATION_BYTES in and out)."""
+    import csv
+    import glob
+
+    per = {}  # (kernel, dispatch) -> counter -> value
+    for d in dirs:
+        for path in glob.glob(os.path.join(d, "**", "*counter_collection.csv"), recursive=True):
+            with open(path) as f:
+                for row in csv.DictReader(f):
+                    key = (row["Kernel_Name"], path, row["Dispatch_Id"])
+                    counters = per.setdefault(key, {})
+                    name = row["Counter_Name"]
+                    counters[name] = counters.get(name, 0.0) + float(row["Counter_Value"])
+    calib = {}
+    sums = {}
+    for (name, _, _), counters in per.items():
+        for counter, value in counters.items():
+            if "neg_kernel" in name:  # torch.neg's elementwise kernel: the calibration copy
+                calib[counter] = max(calib.get(counter, 0.0), value)
+            short = next((v for k, v in KERNEL_NAMES.items() if name.startswith(k) or name.startswith("void " + k)), None)
+            if short:
+                sums.setdefault(short, {}).setdefault(counter, []).append(value)
+    out = {"calibration_bytes": CALIBRATION_BYTES, "calibration_counters_kib": calib, "kernels": {}}
+    factor = {c: CALIBRATION_BYTES / v for c, v in calib.items() if v > 0}
+    out["bytes_per_counter_unit"] = factor
+    for short, counters in sums.items():
+        entry = {}
+        for counter, values in counters.items():
+            avg = sum(values) / len(values)
+            entry[counter.lower() + "_raw"] = avg
+            if counter in factor:
+                entry[{"FETCH_SIZE": "fetch_bytes", "WRITE_SIZE": "write_bytes"}.get(counter, counter)] = avg * factor[counter]
+        out["kernels"][short] = entry
+    return out
 
 
 def main(argv=None) -> int:
@@ -194,15 +272,24 @@ def main(argv=None) -> int:
     parser.add_argument("--steps", type=int, default=20)
     parser.add_argument("--warmup", type=int, default=3)
     parser.add_argument("--kernel-reps", type=int, default=20)
-    parser.add_argument("--cpu-budget", type=float, default=10.0, help="seconds of CPU baseline work")
+    parser.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
     parser.add_argument(
         "--copy-calibration",
         action="store_true",
-        help="first run one device copy of 256 MiB, the known-size kernel that scales FETCH_SIZE/WRITE_SIZE",
+        help="first run one elementwise copy (torch.neg) of 256 MiB, the known-size kernel that scales FETCH_SIZE/WRITE_SIZE",
+    )
+    parser.add_argument(
+        "--pmc-summary",
+        nargs="+",
+        metavar="DIR",
+        help="summarise rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE output directories (no GPU work) and exit",
     )
     args = parser.parse_args(argv)
+    if args.pmc_summary:
+        print(json.dumps(pmc_summary(args.pmc_summary), indent=1))
+        return 0
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
         print("bench.py measures one GPU: this build has no multi-GPU path (run with --gpus 1)", file=sys.stderr)
         return 2
@@ -214,9 +301,10 @@ def main(argv=None) -> int:
 
     device = torch.device("cuda:0")
     if args.copy_calibration:
-        src = torch.ones(256 << 20, dtype=torch.uint8, device=device)
+        # one elementwise kernel that reads and writes exactly CALIBRATION_BYTES
+        src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=device)
         dst = torch.empty_like(src)
-        dst.copy_(src)
+        torch.neg(src, out=dst)
         torch.cuda.synchronize()
         del src, dst
     q, k, v, docs, metadata, meta_ms = strict_jacobi_setup(device)
@@ -244,8 +332,10 @@ def main(argv=None) -> int:
         "bwd_dkv": 8 * dim * heads * pairs,
         "bwd_delta": 0,
     }
+    hbm = algorithmic_bytes(q, k, v)
     dominant = max(kernels, key=kernels.get)
     dom_achieved = algorithmic[dominant] / (kernels[dominant] * 1e-3) / 1e12
+    traffic = measured_traffic(dominant)
     roofline = {
         "bound": "mfma",
         "kernel": dominant,
@@ -253,7 +343,8 @@ def main(argv=None) -> int:
         "peak": PEAK_BF16_TFLOPS,
         "unit": "TFLOP/s",
         "frac": round(dom_achieved / PEAK_BF16_TFLOPS, 4),
-        "traffic": None,
+        "traffic": traffic,
+        "algorithmic_bytes": hbm[dominant],
         "avg_ms": round(kernels[dominant], 4),
     }
     line = {
@@ -286,6 +377,9 @@ def main(argv=None) -> int:
             name: {
                 "avg_ms": round(t, 4),
                 "algorithmic_tflops": round(algorithmic[name] / (t * 1e-3) / 1e12, 2),
+                "frac_mfma": round(algorithmic[name] / (t * 1e-3) / 1e12 / PEAK_BF16_TFLOPS, 4),
+                "algorithmic_gbps": round(hbm[name] / (t * 1e-3) / 1e9, 1),
+                "frac_hbm": round(hbm[name] / (t * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
             }
             for name, t in kernels.items()
         },

@@ -233,10 +233,13 @@ cyclic_attn_doc_bwd.register_fake(_fake_bwd)
 def _setup_ctx(ctx, inputs, output):
     *tensors, ctx.K_stride, ctx.residue, ctx.block_M = inputs
     ctx.save_for_backward(*tensors, *output)
+    ctx.set_materialize_grads(False)  # Lse has no gradient: no zero fill for it
 
 
 def _backward(ctx, dOut, dLse):
     tensors = ctx.saved_tensors
+    if dOut is None:
+        dOut = torch.zeros_like(tensors[-2])
     # Q/K/V, optionally four document tensors, then O and LSE
     if len(tensors) == 9:
         grads = cyclic_attn_doc_bwd(*tensors, dOut, ctx.K_stride, ctx.residue, ctx.block_M)

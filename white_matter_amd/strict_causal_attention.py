@@ -183,11 +183,12 @@ def _segment_layout(indices: torch.Tensor, cu: torch.Tensor, extent: int, skip_f
     return bool((indices == expected).all()) and rows_ok, rows_ok
 
 
-def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int, int, int]:
+def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int, int, int, bool]:
     """Host facts the kernels need, computed once per metadata object and kept
     on it: largest segment (queries, keys), whether key rows repeat across
-    segments, the largest query and key index (for bounds checks), and the
-    segment layout bits of wmx_attn_args (consecutive / one-row slots)."""
+    segments, the largest query and key index (for bounds checks), the
+    segment layout bits of wmx_attn_args (consecutive / one-row slots), and
+    whether query rows repeat."""
     facts = getattr(metadata, "_facts", None)
     if facts is None:
         segments = metadata.segments
@@ -198,6 +199,7 @@ def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int
             raise ValueError("metadata segments do not cover query_indices/key_indices")
         n = ki.numel()
         unique = n == 0 or int(torch.unique(ki).numel()) == n
+        unique_q = qi.numel() == 0 or int(torch.unique(qi).numel()) == qi.numel()
         top_q = int(qi.max()) if qi.numel() else -1
         top_k = int(ki.max()) if n else -1
         if (qi.numel() and int(qi.min()) < 0) or (n and int(ki.min()) < 0):
@@ -205,7 +207,7 @@ def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int
         q_consecutive, q_one_row = _segment_layout(qi, metadata.cu_queries, metadata.max_queries, False)
         k_consecutive, k_one_row = _segment_layout(ki, metadata.cu_keys, metadata.key_extent, True)
         layout = (1 if q_consecutive else 0) | (2 if k_consecutive else 0) | (4 if q_one_row else 0) | (8 if k_one_row else 0)
-        facts = (max_q, max_k, unique, top_q, top_k, layout)
+        facts = (max_q, max_k, unique, top_q, top_k, layout, unique_q)
         object.__setattr__(metadata, "_facts", facts)
     return facts
 
@@ -300,10 +302,13 @@ def _dense_setup(ctx, inputs, output):
     extras = [t for t in (row_offset, row_limit, key_mask) if t is not None]
     ctx.dtypes = (query.dtype, key.dtype, value.dtype)
     ctx.save_for_backward(query, key, value, *output, *extras)
+    ctx.set_materialize_grads(False)  # the LSE output has no gradient: no zero fill for it
 
 
 def _dense_backward(ctx, dout, dlse):
     query, key, value, out, lse, *extras = ctx.saved_tensors
+    if dout is None:
+        dout = torch.zeros_like(out)
     it = iter(extras)
     row_offset, row_limit, key_mask = (next(it) if flag else None for flag in ctx.has)
     dq, dk, dv = strict_dense_bwd(
@@ -320,8 +325,47 @@ _KEYS_UNIQUE = 16  # schedule_flags bit above the four segment-layout bits
 
 def _schedule_flags(metadata: StrictCausalMetadata) -> tuple[int, int, int]:
     """(max_queries, max_keys, flags) passed to the varlen operators."""
-    max_q, max_k, unique, _, _, layout = _schedule_facts(metadata)
+    max_q, max_k, unique, _, _, layout, _ = _schedule_facts(metadata)
     return max_q, max_k, layout | (_KEYS_UNIQUE if unique else 0)
+
+
+def _schedule_gaps(
+    metadata: StrictCausalMetadata, batch: int, length: int, heads: int, key_extent: int, kv_heads: int
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Rows that no segment writes, as flat row indices of the outputs'
+    storage, so the operators zero only these rows (one index_fill each)
+    instead of filling whole tensors:
+      - O rows of the (B*T, H*D) view of the (B, T, H, D) output,
+      - dQ rows of the (B*H*T, D) view of the (B, H, T, D) gradient,
+      - dK/dV rows of the (B*Hkv*N, D) view of the (B, Hkv, N, D) gradients.
+    Repeated key rows go through fp32 accumulators converted in full, which
+    leaves no key gap. Cached on the metadata object per call shape."""
+    cache = metadata.__dict__.setdefault("_gaps", {})
+    key = (batch, length, heads, key_extent, kv_heads)
+    gaps = cache.get(key)
+    if gaps is None:
+        facts = _schedule_facts(metadata)
+        unique_k, unique_q = facts[2], facts[6]
+        device = metadata.query_indices.device
+        none = torch.empty(0, dtype=torch.long, device=device)
+
+        def missing(indices: torch.Tensor, total: int, unique: bool) -> torch.Tensor:
+            if unique and indices.numel() == total:
+                return none
+            seen = torch.zeros(total, dtype=torch.bool, device=device)
+            seen[indices] = True
+            return torch.nonzero(~seen).flatten()
+
+        def per_head(flat: torch.Tensor, extent: int, count: int) -> torch.Tensor:
+            # flat b * extent + t -> (b * count + h) * extent + t for every head h
+            b, t = flat // extent, flat % extent
+            h = torch.arange(count, device=device)
+            return ((b[:, None] * count + h[None, :]) * extent + t[:, None]).flatten()
+
+        out_rows = missing(metadata.query_indices, batch * length, unique_q)
+        key_flat = missing(metadata.key_indices, batch * key_extent, True) if unique_k else none
+        gaps = cache[key] = (out_rows, per_head(out_rows, length, heads), per_head(key_flat, key_extent, kv_heads))
+    return gaps
 
 
 def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, max_k, flags):
@@ -353,12 +397,19 @@ def strict_varlen_fwd(
     max_keys: int,
     schedule_flags: int,
     scale: float,
+    out_gaps: torch.Tensor,
+    dq_gaps: torch.Tensor,
+    dkv_gaps: torch.Tensor,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Packed-segment attention read straight from (B, H, T, D) storage;
-    output (B, T, H, D) with zeros for queries outside every segment."""
+    output (B, T, H, D) with zeros for the queries outside every segment
+    (`out_gaps`: rows of the (B*T, H*D) view). `dq_gaps` and `dkv_gaps`
+    (see _schedule_gaps) are kept for the backward."""
     q, k, v = (_kernels.operand(t) for t in (query, key, value))
     batch, heads, length, dim = q.shape
-    out = torch.zeros(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
+    out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
+    if out_gaps.numel():
+        out.view(batch * length, heads * dim).index_fill_(0, out_gaps, 0)
     lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
     vis = _kernels.Visibility(
         varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags)
@@ -392,13 +443,24 @@ def strict_varlen_bwd(
     max_keys: int,
     schedule_flags: int,
     scale: float,
+    dq_gaps: torch.Tensor,
+    dkv_gaps: torch.Tensor,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients of strict_varlen_fwd; the rows no segment writes (`dq_gaps`
+    of the (B*H*T, D) view of dQ, `dkv_gaps` of the (B*Hkv*N, D) views of dK
+    and dV) are zero."""
     q, k, v = (_kernels.operand(t) for t in (query, key, value))
     o = _kernels.operand(out.transpose(1, 2))
     g = _kernels.operand(dout.transpose(1, 2))
-    dq = torch.zeros(q.shape, device=q.device, dtype=torch.bfloat16)
-    dk = torch.zeros(k.shape, device=q.device, dtype=torch.bfloat16)
-    dv = torch.zeros(v.shape, device=q.device, dtype=torch.bfloat16)
+    dim = q.shape[3]
+    dq = torch.empty(q.shape, device=q.device, dtype=torch.bfloat16)
+    dk = torch.empty(k.shape, device=q.device, dtype=torch.bfloat16)
+    dv = torch.empty(v.shape, device=q.device, dtype=torch.bfloat16)
+    if dq_gaps.numel():
+        dq.view(-1, dim).index_fill_(0, dq_gaps, 0)
+    if dkv_gaps.numel():
+        dk.view(-1, dim).index_fill_(0, dkv_gaps, 0)
+        dv.view(-1, dim).index_fill_(0, dkv_gaps, 0)
     vis = _kernels.Visibility(
         varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags)
     )
@@ -416,17 +478,21 @@ def _(query, key, value, *args):
 
 
 def _varlen_setup(ctx, inputs, output):
-    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale = inputs
+    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale, _, dq_gaps, dkv_gaps = inputs
     ctx.dtypes = (query.dtype, key.dtype, value.dtype)
-    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck)
+    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck, dq_gaps, dkv_gaps)
+    ctx.set_materialize_grads(False)  # the LSE output has no gradient: no zero fill for it
 
 
 def _varlen_backward(ctx, dout, dlse):
-    query, key, value, out, lse, qi, ki, cq, ck = ctx.saved_tensors
+    query, key, value, out, lse, qi, ki, cq, ck, dq_gaps, dkv_gaps = ctx.saved_tensors
+    if dout is None:
+        dout = torch.zeros_like(out)
     dq, dk, dv = strict_varlen_bwd(
-        query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale
+        query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale,
+        dq_gaps, dkv_gaps,
     )
-    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 8
+    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 11
 
 
 strict_varlen_fwd.register_autograd(_varlen_backward, setup_context=_varlen_setup)
@@ -531,13 +597,14 @@ def _hip_attention(query, key, value, query_start, kv_lengths, use_dummy_token, 
     elif metadata is not None:
         if metadata.query_indices.numel() == 0:
             return _zeros_linked(query, key, value, batch, length, heads, dim)
-        _, _, _, top_q, top_k, _ = _schedule_facts(metadata)
+        top_q, top_k = _schedule_facts(metadata)[3:5]
         max_q, max_k, flags = _schedule_flags(metadata)
         if metadata.max_queries != length or top_q >= batch * length or top_k >= batch * key.shape[2]:
             raise ValueError("metadata was prepared for other query/key shapes")
+        gaps = _schedule_gaps(metadata, batch, length, heads, key.shape[2], key.shape[1])
         out, _ = strict_varlen_fwd(
             q, k, v, metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
-            max_q, max_k, flags, scale,
+            max_q, max_k, flags, scale, *gaps,
         )
     else:
         row_offset = row_limit = None

@@ -258,15 +258,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
 }
 
 // ------------------------------------------------------------------ dKV ----
-// One workgroup = 128 keys of one (batch row or segment, kv head), 32 per
-// wave, held in registers. Query and output-gradient tiles of 64 rows for
-// every query head of the group stream through double-buffered LDS
-// (direct-to-LDS loads, the next tile in flight while the current one is
-// computed); each tile is read row-wise for S = Q K^T and dP = dO V^T and
-// with transpose reads for dV^T = dO^T P and dK^T = Q^T dS.
+// One workgroup = 128 keys of one (batch row or segment, kv head) and eight
+// waves: wave pair p (waves p and p + 4, which share SIMD p) owns keys
+// 32p .. 32p + 31. The pair splits the work so each wave holds half of the
+// state and the two waves of a SIMD alternate between matrix and vector work:
+//   wave p     ("S side")  holds K rows, computes S = Q K^T, the mask and
+//              P = exp2(S c log2e - lse), hands P to its partner through LDS
+//              and accumulates dV^T = dO^T P;
+//   wave p + 4 ("dP side") holds V rows, computes dP = dO V^T, takes P and
+//              forms dS = P (dP - delta), and accumulates dK^T = Q^T dS.
+// Query and output-gradient tiles of 64 rows for every query head of the
+// group stream through double-buffered LDS (direct-to-LDS loads); each tile
+// is read row-wise for S and dP and by transpose reads for dV and dK.
 template <int D, int MODE, bool ATOMIC>
-__global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a) {
-  constexpr int BNK = 128, BMQ = 64;
+__global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a) {
+  constexpr int BNK = 128, BMQ = 64, NW = 8;
   static_assert(BMQ == kTileRows, "one LDS tile per query tile");
   constexpr int KS = D / 16, DB = D / 32;
   // two buffers as distinct arrays with static roles (the loop is unrolled
@@ -276,12 +282,16 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   __shared__ __attribute__((aligned(1024))) bf16 q_lds1[kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 g_lds0[kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 g_lds1[kTileElems];
+  // P from the S side to the dP side: [pair][32-row half][register quad][lane]
+  __shared__ __attribute__((aligned(16))) f32x4 p_lds[4][BMQ / 32][4][64];
   __shared__ __attribute__((aligned(16))) float stat_lds[2][2][BMQ];  // lse * log2e, delta
   __shared__ __attribute__((aligned(16))) int qdoc_lds[2][2][BMQ];    // document id, document start
-  __shared__ int red_lds[4];
+  __shared__ int red_lds[NW];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
+  const int pair = wave & 3;
+  const bool dp_side = wave >= 4;  // wave-uniform role
   const int group = a.q_heads / a.kv_heads;
 
   const int ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + BNK - 1) / BNK;
@@ -298,8 +308,8 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   if (n0 >= nk) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
 
-  // this lane's key
-  const int n = n0 + wave * 32 + col;
+  // this lane's key (shared by the two waves of the pair)
+  const int n = n0 + pair * 32 + col;
   const bool valid_k = n < nk;
   bool k_live = valid_k;
   if (MODE == kDense && a.key_mask) k_live = k_live && a.key_mask[(int64_t)b * a.key_mask_stride + min(n, nk - 1)] != 0;
@@ -312,7 +322,7 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
       kqend_n = a.k_qend[(int64_t)b * a.kv_len + n];
     }
   }
-  // query rows that can see any key of the workgroup / of this wave
+  // query rows that can see any key of the workgroup / of this pair
   const int m_begin = (slot0 && n0 == 0) ? 0 : pb.bound.first_row(n0, nq);
   int m_end = nq;
   if constexpr (MODE == kDoc) {
@@ -320,41 +330,39 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
     for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
     if (lane == 0) red_lds[wave] = v;
     __syncthreads();
-    v = max(max(red_lds[0], red_lds[1]), max(red_lds[2], red_lds[3]));
+    v = red_lds[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v = max(v, red_lds[w]);
     m_end = __builtin_amdgcn_readfirstlane(min(m_end, v));  // uniform: keeps the tile loop scalar
   }
-  const int wave_key0 = n0 + wave * 32;
-  const bool wave_live = wave_key0 < nk;
-  const int wave_m_begin = (slot0 && wave_key0 == 0) ? 0 : pb.bound.first_row(wave_key0, nq);
+  const int pair_key0 = n0 + pair * 32;
+  const bool pair_live = pair_key0 < nk;
+  const int pair_m_begin = (slot0 && pair_key0 == 0) ? 0 : pb.bound.first_row(pair_key0, nq);
 
-  bf16x8 kf[KS], vf[KS];
+  // K rows on the S side, V rows on the dP side
+  bf16x8 kvf[KS];
   {
-    const bf16* krow = row_at(a.k, a.k_stride, kb, hk, kslot) + 8 * half;
-    const bf16* vrow = row_at(a.v, a.v_stride, kb, hk, kslot) + 8 * half;
+    const bf16* row = dp_side ? row_at(a.v, a.v_stride, kb, hk, kslot) : row_at(a.k, a.k_stride, kb, hk, kslot);
     const u32x4 z = {0u, 0u, 0u, 0u};
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
-      const u32x4 wk = load16(krow + 16 * s), wv = load16(vrow + 16 * s);
-      kf[s] = as_bf16x8(k_live ? wk : z);
-      vf[s] = as_bf16x8(k_live ? wv : z);
+      const u32x4 w = load16(row + 8 * half + 16 * s);
+      kvf[s] = as_bf16x8(k_live ? w : z);
     }
   }
-
-  f32x16 dkacc[DB], dvacc[DB];
+  // dV^T on the S side, dK^T on the dP side
+  f32x16 acc[DB];
 #pragma unroll
-  for (int d = 0; d < DB; ++d) {
-    dkacc[d] = f32x16{};
-    dvacc[d] = f32x16{};
-  }
+  for (int d = 0; d < DB; ++d) acc[d] = f32x16{};
   const float sl2 = a.softmax_scale * kLog2e;
 
   // ---- query tiles: (head, first row) pairs over the group's heads ----
   const int m_first = (m_begin / BMQ) * BMQ;
   const int nqt = m_end > m_first ? (m_end - m_first + BMQ - 1) / BMQ : 0;
   const int total = nqt * group;
-  TileDMA<D> dma;
+  TileDMA<D, NW> dma;
   dma.init(wave, lane);
-  QueryTiles<MODE, D> qrows;
+  QueryTiles<MODE, D, NW> qrows;
   qrows.init(a, pb, dma);
   RowReads<KS> rrd;
   rrd.init(col, half);
@@ -395,31 +403,34 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
     }
   };
 
-  // One query tile against this wave's 32 keys.
   // first query row that sees this lane's key (INT_MAX for a dead key): the
   // causal/offset rule is then one comparison per score
   const int m_lo = !k_live ? INT_MAX : (slot0 && n == 0) ? 0 : pb.bound.first_row(n, nq);
 
-  // One query tile against this wave's 32 keys, in two halves of 32 query
-  // rows so that only one half's scores are live at a time.
-  auto tile_step = [&](auto bufc, int m0) __attribute__((always_inline)) {
+  // One query tile against the pair's 32 keys: the first half runs before
+  // the P hand-over barrier, the second after it.
+  f32x16 tacc[BMQ / 32];  // S side: P; dP side: dP, then dS
+  // Each role reads its own tile through a compile-time base (a runtime
+  // choice between two LDS arrays would hide from the compiler that the
+  // prefetch never writes them, and it would wait for the prefetch).
+  auto first_half = [&](auto bufc, auto sidec, int m0) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
-    const bf16* qt = B ? q_lds1 : q_lds0;
-    const bf16* gt = B ? g_lds1 : g_lds0;
+    constexpr bool DP = decltype(sidec)::value;
+    const bf16* rows = DP ? (B ? g_lds1 : g_lds0) : (B ? q_lds1 : q_lds0);  // dO rows for dP, Q rows for S
     rrd.refresh();
-    trd.refresh();
-    // every pair of the tile is visible to this wave: no per-element mask
-    const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= wave_m_begin &&
-                      m0 + BMQ <= nq && pb.bound.lim(m0) >= wave_key0 + 31;
+#pragma unroll
+    for (int mb = 0; mb < BMQ / 32; ++mb) {
+      tacc[mb] = f32x16{};
+#pragma unroll
+      for (int s = 0; s < KS; ++s) tacc[mb] = mfma32(rrd.get(rows, s, mb), kvf[s], tacc[mb]);
+    }
+    if constexpr (DP) return;
+    // every pair of the tile is visible to this pair's keys: no per-element mask
+    const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= pair_m_begin &&
+                      m0 + BMQ <= nq && pb.bound.lim(m0) >= pair_key0 + 31;
     const int lo = m_lo - m0, hi = nq - m0;  // rows ml in [lo, hi) see the key
 #pragma unroll
     for (int mb = 0; mb < BMQ / 32; ++mb) {
-      f32x16 sacc = f32x16{}, pacc = f32x16{};
-#pragma unroll
-      for (int s = 0; s < KS; ++s) {
-        sacc = mfma32(rrd.get(qt, s, mb), kf[s], sacc);
-        pacc = mfma32(rrd.get(gt, s, mb), vf[s], pacc);
-      }
       if (!full) {
         // keeps this block a real (wave-uniform) branch instead of selects
         __asm__ volatile("");
@@ -431,34 +442,47 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
             const int qsg = qdoc_lds[B][0][ml], qst = qdoc_lds[B][1][ml];
             keep = keep & (((qsg == kseg_n) & (n >= qst)) | (kseg_n == -1)) & (m0 + ml < kqend_n);
           }
-          sacc[r] = keep ? sacc[r] : kNegInf;
+          tacc[mb][r] = keep ? tacc[mb][r] : kNegInf;
         }
       }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
         const int ml = mb * 32 + 8 * g + 4 * half;
         const f32x4 l4 = *reinterpret_cast<const f32x4*>(&stat_lds[B][0][ml]);
-        const f32x4 d4 = *reinterpret_cast<const f32x4*>(&stat_lds[B][1][ml]);
+        f32x4 p4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int r = 4 * g + e;
           // a masked score is -inf and gives p = 0 exactly (lse is finite or +inf)
-          const float p = __builtin_amdgcn_exp2f(fmaf(sacc[r], sl2, -l4[e]));
-          sacc[r] = p;
-          pacc[r] = p * (pacc[r] - d4[e]);
+          p4[e] = __builtin_amdgcn_exp2f(fmaf(tacc[mb][4 * g + e], sl2, -l4[e]));
+          tacc[mb][4 * g + e] = p4[e];
+        }
+        p_lds[pair][mb][g][lane] = p4;
+      }
+    }
+  };
+  auto second_half = [&](auto bufc, auto sidec) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    constexpr bool DP = decltype(sidec)::value;
+    trd.refresh();
+    if constexpr (DP) {
+#pragma unroll
+      for (int mb = 0; mb < BMQ / 32; ++mb) {
+#pragma unroll
+        for (int g = 0; g < 4; ++g) {
+          const int ml = mb * 32 + 8 * g + 4 * half;
+          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&stat_lds[B][1][ml]);
+          const f32x4 p4 = p_lds[pair][mb][g][lane];
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tacc[mb][4 * g + e] = p4[e] * (tacc[mb][4 * g + e] - d4[e]);
         }
       }
+    }
+    const bf16* tr = DP ? (B ? q_lds1 : q_lds0) : (B ? g_lds1 : g_lds0);  // Q^T for dK, dO^T for dV
 #pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const int s = 2 * mb + h2;
-        const bf16x8 pop = acc_kperm_operand(sacc, s);
-        const bf16x8 dsop = acc_kperm_operand(pacc, s);
+    for (int s = 0; s < BMQ / 16; ++s) {
+      const bf16x8 op = acc_kperm_operand(tacc[s >> 1], s);
 #pragma unroll
-        for (int d = 0; d < DB; ++d) {
-          dvacc[d] = mfma32(trd.get(gt, d, s), pop, dvacc[d]);
-          dkacc[d] = mfma32(trd.get(qt, d, s), dsop, dkacc[d]);
-        }
-      }
+      for (int d = 0; d < DB; ++d) acc[d] = mfma32(trd.get(tr, d, s), op, acc[d]);
     }
   };
 
@@ -473,9 +497,11 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   };
   auto iteration = [&](auto bufc, int it) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
-    const int hq = hq_cur, m0 = m_cur;
-    int hn = hq, mn = m0;
+    const int m0 = m_cur;
+    int hn = hq_cur, mn = m0;
     advance(hn, mn);
+    // tile `it` has landed; every wave is done with the other buffer and
+    // every dP-side wave has taken the previous P
     dma_barrier();
     const bool more = it + 1 < total;
     RowMeta next{};
@@ -483,8 +509,24 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
       qrows.issue(a, pb, dma, hn, mn, B ? q_lds0 : q_lds1, B ? g_lds0 : g_lds1);
       next = load_meta(hn, mn);
     }
-    (void)hq;
-    if (wave_live && m0 + BMQ > wave_m_begin) tile_step(bufc, m0);
+    const bool active = pair_live && m0 + BMQ > pair_m_begin;  // uniform over the pair
+    using S_side = std::integral_constant<bool, false>;
+    using DP_side = std::integral_constant<bool, true>;
+    if (active) {
+      if (dp_side) {
+        first_half(bufc, DP_side{}, m0);
+      } else {
+        first_half(bufc, S_side{}, m0);
+      }
+    }
+    __syncthreads();  // P of this tile is in LDS
+    if (active) {
+      if (dp_side) {
+        second_half(bufc, DP_side{});
+      } else {
+        second_half(bufc, S_side{});
+      }
+    }
     if (more) store_meta(std::integral_constant<int, B ^ 1>{}, next);
     hq_cur = hn;
     m_cur = mn;
@@ -500,23 +542,23 @@ __global__ __launch_bounds__(256) void attn_bwd_dkv_kernel(const wmx_attn_args a
   }
 
   if (!valid_k) return;
+  const float scale = dp_side ? a.softmax_scale : 1.f;
   if constexpr (ATOMIC) {
-    // fp32 accumulators laid out [key row][kv head][D]
+    // fp32 accumulators laid out [key row][kv head][D]; dK first, then dV
     const int64_t row = (int64_t)kb * a.key_extent + kslot;
-    float* acck = (float*)a.workspace + (row * a.kv_heads + hk) * D;
-    float* accv = acck + (int64_t)a.batch * a.key_extent * a.kv_heads * D;
+    float* dst = (float*)a.workspace + (row * a.kv_heads + hk) * D +
+                 (dp_side ? 0 : (int64_t)a.batch * a.key_extent * a.kv_heads * D);
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
 #pragma unroll
       for (int r = 0; r < 16; ++r) {
         const int dd = d * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-        atomicAdd(acck + dd, dkacc[d][r] * a.softmax_scale);
-        atomicAdd(accv + dd, dvacc[d][r]);
+        atomicAdd(dst + dd, acc[d][r] * scale);
       }
     }
   } else {
-    store_acc_row<DB>((bf16*)row_at(a.dk, a.dk_stride, kb, hk, kslot), dkacc, a.softmax_scale, half);
-    store_acc_row<DB>((bf16*)row_at(a.dv, a.dv_stride, kb, hk, kslot), dvacc, 1.f, half);
+    bf16* dst = dp_side ? (bf16*)row_at(a.dk, a.dk_stride, kb, hk, kslot) : (bf16*)row_at(a.dv, a.dv_stride, kb, hk, kslot);
+    store_acc_row<DB>(dst, acc, scale, half);
   }
 }
 
@@ -588,11 +630,11 @@ static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
     const int64_t n = bwd_workspace_size(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,
                        (float*)a.workspace, n);
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true>), grid, dim3(512), 0, stream, a);
     const int64_t total = n / 2;
     hipLaunchKernelGGL(acc_to_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false>), grid, dim3(256), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false>), grid, dim3(512), 0, stream, a);
   }
   return WMX_OK;
 }

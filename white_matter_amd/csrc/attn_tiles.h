@@ -102,18 +102,18 @@ __device__ __forceinline__ const bf16* row_at(const void* base, const int64_t* s
 // slots from key 1 on) a tile is a strided load from a per-tile base;
 // otherwise, and under a key mask (masked-out slots may hold anything), each
 // row is located and gathered.
-template <int MODE, int D>
+template <int MODE, int D, int NW = 4>
 struct KeyTiles {
   const bf16 *kslice, *vslice;  // slot 0 of the keys' row, kv head hk
   int64_t kst, vst;             // slot strides (elements)
   int kfirst;                   // strided: key j at slot kfirst + j
   int reach;
   bool strided;
-  unsigned koff[4], voff[4];
+  unsigned koff[TileDMA<D, NW>::kInstr], voff[TileDMA<D, NW>::kInstr];
   int b, hk, nk;
 
   __device__ __forceinline__ void init(const wmx_attn_args& a, const Problem<MODE>& pb, int hk_, int reach_,
-                                       const TileDMA<D>& dma) {
+                                       const TileDMA<D, NW>& dma) {
     b = pb.b;
     hk = hk_;
     nk = pb.nk;
@@ -145,7 +145,7 @@ struct KeyTiles {
   }
 
   template <class Args>
-  __device__ __forceinline__ void issue(const Args& a, const Problem<MODE>& pb, const TileDMA<D>& dma, int n0,
+  __device__ __forceinline__ void issue(const Args& a, const Problem<MODE>& pb, const TileDMA<D, NW>& dma, int n0,
                                         bf16* ktile, bf16* vtile) const {
     if (strided && (MODE != kVarlen || n0 > 0)) {
       const int nvalid = min(max(reach - n0, 0), kTileRows);
@@ -174,7 +174,7 @@ struct KeyTiles {
 // and dO share the row addressing), for any query head. Rows past nq read as
 // zeros. Dense rows and varlen segments with consecutive query slots are
 // strided loads; other varlen layouts gather each row.
-template <int MODE, int D>
+template <int MODE, int D, int NW = 4>
 struct QueryTiles {
   const bf16 *qslice, *gslice;  // slot 0 of the queries' row, head 0
   int64_t qst, gst, qhs, ghs;   // slot and head strides (elements)
@@ -182,7 +182,7 @@ struct QueryTiles {
   int nq;
   bool strided;
 
-  __device__ __forceinline__ void init(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D>& dma) {
+  __device__ __forceinline__ void init(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D, NW>& dma) {
     nq = pb.nq;
     int qb0 = pb.b;
     qfirst = 0;
@@ -200,7 +200,7 @@ struct QueryTiles {
     strided = layout_ok && stride_ok;
   }
 
-  __device__ __forceinline__ void issue(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D>& dma,
+  __device__ __forceinline__ void issue(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D, NW>& dma,
                                         int hq, int m0, bf16* qtile, bf16* gtile) const {
     if (strided) {
       const int nvalid = min(max(nq - m0, 0), kTileRows);

@@ -127,14 +127,16 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
 // Source of the zero rows of gathered tiles.
 static __device__ __attribute__((aligned(16))) const uint32_t kZeroChunk[4] = {0u, 0u, 0u, 0u};
 
-// This thread's four 16-byte slots of a 64-row tile (256 threads = 4 waves,
-// each wave filling 16 rows with 4 instructions).
-template <int D>
+// This thread's 16-byte slots of a 64-row tile filled by NW waves: each wave
+// fills 64 / NW rows with 16 / NW instructions of 4 rows.
+template <int D, int NW = 4>
 struct TileDMA {
-  // Instruction r of wave w fills tile row (4 w + r) * 4 + sub, sub = lane / 16,
-  // whose swizzle is 4 sub + r: the lane loads logical chunk lc0 ^ r with
-  // lc0 = (lane % 16) ^ 4 sub. Only these three values are kept; rows and
-  // offsets are formed per use.
+  static constexpr int kInstr = 16 / NW;  // instructions per wave per tile
+  static_assert(NW == 4 || NW == 8, "4 or 8 waves fill a tile");
+  // Instruction r of wave w fills tile row 4 g + sub, g = kInstr w + r and
+  // sub = lane / 16, whose swizzle is 4 sub + g % 4: the lane loads logical
+  // chunk lc0 ^ (g % 4) with lc0 = (lane % 16) ^ 4 sub. Only these values are
+  // kept; rows and offsets are formed per use.
   int wave, sub, lc0;
 
   __device__ __forceinline__ void init(int wave_, int lane) {
@@ -142,33 +144,33 @@ struct TileDMA {
     sub = lane >> 4;
     lc0 = (lane & 15) ^ (sub << 2);
   }
-  __device__ __forceinline__ int row(int r) const { return (wave * 4 + r) * 4 + sub; }
+  __device__ __forceinline__ int group(int r) const { return wave * kInstr + r; }
+  __device__ __forceinline__ int row(int r) const { return group(r) * 4 + sub; }
   // byte offset of this lane's chunk of instruction r in its row, or -1 for padding
   __device__ __forceinline__ int chunk16(int r) const {
-    const int c = lc0 ^ r;
+    const int c = lc0 ^ (group(r) & 3);
     return (D == 128 || c < D / 8) ? 16 * c : -1;
   }
+  __device__ __forceinline__ lds_void* dst(bf16* tile, int r) const { return (lds_void*)(tile + group(r) * 512); }
   // Per-lane byte offset of instruction r of a strided tile with row stride
   // row_bytes (0 <= row_bytes * 64 < 2^31).
   __device__ __forceinline__ unsigned strided_offset(int r, int row_bytes) const {
     const int c = chunk16(r);
     return c < 0 ? kOutOfRange : (unsigned)(row(r) * row_bytes + c);
   }
-  __device__ __forceinline__ void strided_offsets(int row_bytes, unsigned (&off)[4]) const {
+  __device__ __forceinline__ void strided_offsets(int row_bytes, unsigned (&off)[kInstr]) const {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) off[r] = strided_offset(r, row_bytes);
+    for (int r = 0; r < kInstr; ++r) off[r] = strided_offset(r, row_bytes);
   }
-  __device__ __forceinline__ void issue_strided(const rsrc_t& rs, bf16* tile, const unsigned (&off)[4]) const {
+  __device__ __forceinline__ void issue_strided(const rsrc_t& rs, bf16* tile, const unsigned (&off)[kInstr]) const {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + (wave * 4 + r) * 512), 16, off[r], 0, 0, 0);
+    for (int r = 0; r < kInstr; ++r) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst(tile, r), 16, off[r], 0, 0, 0);
   }
   // Offsets formed at issue time (no registers held between tiles).
   __device__ __forceinline__ void issue_strided_rows(const rsrc_t& rs, bf16* tile, int row_bytes) const {
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)(tile + (wave * 4 + r) * 512), 16,
-                                               strided_offset(r, row_bytes), 0, 0, 0);
+    for (int r = 0; r < kInstr; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst(tile, r), 16, strided_offset(r, row_bytes), 0, 0, 0);
   }
   // Two tiles whose rows are located together: rows(tr, ok, p0, p1) returns
   // the addresses of tile row tr and sets ok = false for a row that must read
@@ -176,7 +178,7 @@ struct TileDMA {
   template <class Rows>
   __device__ __forceinline__ void issue_gathered2(bf16* t0, bf16* t1, Rows rows) const {
 #pragma unroll
-    for (int r = 0; r < 4; ++r) {
+    for (int r = 0; r < kInstr; ++r) {
       bool ok;
       const bf16 *p0, *p1;
       rows(row(r), ok, p0, p1);
@@ -184,8 +186,8 @@ struct TileDMA {
       const bool use = ok && c >= 0;
       const void* s0 = use ? (const void*)((const char*)p0 + c) : (const void*)kZeroChunk;
       const void* s1 = use ? (const void*)((const char*)p1 + c) : (const void*)kZeroChunk;
-      __builtin_amdgcn_global_load_lds(s0, (lds_void*)(t0 + (wave * 4 + r) * 512), 16, 0, 0);
-      __builtin_amdgcn_global_load_lds(s1, (lds_void*)(t1 + (wave * 4 + r) * 512), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(s0, dst(t0, r), 16, 0, 0);
+      __builtin_amdgcn_global_load_lds(s1, dst(t1, r), 16, 0, 0);
     }
   }
 };

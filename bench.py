@@ -110,13 +110,15 @@ def kernel_times(q, k, v, metadata, reps):
     """Average duration (ms) of each kernel of one forward+backward, launched
     alone through the C ABI between HIP events on the current stream."""
     from white_matter_amd import _kernels, _native
-    from white_matter_amd.strict_causal_attention import _schedule_flags
+    from white_matter_amd.strict_causal_attention import _schedule_flags, _work_units
 
     batch, heads, length, dim = q.shape
     max_q, max_k, flags = _schedule_flags(metadata)
+    q_units, k_units = _work_units(metadata)
     varlen = _kernels.Varlen(
         metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
         metadata.cu_queries.numel() - 1, max_q, max_k, length, k.shape[2], bool(flags & 16), flags & 15,
+        q_units, k_units,
     )
     vis = _kernels.Visibility(varlen=varlen)
     out = torch.zeros(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)

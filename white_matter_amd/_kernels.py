@@ -71,6 +71,8 @@ class Varlen:
     key_extent: int
     keys_unique: bool
     segment_layout: int = 0  # bit 0 consecutive queries, bit 1 consecutive keys from key 1
+    q_units: torch.Tensor | None = None  # int32 (n, 2) (segment, query tile), heaviest first
+    k_units: torch.Tensor | None = None  # int32 (n, 2) (segment, key tile), heaviest first
 
 
 @dataclass
@@ -110,6 +112,10 @@ class Visibility:
             args.key_extent = s.key_extent
             args.keys_unique = int(s.keys_unique)
             args.segment_layout = s.segment_layout
+            if s.q_units is not None:
+                args.q_units, args.num_q_units = s.q_units.data_ptr(), s.q_units.shape[0]
+            if s.k_units is not None:
+                args.k_units, args.num_k_units = s.k_units.data_ptr(), s.k_units.shape[0]
 
 
 def _base_args(q, k, v, o, lse, scale: float, vis: Visibility, q_len: int) -> _native.AttnArgs:

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -75,6 +75,10 @@ class AttnArgs(ctypes.Structure):
         ("key_extent", ctypes.c_int32),
         ("segment_layout", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float),
+        ("q_units", _vp),
+        ("k_units", _vp),
+        ("num_q_units", ctypes.c_int32),
+        ("num_k_units", ctypes.c_int32),
     ]
 
 

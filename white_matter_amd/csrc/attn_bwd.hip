@@ -60,7 +60,8 @@ __global__ __launch_bounds__(256) void bwd_delta_kernel(const wmx_attn_args a, i
 // through double-buffered LDS exactly as in the forward; the K tile is read
 // row-wise for S^T = K Q^T and with transpose reads for dQ^T = K^T dS^T.
 template <int D, int MODE>
-__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args a) {
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args args) {
+  const wmx_attn_args& a = args;
   constexpr int BM = 128, BN = 64;
   static_assert(BN == kTileRows, "one LDS tile per key tile");
   constexpr int KS = D / 16, DB = D / 32;
@@ -72,17 +73,21 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   __shared__ int meta_lds[2][2][BN];  // per buffer: key ids (or key mask), key query ends
   __shared__ int red_lds[4];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int half = lane >> 5, col = lane & 31;
-
   const int qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
   const unsigned outer = MODE == kVarlen ? (unsigned)a.num_segments : (unsigned)a.batch;
-  unsigned unit;
-  if (!logical_unit((unsigned)qtiles * outer * a.q_heads, unit)) return;
-  const int q0 = (qtiles - 1 - (int)(unit % qtiles)) * BM;
-  const unsigned rest = unit / qtiles;
-  const int h = MODE == kVarlen ? (int)(rest / outer) : (int)(rest % a.q_heads);
-  const int grp = MODE == kVarlen ? (int)(rest % outer) : (int)(rest / a.q_heads);
+  const int32_t* list = MODE == kVarlen ? a.q_units : nullptr;
+  const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
+
+  // One unit: 128 query rows of one (batch row or segment, query head).
+  auto process = [&](const TileUnit& tu) __attribute__((always_inline)) {
+  // per-lane constants are formed inside each unit (not hoisted and held
+  // in registers across the unit loop)
+  int tid = threadIdx.x;
+  opaque(tid);
+  const int lane = tid & 63, wave = wave_id();
+  const int half = lane >> 5, col = lane & 31;
+  const int q0 = tu.tile * BM;
+  const int h = tu.head, grp = tu.grp;
   const int hk = h / (a.q_heads / a.kv_heads);
   Problem<MODE> pb;
   pb.init(a, grp);
@@ -255,6 +260,17 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   if (!valid_q) return;
   bf16* dqrow = (bf16*)row_at(a.dq, a.dq_stride, qb, h, qt);
   store_acc_row<DB>(dqrow, dqacc, a.softmax_scale, half);
+  };
+
+  WorkRange work;
+  work.init(count * (uint32_t)a.q_heads);
+  uint32_t unit;
+  while (work.take(unit)) {
+    TileUnit tu;
+    tu.decode(unit, count, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+    __syncthreads();  // every wave is done with the previous unit's LDS tiles
+    if (tu.ok) process(tu);
+  }
 }
 
 // ------------------------------------------------------------------ dKV ----
@@ -271,7 +287,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
 // group stream through double-buffered LDS (direct-to-LDS loads); each tile
 // is read row-wise for S and dP and by transpose reads for dV and dK.
 template <int D, int MODE, bool ATOMIC>
-__global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a) {
+__global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args args) {
+  const wmx_attn_args& a = args;
   constexpr int BNK = 128, BMQ = 64, NW = 8;
   static_assert(BMQ == kTileRows, "one LDS tile per query tile");
   constexpr int KS = D / 16, DB = D / 32;
@@ -288,20 +305,25 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   __shared__ __attribute__((aligned(16))) int qdoc_lds[2][2][BMQ];    // document id, document start
   __shared__ int red_lds[NW];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int half = lane >> 5, col = lane & 31;
-  const int pair = wave & 3;
-  const bool dp_side = wave >= 4;  // wave-uniform role
   const int group = a.q_heads / a.kv_heads;
 
   const int ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + BNK - 1) / BNK;
   const unsigned outer = MODE == kVarlen ? (unsigned)a.num_segments : (unsigned)a.batch;
-  unsigned unit;
-  if (!logical_unit((unsigned)ktiles * outer * a.kv_heads, unit)) return;
-  const int n0 = (int)(unit % ktiles) * BNK;  // low key tiles are read by the most queries
-  const unsigned rest = unit / ktiles;
-  const int hk = MODE == kVarlen ? (int)(rest / outer) : (int)(rest % a.kv_heads);
-  const int grp = MODE == kVarlen ? (int)(rest % outer) : (int)(rest / a.kv_heads);
+  const int32_t* list = MODE == kVarlen ? a.k_units : nullptr;
+  const uint32_t count = list ? (uint32_t)a.num_k_units : (uint32_t)ktiles * outer;
+
+  // One unit: 128 keys of one (batch row or segment, kv head).
+  auto process = [&](const TileUnit& tu) __attribute__((always_inline)) {
+  // per-lane constants are formed inside each unit (not hoisted and held
+  // in registers across the unit loop)
+  int tid = threadIdx.x;
+  opaque(tid);
+  const int lane = tid & 63, wave = wave_id();
+  const int half = lane >> 5, col = lane & 31;
+  const int pair = wave & 3;
+  const bool dp_side = wave >= 4;  // wave-uniform role
+  const int n0 = tu.tile * BNK;
+  const int hk = tu.head, grp = tu.grp;
   Problem<MODE> pb;
   pb.init(a, grp);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
@@ -560,6 +582,17 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     bf16* dst = dp_side ? (bf16*)row_at(a.dk, a.dk_stride, kb, hk, kslot) : (bf16*)row_at(a.dv, a.dv_stride, kb, hk, kslot);
     store_acc_row<DB>(dst, acc, scale, half);
   }
+  };
+
+  WorkRange work;
+  work.init(count * (uint32_t)a.kv_heads);
+  uint32_t unit;
+  while (work.take(unit)) {
+    TileUnit tu;
+    tu.decode(unit, count, ktiles, list, (int)outer, false);  // low key tiles see the most queries
+    __syncthreads();  // every wave is done with the previous unit's LDS tiles
+    if (tu.ok) process(tu);
+  }
 }
 
 // ----------------------------------------------- varlen accumulator glue ----
@@ -614,18 +647,27 @@ int64_t bwd_workspace_size(const wmx_attn_args& a) {
 template <int D, int MODE>
 static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + 127) / 128;
-  const int64_t units = qtiles * (MODE == kVarlen ? a.num_segments : a.batch) * a.q_heads;
+  const int64_t per_head =
+      (MODE == kVarlen && a.q_units) ? a.num_q_units : qtiles * (MODE == kVarlen ? a.num_segments : a.batch);
+  const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)logical_grid(units)), dim3(256), 0, stream, a);
+  if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
+  // two workgroups per compute unit (256 VGPRs x 4 waves, 65 KB LDS each)
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)persistent_grid(units, 2)), dim3(256), 0, stream,
+                     a);
   return WMX_OK;
 }
 
 template <int D, int MODE>
 static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + 127) / 128;
-  const int64_t units = ktiles * (MODE == kVarlen ? a.num_segments : a.batch) * a.kv_heads;
+  const int64_t per_head =
+      (MODE == kVarlen && a.k_units) ? a.num_k_units : ktiles * (MODE == kVarlen ? a.num_segments : a.batch);
+  const int64_t units = per_head * a.kv_heads;
   if (units <= 0) return WMX_OK;
-  const dim3 grid((unsigned)logical_grid(units));
+  if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
+  // one 8-wave workgroup per compute unit (2 waves per SIMD, 99 KB LDS)
+  const dim3 grid((unsigned)persistent_grid(units, 1));
   if (MODE == kVarlen && !a.keys_unique) {
     const int64_t n = bwd_workspace_size(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,

@@ -33,7 +33,8 @@ constexpr int kFwdBM = 128;  // query rows per workgroup
 constexpr int kFwdBN = 64;   // keys per tile
 
 template <int D, int MODE>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a) {
+__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args args) {
+  const wmx_attn_args& a = args;
   constexpr int BM = kFwdBM, BN = kFwdBN;
   static_assert(BN == kTileRows, "one LDS tile per key tile");
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
@@ -50,18 +51,22 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
   __shared__ int meta_lds[2][2][BN];  // per buffer: key ids (or key mask), key query ends
   __shared__ int red_lds[4];
 
-  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
-  const int half = lane >> 5, col = lane & 31;
-
-  // ---- resolve the problem this workgroup works on ----
+  // ---- the work units: (batch row or segment, query tile, head) ----
   const int qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
   const unsigned outer = MODE == kVarlen ? (unsigned)a.num_segments : (unsigned)a.batch;
-  unsigned unit;
-  if (!logical_unit((unsigned)qtiles * outer * a.q_heads, unit)) return;
-  const int q0 = (qtiles - 1 - (int)(unit % qtiles)) * BM;
-  const unsigned rest = unit / qtiles;
-  const int h = MODE == kVarlen ? (int)(rest / outer) : (int)(rest % a.q_heads);
-  const int grp = MODE == kVarlen ? (int)(rest % outer) : (int)(rest / a.q_heads);
+  const int32_t* list = MODE == kVarlen ? a.q_units : nullptr;
+  const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
+
+  // One unit: 128 query rows of one (batch row or segment, query head).
+  auto process = [&](const TileUnit& tu) __attribute__((always_inline)) {
+  // per-lane constants are formed inside each unit (not hoisted and held
+  // in registers across the unit loop)
+  int tid = threadIdx.x;
+  opaque(tid);
+  const int lane = tid & 63, wave = wave_id();
+  const int half = lane >> 5, col = lane & 31;
+  const int q0 = tu.tile * BM;
+  const int h = tu.head, grp = tu.grp;
   const int hk = h / (a.q_heads / a.kv_heads);
   Problem<MODE> pb;
   pb.init(a, grp);
@@ -286,17 +291,29 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args a)
     const float lse = l_run > 0.f ? (m_run + __log2f(l_run)) * kLn2 : kPosInf;
     a.lse[((int64_t)qb * a.q_heads + h) * a.q_len + qt] = lse;
   }
+  };
+
+  WorkRange work;
+  work.init(count * (uint32_t)a.q_heads);
+  uint32_t unit;
+  while (work.take(unit)) {
+    TileUnit tu;
+    tu.decode(unit, count, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+    __syncthreads();  // every wave is done with the previous unit's LDS tiles
+    if (tu.ok) process(tu);
+  }
 }
 
 template <int D, int MODE>
 static int launch_fwd_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + kFwdBM - 1) / kFwdBM;
   const int64_t outer = MODE == kVarlen ? a.num_segments : a.batch;
-  const int64_t units = qtiles * outer * a.q_heads;
+  const int64_t per_head = (MODE == kVarlen && a.q_units) ? a.num_q_units : qtiles * outer;
+  const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
-  const int64_t blocks = logical_grid(units);
-  if (blocks > INT_MAX) return WMX_E_UNSUPPORTED;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), dim3((unsigned)blocks), dim3(256), 0, stream, a);
+  if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
+  // two workgroups per compute unit (256 VGPRs x 4 waves, 65 KB LDS each)
+  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), dim3((unsigned)persistent_grid(units, 2)), dim3(256), 0, stream, a);
   return WMX_OK;
 }
 

@@ -55,6 +55,10 @@ int check_common(const wmx_attn_args* a, bool backward) {
     if (a->q_seg) return fail(WMX_E_INVALID, "varlen schedule and document metadata are exclusive");
     if (a->key_mask) return fail(WMX_E_INVALID, "varlen schedule and key_mask are exclusive");
     if (a->row_offset || a->row_limit) return fail(WMX_E_INVALID, "varlen schedule takes no row offsets");
+    if ((a->q_units && a->num_q_units < 0) || (a->k_units && a->num_k_units < 0))
+      return fail(WMX_E_INVALID, "negative work-list length");
+  } else if (a->q_units || a->k_units) {
+    return fail(WMX_E_INVALID, "work lists need a varlen schedule");
   }
   if (a->q_seg && (!a->k_seg || !a->q_start || !a->k_qend))
     return fail(WMX_E_INVALID, "document metadata needs all four arrays");
@@ -86,6 +90,25 @@ int launched(int rc) {
 }
 
 }  // namespace
+
+namespace wmx {
+
+int64_t persistent_grid(int64_t units, int per_cu) {
+  // compute units per device, read once per device
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
+  if (cus[dev] <= 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  const int64_t slots = (int64_t)cus[dev] * per_cu / 8 * 8;
+  const int64_t want = (units + 7) / 8 * 8;
+  return want < slots ? want : (slots > 0 ? slots : 8);
+}
+
+}  // namespace wmx
 
 extern "C" {
 

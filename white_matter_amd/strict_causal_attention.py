@@ -368,7 +368,39 @@ def _schedule_gaps(
     return gaps
 
 
-def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, max_k, flags):
+_TILE = 128  # rows of the kernels' query and key tiles
+
+
+def _work_units(metadata: StrictCausalMetadata) -> tuple[torch.Tensor, torch.Tensor]:
+    """The (segment, 128-row tile) units of the query-tiled kernels (forward,
+    dQ) and of the key-tiled kernel (dK/dV), heaviest first, as int32 (n, 2)
+    device tensors cached on the metadata object. Segments are bottom-right
+    causal: query i of a segment with nq queries and nk keys sees keys
+    0 .. nk - nq + i, which gives each tile's number of visible pairs."""
+    units = metadata.__dict__.get("_units")
+    if units is None:
+        q_units, k_units = [], []
+        for s, (qs, qe, ks, ke) in enumerate(metadata.segments):
+            nq, nk = qe - qs, ke - ks
+            off = nk - nq
+            for t in range(0, -(-nq // _TILE)):
+                rows = range(t * _TILE, min(nq, (t + 1) * _TILE))
+                q_units.append((sum(min(nk, max(0, off + r + 1)) for r in (rows[0], rows[-1])) * len(rows), s, t))
+            for t in range(0, -(-nk // _TILE)):
+                keys = range(t * _TILE, min(nk, (t + 1) * _TILE))
+                k_units.append((sum(max(0, nq - max(0, j - off)) for j in (keys[0], keys[-1])) * len(keys), s, t))
+        device = metadata.query_indices.device
+
+        def table(entries):
+            entries.sort(key=lambda e: -e[0])
+            flat = [v for _, seg, tile in entries for v in (seg, tile)]
+            return torch.tensor(flat, dtype=torch.int32).view(-1, 2).to(device)
+
+        units = metadata.__dict__["_units"] = (table(q_units), table(k_units))
+    return units
+
+
+def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, max_k, flags, q_units=None, k_units=None):
     return _kernels.Varlen(
         query_indices=query_indices.contiguous(),
         key_indices=key_indices.contiguous(),
@@ -381,6 +413,8 @@ def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, 
         key_extent=key.shape[2],
         keys_unique=bool(flags & _KEYS_UNIQUE),
         segment_layout=flags & 15,
+        q_units=q_units,
+        k_units=k_units,
     )
 
 
@@ -400,11 +434,14 @@ def strict_varlen_fwd(
     out_gaps: torch.Tensor,
     dq_gaps: torch.Tensor,
     dkv_gaps: torch.Tensor,
+    q_units: torch.Tensor,
+    k_units: torch.Tensor,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Packed-segment attention read straight from (B, H, T, D) storage;
     output (B, T, H, D) with zeros for the queries outside every segment
     (`out_gaps`: rows of the (B*T, H*D) view). `dq_gaps` and `dkv_gaps`
-    (see _schedule_gaps) are kept for the backward."""
+    (see _schedule_gaps) are kept for the backward; `q_units` and `k_units`
+    are the kernels' work lists (see _work_units)."""
     q, k, v = (_kernels.operand(t) for t in (query, key, value))
     batch, heads, length, dim = q.shape
     out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
@@ -412,7 +449,9 @@ def strict_varlen_fwd(
         out.view(batch * length, heads * dim).index_fill_(0, out_gaps, 0)
     lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
     vis = _kernels.Visibility(
-        varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags)
+        varlen=_varlen(
+            q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags, q_units, k_units
+        )
     )
     _kernels.forward(q, k, v, out.transpose(1, 2), lse, scale, vis)
     return out, lse
@@ -445,6 +484,8 @@ def strict_varlen_bwd(
     scale: float,
     dq_gaps: torch.Tensor,
     dkv_gaps: torch.Tensor,
+    q_units: torch.Tensor,
+    k_units: torch.Tensor,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients of strict_varlen_fwd; the rows no segment writes (`dq_gaps`
     of the (B*H*T, D) view of dQ, `dkv_gaps` of the (B*Hkv*N, D) views of dK
@@ -462,7 +503,9 @@ def strict_varlen_bwd(
         dk.view(-1, dim).index_fill_(0, dkv_gaps, 0)
         dv.view(-1, dim).index_fill_(0, dkv_gaps, 0)
     vis = _kernels.Visibility(
-        varlen=_varlen(q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags)
+        varlen=_varlen(
+            q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags, q_units, k_units
+        )
     )
     _kernels.backward(q, k, v, o, lse, g, dq, dk, dv, scale, vis)
     return dq, dk, dv
@@ -478,21 +521,21 @@ def _(query, key, value, *args):
 
 
 def _varlen_setup(ctx, inputs, output):
-    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale, _, dq_gaps, dkv_gaps = inputs
+    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale, _, dq_gaps, dkv_gaps, qu, ku = inputs
     ctx.dtypes = (query.dtype, key.dtype, value.dtype)
-    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck, dq_gaps, dkv_gaps)
+    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck, dq_gaps, dkv_gaps, qu, ku)
     ctx.set_materialize_grads(False)  # the LSE output has no gradient: no zero fill for it
 
 
 def _varlen_backward(ctx, dout, dlse):
-    query, key, value, out, lse, qi, ki, cq, ck, dq_gaps, dkv_gaps = ctx.saved_tensors
+    query, key, value, out, lse, qi, ki, cq, ck, dq_gaps, dkv_gaps, qu, ku = ctx.saved_tensors
     if dout is None:
         dout = torch.zeros_like(out)
     dq, dk, dv = strict_varlen_bwd(
         query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale,
-        dq_gaps, dkv_gaps,
+        dq_gaps, dkv_gaps, qu, ku,
     )
-    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 11
+    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 13
 
 
 strict_varlen_fwd.register_autograd(_varlen_backward, setup_context=_varlen_setup)
@@ -604,7 +647,7 @@ def _hip_attention(query, key, value, query_start, kv_lengths, use_dummy_token, 
         gaps = _schedule_gaps(metadata, batch, length, heads, key.shape[2], key.shape[1])
         out, _ = strict_varlen_fwd(
             q, k, v, metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
-            max_q, max_k, flags, scale, *gaps,
+            max_q, max_k, flags, scale, *gaps, *_work_units(metadata),
         )
     else:
         row_offset = row_limit = None

@@ -78,13 +78,13 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   const int32_t* list = MODE == kVarlen ? a.q_units : nullptr;
   const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
 
-  // One unit: 128 query rows of one (batch row or segment, query head).
-  auto process = [&](const TileUnit& tu) __attribute__((always_inline)) {
-  // per-lane constants are formed inside each unit (not hoisted and held
-  // in registers across the unit loop)
-  int tid = threadIdx.x;
-  opaque(tid);
-  const int lane = tid & 63, wave = wave_id();
+  // this workgroup's unit: 128 query rows of one (batch row or segment, query head)
+  uint32_t unit;
+  if (!logical_unit(count * (uint32_t)a.q_heads, unit)) return;
+  TileUnit tu;
+  tu.decode(unit, count, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+  if (!tu.ok) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
   const int q0 = tu.tile * BM;
   const int h = tu.head, grp = tu.grp;
@@ -260,17 +260,6 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   if (!valid_q) return;
   bf16* dqrow = (bf16*)row_at(a.dq, a.dq_stride, qb, h, qt);
   store_acc_row<DB>(dqrow, dqacc, a.softmax_scale, half);
-  };
-
-  WorkRange work;
-  work.init(count * (uint32_t)a.q_heads);
-  uint32_t unit;
-  while (work.take(unit)) {
-    TileUnit tu;
-    tu.decode(unit, count, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
-    __syncthreads();  // every wave is done with the previous unit's LDS tiles
-    if (tu.ok) process(tu);
-  }
 }
 
 // ------------------------------------------------------------------ dKV ----
@@ -312,13 +301,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   const int32_t* list = MODE == kVarlen ? a.k_units : nullptr;
   const uint32_t count = list ? (uint32_t)a.num_k_units : (uint32_t)ktiles * outer;
 
-  // One unit: 128 keys of one (batch row or segment, kv head).
-  auto process = [&](const TileUnit& tu) __attribute__((always_inline)) {
-  // per-lane constants are formed inside each unit (not hoisted and held
-  // in registers across the unit loop)
-  int tid = threadIdx.x;
-  opaque(tid);
-  const int lane = tid & 63, wave = wave_id();
+  // this workgroup's unit: 128 keys of one (batch row or segment, kv head)
+  uint32_t unit;
+  if (!logical_unit(count * (uint32_t)a.kv_heads, unit)) return;
+  TileUnit tu;
+  tu.decode(unit, count, ktiles, list, (int)outer, false);  // low key tiles see the most queries
+  if (!tu.ok) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
   const int pair = wave & 3;
   const bool dp_side = wave >= 4;  // wave-uniform role
@@ -582,17 +571,6 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     bf16* dst = dp_side ? (bf16*)row_at(a.dk, a.dk_stride, kb, hk, kslot) : (bf16*)row_at(a.dv, a.dv_stride, kb, hk, kslot);
     store_acc_row<DB>(dst, acc, scale, half);
   }
-  };
-
-  WorkRange work;
-  work.init(count * (uint32_t)a.kv_heads);
-  uint32_t unit;
-  while (work.take(unit)) {
-    TileUnit tu;
-    tu.decode(unit, count, ktiles, list, (int)outer, false);  // low key tiles see the most queries
-    __syncthreads();  // every wave is done with the previous unit's LDS tiles
-    if (tu.ok) process(tu);
-  }
 }
 
 // ----------------------------------------------- varlen accumulator glue ----
@@ -652,8 +630,7 @@ static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
-  // two workgroups per compute unit (256 VGPRs x 4 waves, 65 KB LDS each)
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)persistent_grid(units, 2)), dim3(256), 0, stream,
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)logical_grid(units)), dim3(256), 0, stream,
                      a);
   return WMX_OK;
 }
@@ -666,8 +643,7 @@ static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t units = per_head * a.kv_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
-  // one 8-wave workgroup per compute unit (2 waves per SIMD, 99 KB LDS)
-  const dim3 grid((unsigned)persistent_grid(units, 1));
+  const dim3 grid((unsigned)logical_grid(units));
   if (MODE == kVarlen && !a.keys_unique) {
     const int64_t n = bwd_workspace_size(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,

@@ -57,13 +57,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
   const int32_t* list = MODE == kVarlen ? a.q_units : nullptr;
   const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
 
-  // One unit: 128 query rows of one (batch row or segment, query head).
-  auto process = [&](const TileUnit& tu) __attribute__((always_inline)) {
-  // per-lane constants are formed inside each unit (not hoisted and held
-  // in registers across the unit loop)
-  int tid = threadIdx.x;
-  opaque(tid);
-  const int lane = tid & 63, wave = wave_id();
+  // this workgroup's unit: 128 query rows of one (batch row or segment, query head)
+  uint32_t unit;
+  if (!logical_unit(count * (uint32_t)a.q_heads, unit)) return;
+  TileUnit tu;
+  tu.decode(unit, count, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+  if (!tu.ok) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
   const int q0 = tu.tile * BM;
   const int h = tu.head, grp = tu.grp;
@@ -291,17 +291,6 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
     const float lse = l_run > 0.f ? (m_run + __log2f(l_run)) * kLn2 : kPosInf;
     a.lse[((int64_t)qb * a.q_heads + h) * a.q_len + qt] = lse;
   }
-  };
-
-  WorkRange work;
-  work.init(count * (uint32_t)a.q_heads);
-  uint32_t unit;
-  while (work.take(unit)) {
-    TileUnit tu;
-    tu.decode(unit, count, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
-    __syncthreads();  // every wave is done with the previous unit's LDS tiles
-    if (tu.ok) process(tu);
-  }
 }
 
 template <int D, int MODE>
@@ -312,8 +301,7 @@ static int launch_fwd_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
-  // two workgroups per compute unit (256 VGPRs x 4 waves, 65 KB LDS each)
-  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), dim3((unsigned)persistent_grid(units, 2)), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), dim3((unsigned)logical_grid(units)), dim3(256), 0, stream, a);
   return WMX_OK;
 }
 

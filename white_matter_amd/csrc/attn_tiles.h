@@ -26,34 +26,6 @@ __device__ __forceinline__ bool logical_unit(unsigned total, unsigned& unit) {
 // Launch size for `units` logical units (a multiple of 8 workgroups).
 inline int64_t logical_grid(int64_t units) { return (units + 7) / 8 * 8; }
 
-// Persistent schedule: the grid holds as many workgroups as the GPU runs at
-// once (a multiple of 8) and each workgroup walks logical work units until
-// none are left, so there is no per-workgroup launch gap and no idle tail of
-// empty workgroups. The units are split into eight contiguous ranges, one per
-// XCD (blockIdx.x % 8 picks the XCD), so units that share K/V or Q/dO tiles
-// (same head, same segment) meet in one XCD's L2. Inside a range the S
-// workgroups of the XCD deal the units in rounds of S, snake order (round r
-// gives unit r S + s to workgroup s when r is even and to workgroup S - 1 - s
-// when r is odd), which balances a heaviest-first order.
-struct WorkRange {
-  uint32_t base, end, slot, slots, round;
-  __device__ __forceinline__ void init(uint32_t total) {
-    const uint32_t x = blockIdx.x & 7u;
-    base = (uint32_t)((uint64_t)total * x / 8);
-    end = (uint32_t)((uint64_t)total * (x + 1) / 8);
-    slot = blockIdx.x >> 3;
-    slots = gridDim.x >> 3;
-    round = 0;
-  }
-  __device__ __forceinline__ bool take(uint32_t& unit) {
-    const uint32_t u = base + round * slots + ((round & 1) ? slots - 1 - slot : slot);
-    ++round;
-    if (u >= end) return false;
-    unit = u;
-    return true;
-  }
-};
-
 // One work unit of a query- or key-tiled kernel: a batch row or varlen
 // segment, a 128-row tile of it, and a head. Logical units are head-major
 // (unit = head * count + u); u names a listed (segment, tile) pair when a

@@ -91,25 +91,6 @@ int launched(int rc) {
 
 }  // namespace
 
-namespace wmx {
-
-int64_t persistent_grid(int64_t units, int per_cu) {
-  // compute units per device, read once per device
-  static int cus[64] = {0};
-  int dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) dev = 0;
-  if (cus[dev] <= 0) {
-    int n = 0;
-    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
-  }
-  const int64_t slots = (int64_t)cus[dev] * per_cu / 8 * 8;
-  const int64_t want = (units + 7) / 8 * 8;
-  return want < slots ? want : (slots > 0 ? slots : 8);
-}
-
-}  // namespace wmx
-
 extern "C" {
 
 int wmx_abi_version(void) { return WMX_ABI_VERSION; }

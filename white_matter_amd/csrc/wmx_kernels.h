@@ -14,11 +14,6 @@ enum Mode {
   kVarlen = 2,  // packed segments addressed through flat query/key indices
 };
 
-// Workgroups of a persistent launch: `per_cu` resident workgroups on every
-// compute unit of the current device, at most `units` (rounded up to a
-// multiple of 8, the XCD count).
-int64_t persistent_grid(int64_t units, int per_cu);
-
 int launch_fwd(const wmx_attn_args& a, hipStream_t stream);
 int launch_bwd_preprocess(const wmx_attn_args& a, hipStream_t stream);
 int64_t bwd_workspace_size(const wmx_attn_args& a);

@@ -79,10 +79,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
 
   // this workgroup's unit: 128 query rows of one (batch row or segment, query head)
-  uint32_t unit;
-  if (!logical_unit(count * (uint32_t)a.q_heads, unit)) return;
   TileUnit tu;
-  tu.decode(unit, count, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
   if (!tu.ok) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
@@ -302,10 +300,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   const uint32_t count = list ? (uint32_t)a.num_k_units : (uint32_t)ktiles * outer;
 
   // this workgroup's unit: 128 keys of one (batch row or segment, kv head)
-  uint32_t unit;
-  if (!logical_unit(count * (uint32_t)a.kv_heads, unit)) return;
   TileUnit tu;
-  tu.decode(unit, count, ktiles, list, (int)outer, false);  // low key tiles see the most queries
+  tu.decode(a.kv_heads, count, list != nullptr, ktiles, list, (int)outer, false);  // low key tiles see the most queries
   if (!tu.ok) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
@@ -630,7 +626,7 @@ static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)logical_grid(units)), dim3(256), 0, stream,
+  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)units), dim3(256), 0, stream,
                      a);
   return WMX_OK;
 }
@@ -643,7 +639,7 @@ static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t units = per_head * a.kv_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
-  const dim3 grid((unsigned)logical_grid(units));
+  const dim3 grid((unsigned)units);
   if (MODE == kVarlen && !a.keys_unique) {
     const int64_t n = bwd_workspace_size(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,

@@ -58,10 +58,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
   const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
 
   // this workgroup's unit: 128 query rows of one (batch row or segment, query head)
-  uint32_t unit;
-  if (!logical_unit(count * (uint32_t)a.q_heads, unit)) return;
   TileUnit tu;
-  tu.decode(unit, count, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
   if (!tu.ok) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
@@ -301,7 +299,7 @@ static int launch_fwd_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), dim3((unsigned)logical_grid(units)), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), dim3((unsigned)units), dim3(256), 0, stream, a);
   return WMX_OK;
 }
 

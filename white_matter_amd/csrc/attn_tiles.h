@@ -2,8 +2,8 @@
 //
 // A workgroup owns either 128 query rows (forward, dQ) or 128 key rows (dK/dV)
 // of one (batch row or varlen segment, head). These structs decode its
-// logical index (XCD-aware: consecutive units share one XCD's L2, heavy query
-// tiles first), locate its rows, and evaluate the visibility bound
+// logical index (heaviest units first over all heads), locate its rows, and
+// evaluate the visibility bound
 //   lim(i) = clamp(min(offset + stride * i, limit), -1, nk - 1)
 // of wmx_attn_args.
 #pragma once
@@ -15,31 +15,44 @@
 
 namespace wmx {
 
-// Workgroups are dispatched round-robin over the 8 XCDs: blockIdx.x % 8 picks
-// the XCD. Consecutive logical units are mapped to one XCD.
-__device__ __forceinline__ bool logical_unit(unsigned total, unsigned& unit) {
-  const unsigned per_xcd = gridDim.x >> 3;
-  unit = (blockIdx.x & 7u) * per_xcd + (blockIdx.x >> 3);
-  return unit < total;
-}
-
-// Launch size for `units` logical units (a multiple of 8 workgroups).
-inline int64_t logical_grid(int64_t units) { return (units + 7) / 8 * 8; }
-
 // One work unit of a query- or key-tiled kernel: a batch row or varlen
-// segment, a 128-row tile of it, and a head. Logical units are head-major
-// (unit = head * count + u); u names a listed (segment, tile) pair when a
-// work list is given (heaviest first), else tile u / groups of batch row
-// u % groups, tiles counted from the last one when `descending` (the
-// heaviest query tiles of a causal problem are the last, the heaviest key
-// tiles the first), so the order is heaviest first as well.
+// segment, a 128-row tile of it, and a head. Per head, units u = 0 .. count-1
+// are heaviest first: u names a listed (segment, tile) pair when a work list
+// is given (sorted by the host), else tile u / groups of batch row u % groups,
+// tiles counted from the last one when `descending` (the heaviest query tiles
+// of a causal problem are the last, the heaviest key tiles the first).
+//
+// Blocks start in index order as CU slots free up and are dealt round-robin
+// over the 8 XCDs (block b runs on XCD b % 8). When the heads split evenly
+// over the XCDs, XCD x takes heads [x H/8, (x+1) H/8), so every unit of a head
+// shares one L2, in unit-major order (unit u of each of its heads, then unit
+// u + 1: heaviest first over its heads) or head-major order (all units of
+// one head, then the next head: fewer heads resident at a time). Otherwise
+// units are unit-major over all heads. A launch has exactly count * heads
+// blocks.
 struct TileUnit {
   int grp, tile, head;
   bool ok;
-  __device__ __forceinline__ void decode(uint32_t unit, uint32_t count, int tiles, const int32_t* list,
-                                         int num_groups, bool descending) {
-    head = (int)(unit / count);
-    const uint32_t u = unit - (uint32_t)head * count;
+  __device__ __forceinline__ void decode(int heads, uint32_t count, bool unit_major, int tiles,
+                                         const int32_t* list, int num_groups, bool descending) {
+    const uint32_t b = blockIdx.x, nh = (uint32_t)heads;
+    uint32_t u;
+    if ((nh & 7u) == 0) {
+      const uint32_t hpx = nh >> 3, x = b & 7u, s = b >> 3;
+      if (unit_major) {
+        u = s / hpx;
+        head = (int)(x * hpx + (s - u * hpx));
+      } else {
+        const uint32_t hl = s / count;
+        u = s - hl * count;
+        head = (int)(x * hpx + hl);
+      }
+    } else {
+      u = b / nh;
+      head = (int)(b - u * nh);
+    }
+    ok = u < count && head < heads;
+    if (!ok) return;
     if (list) {
       grp = __builtin_amdgcn_readfirstlane(list[2 * u]);
       tile = __builtin_amdgcn_readfirstlane(list[2 * u + 1]);

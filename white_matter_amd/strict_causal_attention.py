@@ -369,14 +369,18 @@ def _schedule_gaps(
 
 
 _TILE = 128  # rows of the kernels' query and key tiles
+_STEP = 64  # rows of the tiles their loops step over
 
 
 def _work_units(metadata: StrictCausalMetadata) -> tuple[torch.Tensor, torch.Tensor]:
     """The (segment, 128-row tile) units of the query-tiled kernels (forward,
     dQ) and of the key-tiled kernel (dK/dV), heaviest first, as int32 (n, 2)
-    device tensors cached on the metadata object. Segments are bottom-right
-    causal: query i of a segment with nq queries and nk keys sees keys
-    0 .. nk - nq + i, which gives each tile's number of visible pairs."""
+    device tensors cached on the metadata object. A unit's cost is the number
+    of 64-row tiles its loop visits (then its row count): segments are
+    bottom-right causal, so query i of a segment with nq queries and nk keys
+    sees keys 0 .. nk - nq + i; a query tile visits the key tiles up to its
+    last row's bound, a key tile the query tiles from the one holding the
+    first row that sees its first key."""
     units = metadata.__dict__.get("_units")
     if units is None:
         q_units, k_units = [], []
@@ -384,15 +388,18 @@ def _work_units(metadata: StrictCausalMetadata) -> tuple[torch.Tensor, torch.Ten
             nq, nk = qe - qs, ke - ks
             off = nk - nq
             for t in range(0, -(-nq // _TILE)):
-                rows = range(t * _TILE, min(nq, (t + 1) * _TILE))
-                q_units.append((sum(min(nk, max(0, off + r + 1)) for r in (rows[0], rows[-1])) * len(rows), s, t))
+                rows = min(nq, (t + 1) * _TILE) - t * _TILE
+                reach = min(nk, max(0, off + t * _TILE + rows))
+                q_units.append(((-(-reach // _STEP), rows), s, t))
             for t in range(0, -(-nk // _TILE)):
-                keys = range(t * _TILE, min(nk, (t + 1) * _TILE))
-                k_units.append((sum(max(0, nq - max(0, j - off)) for j in (keys[0], keys[-1])) * len(keys), s, t))
+                keys = min(nk, (t + 1) * _TILE) - t * _TILE
+                first = max(0, t * _TILE - off)
+                steps = -(-(nq - first // _STEP * _STEP) // _STEP) if first < nq else 0
+                k_units.append(((steps, keys), s, t))
         device = metadata.query_indices.device
 
         def table(entries):
-            entries.sort(key=lambda e: -e[0])
+            entries.sort(key=lambda e: (-e[0][0], -e[0][1], e[1], e[2]))
             flat = [v for _, seg, tile in entries for v in (seg, tile)]
             return torch.tensor(flat, dtype=torch.int32).view(-1, 2).to(device)
 

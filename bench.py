@@ -39,6 +39,7 @@ KERNEL_NAMES = {  # rocprof kernel name prefix -> bench kernel key
     "wmx::attn_fwd_kernel": "attn_fwd",
     "wmx::bwd_delta_kernel": "bwd_delta",
     "wmx::attn_bwd_dq_kernel": "bwd_dq",
+    "wmx::attn_bwd_dq_ds_kernel": "bwd_dq",
     "wmx::attn_bwd_dkv_kernel": "bwd_dkv",
     "wmx::decode_split_kernel": "decode_split",
     "wmx::decode_combine_kernel": "decode_combine",
@@ -108,17 +109,17 @@ def strict_jacobi_setup(device, seed=0, batch=8, heads=16, length=2048, dim=128)
 
 def kernel_times(q, k, v, metadata, reps):
     """Average duration (ms) of each kernel of one forward+backward, launched
-    alone through the C ABI between HIP events on the current stream."""
+    alone through the C ABI between HIP events on the current stream, in the
+    backward's order (dK/dV stores the dS that dQ reads)."""
     from white_matter_amd import _kernels, _native
     from white_matter_amd.strict_causal_attention import _schedule_flags, _work_units
 
     batch, heads, length, dim = q.shape
     max_q, max_k, flags = _schedule_flags(metadata)
-    q_units, k_units = _work_units(metadata)
     varlen = _kernels.Varlen(
         metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
         metadata.cu_queries.numel() - 1, max_q, max_k, length, k.shape[2], bool(flags & 16), flags & 15,
-        q_units, k_units,
+        *_work_units(metadata),
     )
     vis = _kernels.Visibility(varlen=varlen)
     out = torch.zeros(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
@@ -140,8 +141,8 @@ def kernel_times(q, k, v, metadata, reps):
     calls = {
         "attn_fwd": lambda: _native.attn_fwd(args, dev),
         "bwd_delta": lambda: _native.attn_bwd_preprocess(args, dev),
-        "bwd_dq": lambda: _native.attn_bwd_dq(args, dev),
         "bwd_dkv": lambda: _native.attn_bwd_dkv(args, dev),
+        "bwd_dq": lambda: _native.attn_bwd_dq(args, dev),
     }
     result = {}
     for name, fn in calls.items():
@@ -200,17 +201,20 @@ def cpu_baseline(q, k, v, metadata, budget_s: float):
     }
 
 
-def algorithmic_bytes(q, k, v) -> dict[str, int]:
+def algorithmic_bytes(q, k, v, pairs) -> dict[str, int]:
     """HBM bytes each kernel must move at least once per launch: its operands
-    read and its results written (bf16 tensors, fp32 LSE and delta)."""
+    read and its results written (bf16 tensors, fp32 LSE and delta, bf16 dS
+    for the visible pairs of every query head, which the dK/dV kernel writes
+    and the dQ kernel reads)."""
     t = q.numel() * 2  # Q, O, dO, dQ each
     kv = k.numel() * 2 + v.numel() * 2
     rows = q.shape[0] * q.shape[1] * q.shape[2] * 4  # LSE or delta
+    ds = 2 * q.shape[1] * pairs
     return {
         "attn_fwd": 2 * t + kv + rows,  # Q, K, V in; O, LSE out
         "bwd_delta": 2 * t + rows,  # O, dO in; delta out
-        "bwd_dq": 3 * t + kv + 2 * rows,  # Q, dO, K, V, LSE, delta in; dQ out
-        "bwd_dkv": 2 * t + 2 * kv + 2 * rows,  # Q, dO, K, V, LSE, delta in; dK, dV out
+        "bwd_dq": t + k.numel() * 2 + ds,  # K, dS in; dQ out
+        "bwd_dkv": 2 * t + 2 * kv + 2 * rows + ds,  # Q, dO, K, V, LSE, delta in; dK, dV, dS out
     }
 
 
@@ -334,7 +338,7 @@ def main(argv=None) -> int:
         "bwd_dkv": 8 * dim * heads * pairs,
         "bwd_delta": 0,
     }
-    hbm = algorithmic_bytes(q, k, v)
+    hbm = algorithmic_bytes(q, k, v, pairs)
     dominant = max(kernels, key=kernels.get)
     dom_achieved = algorithmic[dominant] / (kernels[dominant] * 1e-3) / 1e12
     traffic = measured_traffic(dominant)

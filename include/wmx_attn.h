@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 2
+#define WMX_ABI_VERSION 3
 
 enum {
   WMX_OK = 0,
@@ -130,6 +130,13 @@ typedef struct wmx_attn_args {
   const int32_t* k_units;     /* key tiles: dK/dV */
   int32_t num_q_units;
   int32_t num_k_units;
+  /* Optional varlen dS layout (see wmx_attn_bwd_workspace_size), int64
+   * [num_segments + 1]: segment s's dS block starts ds_offsets[s] elements
+   * into each query head's region and holds keys(s) x pad128(queries(s))
+   * elements, ds_offsets[0] = 0, ds_elements = ds_offsets[num_segments].
+   * NULL: varlen backward passes recompute dQ without a dS buffer. */
+  const int64_t* ds_offsets;
+  int64_t ds_elements;
 } wmx_attn_args;
 
 /*
@@ -180,17 +187,28 @@ int wmx_attn_fwd(const wmx_attn_args* args, void* stream);
 /* delta[b,h,i] = sum_d dout[b,h,i,d] * o[b,h,i,d] in fp32. */
 int wmx_attn_bwd_preprocess(const wmx_attn_args* args, void* stream);
 
-/* Workspace bytes wmx_attn_bwd needs for these arguments (0 when none). */
+/* Workspace bytes for the fastest backward of these arguments (0 when it
+ * needs none): the fp32 dK/dV accumulators of varlen schedules whose key rows
+ * repeat (required), then, from a 256-byte aligned offset, the bf16 dS
+ * buffer that the dK/dV kernel writes and the dQ kernel reads (a
+ * keys x pad128(queries) block per batch row or segment and query head; for
+ * varlen schedules laid out by ds_offsets) when it totals at most 4 GiB.
+ * wmx_attn_bwd_min_workspace_size is the required part: a workspace between
+ * the two sizes runs the backward without the dS buffer, recomputing S and
+ * dP in the dQ kernel. */
 int64_t wmx_attn_bwd_workspace_size(const wmx_attn_args* args);
+int64_t wmx_attn_bwd_min_workspace_size(const wmx_attn_args* args);
 
-/* Backward: delta, then dq, dk, dv. Varlen mode accumulates into dk/dv,
- * which the caller zero-fills. */
+/* Backward: delta, then dk and dv (and dS), then dq (with a dS buffer), or
+ * delta, dq, dk and dv (without). */
 int wmx_attn_bwd(const wmx_attn_args* args, void* stream);
 
 /* The two halves of wmx_attn_bwd, for callers that schedule or time them
  * separately; both read the delta that wmx_attn_bwd_preprocess wrote.
- * wmx_attn_bwd_dq writes dq (query-parallel); wmx_attn_bwd_dkv writes dk/dv
- * (key-parallel). */
+ * wmx_attn_bwd_dkv writes dk/dv (key-parallel) and, with a dS workspace, dS;
+ * wmx_attn_bwd_dq writes dq (query-parallel) from that dS, so it runs after
+ * wmx_attn_bwd_dkv on the same workspace (without a dS workspace it
+ * recomputes and has no order). */
 int wmx_attn_bwd_dq(const wmx_attn_args* args, void* stream);
 int wmx_attn_bwd_dkv(const wmx_attn_args* args, void* stream);
 

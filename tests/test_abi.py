@@ -61,9 +61,17 @@ def test_workspace_sizes():
     args = _native.AttnArgs()
     args.head_dim, args.batch, args.kv_heads, args.key_extent = 128, 2, 4, 100
     assert lib.wmx_attn_bwd_workspace_size(ctypes.byref(args)) == 0
+    # dense: a bf16 dS^T block of kv_len x (q_len rounded up to 128) per (batch row, query head)
+    args.q_heads, args.q_len, args.kv_len = 8, 130, 300
+    assert lib.wmx_attn_bwd_workspace_size(ctypes.byref(args)) == 2 * 8 * 300 * 256 * 2
+    assert lib.wmx_attn_bwd_min_workspace_size(ctypes.byref(args)) == 0
     args.query_indices = 0x1000
     args.keys_unique = 0
-    assert lib.wmx_attn_bwd_workspace_size(ctypes.byref(args)) == 2 * 2 * 100 * 4 * 128 * 4
+    acc = 2 * 2 * 100 * 4 * 128 * 4
+    assert lib.wmx_attn_bwd_workspace_size(ctypes.byref(args)) == acc  # no dS layout given
+    assert lib.wmx_attn_bwd_min_workspace_size(ctypes.byref(args)) == acc
+    args.ds_offsets, args.ds_elements = 0x2000, 1000
+    assert lib.wmx_attn_bwd_workspace_size(ctypes.byref(args)) == acc + 8 * 1000 * 2
     dec = _native.DecodeArgs()
     dec.batch, dec.q_heads, dec.kv_heads, dec.capacity, dec.head_dim, dec.num_splits = 2, 4, 4, 1000, 64, 3
     assert lib.wmx_decode_num_splits(ctypes.byref(dec)) == 3

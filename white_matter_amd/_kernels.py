@@ -73,6 +73,8 @@ class Varlen:
     segment_layout: int = 0  # bit 0 consecutive queries, bit 1 consecutive keys from key 1
     q_units: torch.Tensor | None = None  # int32 (n, 2) (segment, query tile), heaviest first
     k_units: torch.Tensor | None = None  # int32 (n, 2) (segment, key tile), heaviest first
+    ds_offsets: torch.Tensor | None = None  # int64 (num_segments + 1) dS block offsets (see wmx_attn.h)
+    ds_elements: int = 0  # ds_offsets[-1]
 
 
 @dataclass
@@ -116,6 +118,8 @@ class Visibility:
                 args.q_units, args.num_q_units = s.q_units.data_ptr(), s.q_units.shape[0]
             if s.k_units is not None:
                 args.k_units, args.num_k_units = s.k_units.data_ptr(), s.k_units.shape[0]
+            if s.ds_offsets is not None:
+                args.ds_offsets, args.ds_elements = s.ds_offsets.data_ptr(), s.ds_elements
 
 
 def _base_args(q, k, v, o, lse, scale: float, vis: Visibility, q_len: int) -> _native.AttnArgs:

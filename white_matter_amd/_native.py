@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -79,6 +79,8 @@ class AttnArgs(ctypes.Structure):
         ("k_units", _vp),
         ("num_q_units", ctypes.c_int32),
         ("num_k_units", ctypes.c_int32),
+        ("ds_offsets", _vp),
+        ("ds_elements", ctypes.c_int64),
     ]
 
 
@@ -118,6 +120,7 @@ EXPORTS = (
     "wmx_attn_fwd",
     "wmx_attn_bwd_preprocess",
     "wmx_attn_bwd_workspace_size",
+    "wmx_attn_bwd_min_workspace_size",
     "wmx_attn_bwd",
     "wmx_attn_bwd_dq",
     "wmx_attn_bwd_dkv",
@@ -146,8 +149,9 @@ def load() -> ctypes.CDLL:
     for name in ("wmx_attn_fwd", "wmx_attn_bwd_preprocess", "wmx_attn_bwd", "wmx_attn_bwd_dq", "wmx_attn_bwd_dkv"):
         getattr(lib, name).argtypes = [ctypes.POINTER(AttnArgs), _vp]
         getattr(lib, name).restype = ctypes.c_int
-    lib.wmx_attn_bwd_workspace_size.argtypes = [ctypes.POINTER(AttnArgs)]
-    lib.wmx_attn_bwd_workspace_size.restype = ctypes.c_int64
+    for name in ("wmx_attn_bwd_workspace_size", "wmx_attn_bwd_min_workspace_size"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(AttnArgs)]
+        getattr(lib, name).restype = ctypes.c_int64
     lib.wmx_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
     lib.wmx_decode.restype = ctypes.c_int
     lib.wmx_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs)]

@@ -8,14 +8,18 @@
 // (src/white_matter/ops/cyclic_attention/_tilelang/backward_query.py:86-109,
 //  backward_key_value.py:102-132, backward_preprocess.py:34-49).
 //
-// Two deterministic kernels, no atomics on the dense paths:
-//   dQ  : query-parallel (4 waves x 32 query rows), loops over visible key
-//         tiles of 64; a lane owns one query column of S^T = K Q^T, so its
-//         LSE and delta are scalars; dQ^T = K^T dS^T accumulates in registers.
-//   dKV : key-parallel (4 waves x 32 keys), loops over the query heads of the
+// Deterministic kernels, no atomics on the dense paths:
+//   dKV : key-parallel (128 keys, 8 waves), loops over the query heads of the
 //         KV head and over the query tiles of 64 that can see the key tile;
 //         a lane owns one key column of S = Q K^T; dV^T = dO^T P and
-//         dK^T = Q^T dS accumulate in registers.
+//         dK^T = Q^T dS accumulate in registers. With a dS buffer in the
+//         workspace it also stores dS^T (bf16, the value its dK product
+//         uses) for every query tile it visits.
+//   dQ  : query-parallel (4 waves x 32 query rows), loops over visible key
+//         tiles of 64; dQ^T = K^T dS^T accumulates in registers. The stored-
+//         dS form streams K and dS^T tiles and runs after dKV; the recompute
+//         form (no dS buffer) evaluates S^T = K Q^T and dP^T = V dO^T itself,
+//         a lane owning one query column so its LSE and delta are scalars.
 // Varlen schedules whose key rows repeat across segments (the shared dummy
 // slot, capped histories) accumulate dK/dV in fp32 workspace rows with
 // atomics and convert once at the end.
@@ -260,6 +264,180 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   store_acc_row<DB>(dqrow, dqacc, a.softmax_scale, half);
 }
 
+// ------------------------------------------------------- dQ from dS ----
+// One workgroup = 128 query rows (4 waves x 32) of one (batch row or segment,
+// query head): dQ^T = K^T dS^T over the visible key tiles of 64, with the K
+// tile and the dS^T tile (64 keys x the workgroup's 128 queries, written by
+// the dK/dV kernel) streaming through double-buffered LDS; both operands are
+// transpose reads. The dK/dV kernel stores every (key, query) pair of each
+// query tile it visits, zeros for invisible pairs, and visits every tile a
+// wave here reads under the causal/offset bound, so only document masks
+// (whose rows past a key's document end the dK/dV kernel skips) are applied
+// here.
+template <int D, int MODE>
+__global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_args args) {
+  const wmx_attn_args& a = args;
+  constexpr int BM = 128, BN = 64;
+  static_assert(BN == kTileRows && BM == kRowElems, "one LDS tile per key tile, one row per query tile");
+  constexpr int DB = D / 32;
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 k_lds1[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 s_lds0[kTileElems];
+  __shared__ __attribute__((aligned(1024))) bf16 s_lds1[kTileElems];
+  __shared__ int meta_lds[2][2][BN];  // per buffer: key document ids, key query ends
+  __shared__ int red_lds[4];
+
+  const int qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
+  const unsigned outer = MODE == kVarlen ? (unsigned)a.num_segments : (unsigned)a.batch;
+  const int32_t* list = MODE == kVarlen ? a.q_units : nullptr;
+  const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
+  TileUnit tu;
+  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+  if (!tu.ok) return;
+  const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
+  const int half = lane >> 5, col = lane & 31;
+  const int q0 = tu.tile * BM;
+  const int h = tu.head, grp = tu.grp;
+  const int hk = h / (a.q_heads / a.kv_heads);
+  Problem<MODE> pb;
+  pb.init(a, grp);
+  const int b = pb.b, nq = pb.nq, nk = pb.nk;
+  if (q0 >= nq) return;
+  const bool slot0 = a.keep_slot0 && nk > 0;
+  const int lim_max_wg = pb.bound.lim(min(q0 + BM, nq) - 1);
+  const int i = q0 + wave * 32 + col;
+  const bool valid_q = i < nq;
+  const int lim_i = pb.bound.lim(i);
+  const int wave_first = q0 + wave * 32;
+  const bool wave_live = wave_first < nq;
+  const int lim_max_wave = pb.bound.lim(min(wave_first + 31, nq - 1));
+
+  int qseg_i = 0, qstart_i = 0, kt_begin_main = 0;
+  if constexpr (MODE == kDoc) {
+    if (valid_q) {
+      qseg_i = a.q_seg[(int64_t)b * a.q_len + i];
+      qstart_i = a.q_start[(int64_t)b * a.q_len + i];
+    }
+    int v = INT_MAX;
+    if (tid < BM && q0 + tid < nq) v = a.q_start[(int64_t)b * a.q_len + q0 + tid];
+    for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
+    if (lane == 0) red_lds[wave] = v;
+    __syncthreads();
+    v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
+    kt_begin_main = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v / BN);  // uniform: keeps the tile loop scalar
+  }
+  int kt_end = (lim_max_wg + 1 + BN - 1) / BN;
+  if (slot0 && kt_end < 1) kt_end = 1;
+  const int first_main = kt_begin_main > 1 ? kt_begin_main : 1;
+  const bool gap = (MODE == kDoc) && first_main > 1;
+  const int ntiles = gap ? 1 + max(0, kt_end - first_main) : kt_end;
+  auto tile_of = [&](int it) { return gap ? (it == 0 ? 0 : first_main + it - 1) : it; };
+
+  const int reach = slot0 ? max(lim_max_wg + 1, 1) : lim_max_wg + 1;
+  TileDMA<D> dma;
+  dma.init(wave, lane);
+  KeyTiles<MODE, D> keys;
+  keys.init(a, pb, hk, reach, dma);
+  // dS^T tile: rows = keys n0 .. n0 + 63 (zeros past the reach), columns =
+  // this workgroup's queries
+  TileDMA<kRowElems> sdma;
+  sdma.init(wave, lane);
+  const int64_t ld = ds_ld(nq);
+  const bf16* ds = (const bf16*)((const char*)a.workspace + bwd_ds_offset(a)) + q0;
+  if constexpr (MODE == kVarlen) {
+    ds += h * a.ds_elements + a.ds_offsets[grp];
+  } else {
+    ds += ((int64_t)b * a.q_heads + h) * a.kv_len * ld;
+  }
+  auto issue_ds = [&](int n0, bf16* tile) __attribute__((always_inline)) {
+    const int nvalid = min(max(reach - n0, 0), kTileRows);
+    sdma.issue_strided_rows(make_rsrc(ds + (int64_t)n0 * ld, nvalid * (int)ld * 2), tile, (int)ld * 2);
+  };
+  auto load_meta = [&](int n0) -> int {
+    const int j = n0 + (tid & 63);
+    if constexpr (MODE == kDoc) {
+      if (tid < 64) return j < nk ? a.k_seg[(int64_t)b * a.kv_len + j] : INT_MIN;
+      if (tid < 128) return j < nk ? a.k_qend[(int64_t)b * a.kv_len + j] : 0;
+    }
+    return 0;
+  };
+  auto store_meta = [&](int buf, int v) {
+    if constexpr (MODE == kDoc) {
+      if (tid < 128) meta_lds[buf][tid >> 6][tid & 63] = v;
+    }
+  };
+
+  f32x16 dqacc[DB];
+#pragma unroll
+  for (int d = 0; d < DB; ++d) dqacc[d] = f32x16{};
+  TrReads<DB> trd;  // K^T: rows d, contraction over keys
+  trd.init(lane);
+  TrReads<1> srd;  // dS^T: this wave's 32 query columns, contraction over keys
+  srd.init(lane, 32 * wave);
+
+  auto tile_step = [&](int n0, int buf, const bf16* kt, const bf16* st) __attribute__((always_inline)) {
+    trd.refresh();
+    srd.refresh();
+#pragma unroll
+    for (int s = 0; s < BN / 16; ++s) {
+      bf16x8 op = srd.get(st, 0, s);
+      if constexpr (MODE == kDoc) {
+        // element e is key n0 + 16 s + 8 (e / 4) + 4 half + e % 4
+        u32x4 w = __builtin_bit_cast(u32x4, op);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const int jl = 16 * s + 8 * (e >> 2) + 4 * half + (e & 3);
+          const int j = n0 + jl;
+          const int ksg = meta_lds[buf][0][jl], kqe = meta_lds[buf][1][jl];
+          const bool keep = ((j <= lim_i) | (slot0 & (j == 0))) & (j < nk) &
+                            (((ksg == qseg_i) & (j >= qstart_i)) | (ksg == -1)) & (i < kqe);
+          const uint32_t m = (e & 1) ? 0xffff0000u : 0x0000ffffu;
+          w[e >> 1] &= keep ? 0xffffffffu : ~m;
+        }
+        op = as_bf16x8(w);
+      }
+#pragma unroll
+      for (int d = 0; d < DB; ++d) dqacc[d] = mfma32(trd.get(kt, d, s), op, dqacc[d]);
+    }
+  };
+
+  auto iteration = [&](auto bufc, int it) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    const bf16* kcur = B ? k_lds1 : k_lds0;
+    const bf16* scur = B ? s_lds1 : s_lds0;
+    const int n0 = tile_of(it) * BN;
+    dma_barrier();
+    const bool more = it + 1 < ntiles;
+    int next_meta = 0;
+    if (more) {
+      const int n1 = tile_of(it + 1) * BN;
+      issue_key_tile(keys, a, pb, dma, n1, B ? k_lds0 : k_lds1);
+      issue_ds(n1, B ? s_lds0 : s_lds1);
+      next_meta = load_meta(n1);
+    }
+    const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    if (wave_sees) tile_step(n0, B, kcur, scur);
+    if (more) store_meta(B ^ 1, next_meta);
+  };
+
+  if (ntiles > 0) {
+    const int n0 = tile_of(0) * BN;
+    issue_key_tile(keys, a, pb, dma, n0, k_lds0);
+    issue_ds(n0, s_lds0);
+    store_meta(0, load_meta(n0));
+  }
+  for (int it = 0; it < ntiles; it += 2) {
+    iteration(std::integral_constant<int, 0>{}, it);
+    if (it + 1 < ntiles) iteration(std::integral_constant<int, 1>{}, it + 1);
+  }
+
+  if (!valid_q) return;
+  int qb, qt;
+  pb.query_loc(i, qb, qt);
+  bf16* dqrow = (bf16*)row_at(a.dq, a.dq_stride, qb, h, qt);
+  store_acc_row<DB>(dqrow, dqacc, a.softmax_scale, half);
+}
+
 // ------------------------------------------------------------------ dKV ----
 // One workgroup = 128 keys of one (batch row or segment, kv head) and eight
 // waves: wave pair p (waves p and p + 4, which share SIMD p) owns keys
@@ -273,7 +451,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
 // Query and output-gradient tiles of 64 rows for every query head of the
 // group stream through double-buffered LDS (direct-to-LDS loads); each tile
 // is read row-wise for S and dP and by transpose reads for dV and dK.
-template <int D, int MODE, bool ATOMIC>
+template <int D, int MODE, bool ATOMIC, bool DS>
 __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args args) {
   const wmx_attn_args& a = args;
   constexpr int BNK = 128, BMQ = 64, NW = 8;
@@ -344,6 +522,23 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   }
   const int pair_key0 = n0 + pair * 32;
   const bool pair_live = pair_key0 < nk;
+
+  // dS^T rows of this lane's key: block of (problem, query head hq) at
+  // ds_key + hq * ds_head, query i at element i
+  bf16* ds_key = nullptr;
+  int64_t ds_head = 0;
+  if constexpr (DS) {
+    const int64_t ld = ds_ld(nq);
+    bf16* ds = (bf16*)((char*)a.workspace + bwd_ds_offset(a));
+    if constexpr (MODE == kVarlen) {
+      ds_head = a.ds_elements;
+      ds += a.ds_offsets[grp];
+    } else {
+      ds_head = (int64_t)a.kv_len * ld;
+      ds += (int64_t)b * a.q_heads * ds_head;
+    }
+    ds_key = ds + (int64_t)(valid_k ? n : n0) * ld + 8 * half;
+  }
   const int pair_m_begin = (slot0 && pair_key0 == 0) ? 0 : pb.bound.first_row(pair_key0, nq);
 
   // K rows on the S side, V rows on the dP side
@@ -376,36 +571,25 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   TrReads<DB> trd;
   trd.init(lane);
 
-  // per-row statistics (and document metadata) of a query tile, loaded into
-  // registers while the tile streams in, stored once the other buffer is free
-  struct RowMeta {
-    float lse2, delta;
-    int seg, start;
-  };
-  auto load_meta = [&](int hq, int m0) {
-    RowMeta r{kPosInf, 0.f, INT_MIN, INT_MAX};
-    const int m = m0 + (tid & 63);
-    if (tid < BMQ && m < nq) {
-      int rb, rt;
-      pb.query_loc(m, rb, rt);
-      const int64_t idx = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
-      r.lse2 = a.lse[idx] * kLog2e;
-      r.delta = a.delta[idx];
-      if constexpr (MODE == kDoc) {
-        r.seg = a.q_seg[(int64_t)b * a.q_len + m];
-        r.start = a.q_start[(int64_t)b * a.q_len + m];
-      }
-    }
-    return r;
-  };
-  auto store_meta = [&](auto bufc, const RowMeta& r) __attribute__((always_inline)) {
+  // per-row statistics (and document metadata) of query tile (hq, m0), loaded
+  // by wave 0 straight into LDS buffer B with the tile (one 4-byte direct-to-
+  // LDS load per array: no registers, no waits until the tile barrier). Rows
+  // past nq read as zeros; their scores are masked.
+  auto issue_meta = [&](auto bufc, int hq, int m0) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
-    if (tid < BMQ) {
-      stat_lds[B][0][tid] = r.lse2;
-      stat_lds[B][1][tid] = r.delta;
+    if (wave == 0) {
+      const int m = m0 + lane;
+      const bool ok = m < nq;
+      int rb, rt;
+      pb.query_loc(ok ? m : 0, rb, rt);
+      const int64_t idx = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
+      const void* zero = (const void*)kZeroChunk;
+      __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.lse + idx) : zero, (lds_void*)&stat_lds[B][0][0], 4, 0, 0);
+      __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.delta + idx) : zero, (lds_void*)&stat_lds[B][1][0], 4, 0, 0);
       if constexpr (MODE == kDoc) {
-        qdoc_lds[B][0][tid] = r.seg;
-        qdoc_lds[B][1][tid] = r.start;
+        const int64_t di = (int64_t)b * a.q_len + m;
+        __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.q_seg + di) : zero, (lds_void*)&qdoc_lds[B][0][0], 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.q_start + di) : zero, (lds_void*)&qdoc_lds[B][1][0], 4, 0, 0);
       }
     }
   };
@@ -460,14 +644,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
           // a masked score is -inf and gives p = 0 exactly (lse is finite or +inf)
-          p4[e] = __builtin_amdgcn_exp2f(fmaf(tacc[mb][4 * g + e], sl2, -l4[e]));
+          p4[e] = __builtin_amdgcn_exp2f(fmaf(tacc[mb][4 * g + e], sl2, -l4[e] * kLog2e));
           tacc[mb][4 * g + e] = p4[e];
         }
         p_lds[pair][mb][g][lane] = p4;
       }
     }
   };
-  auto second_half = [&](auto bufc, auto sidec) __attribute__((always_inline)) {
+  auto second_half = [&](auto bufc, auto sidec, int hq, int m0) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
     constexpr bool DP = decltype(sidec)::value;
     trd.refresh();
@@ -485,9 +669,20 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       }
     }
     const bf16* tr = DP ? (B ? q_lds1 : q_lds0) : (B ? g_lds1 : g_lds0);  // Q^T for dK, dO^T for dV
+    bf16* ds_row = nullptr;
+    if constexpr (DP && DS) ds_row = ds_key + hq * ds_head + m0;
 #pragma unroll
     for (int s = 0; s < BMQ / 16; ++s) {
       const bf16x8 op = acc_kperm_operand(tacc[s >> 1], s);
+      if constexpr (DP && DS) {
+        // operand element e is query m0 + 16 s + 8 (e / 4) + 4 half + e % 4;
+        // swapping dwords with the partner lane (lane ^ 32) gives each lane
+        // the 8 queries 16 s + 8 half .. + 7 of its key: one 16-byte store
+        const u32x4 w = __builtin_bit_cast(u32x4, op);
+        const auto lo = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+        const auto hi = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+        if (valid_k) *reinterpret_cast<u32x4*>(ds_row + 16 * s) = u32x4{lo[0], hi[0], lo[1], hi[1]};
+      }
 #pragma unroll
       for (int d = 0; d < DB; ++d) acc[d] = mfma32(trd.get(tr, d, s), op, acc[d]);
     }
@@ -508,13 +703,18 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     int hn = hq_cur, mn = m0;
     advance(hn, mn);
     // tile `it` has landed; every wave is done with the other buffer and
-    // every dP-side wave has taken the previous P
-    dma_barrier();
+    // every dP-side wave has taken the previous P. A dP-side wave that stored
+    // dS in the previous step issued its 4 stores after this tile's loads:
+    // those may still be in flight.
+    if (DS && dp_side && pair_live && it > 0) {
+      lds_sync<4>();
+    } else {
+      lds_sync<0>();
+    }
     const bool more = it + 1 < total;
-    RowMeta next{};
     if (more) {
       qrows.issue(a, pb, dma, hn, mn, B ? q_lds0 : q_lds1, B ? g_lds0 : g_lds1);
-      next = load_meta(hn, mn);
+      issue_meta(std::integral_constant<int, B ^ 1>{}, hn, mn);
     }
     const bool active = pair_live && m0 + BMQ > pair_m_begin;  // uniform over the pair
     using S_side = std::integral_constant<bool, false>;
@@ -526,22 +726,29 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
         first_half(bufc, S_side{}, m0);
       }
     }
-    __syncthreads();  // P of this tile is in LDS
+    lds_barrier();  // P of this tile is in LDS
     if (active) {
       if (dp_side) {
-        second_half(bufc, DP_side{});
+        second_half(bufc, DP_side{}, hq_cur, m0);
       } else {
-        second_half(bufc, S_side{});
+        second_half(bufc, S_side{}, hq_cur, m0);
+      }
+    } else if constexpr (DS) {
+      // the dQ kernel reads every key row of a visited tile: zeros for a
+      // pair that sees none of its rows
+      if (dp_side && valid_k) {
+        bf16* row = ds_key + hq_cur * ds_head + m0;
+#pragma unroll
+        for (int s = 0; s < BMQ / 16; ++s) *reinterpret_cast<u32x4*>(row + 16 * s) = u32x4{0u, 0u, 0u, 0u};
       }
     }
-    if (more) store_meta(std::integral_constant<int, B ^ 1>{}, next);
     hq_cur = hn;
     m_cur = mn;
   };
 
   if (total > 0) {
     qrows.issue(a, pb, dma, hq_cur, m_cur, q_lds0, g_lds0);
-    store_meta(std::integral_constant<int, 0>{}, load_meta(hq_cur, m_cur));
+    issue_meta(std::integral_constant<int, 0>{}, hq_cur, m_cur);
   }
   for (int it = 0; it < total; it += 2) {
     iteration(std::integral_constant<int, 0>{}, it);
@@ -613,9 +820,34 @@ int launch_bwd_preprocess(const wmx_attn_args& a, hipStream_t stream) {
   return WMX_OK;
 }
 
+// Largest dS buffer the backward uses (beyond it dQ recomputes S and dP).
+constexpr int64_t kMaxDsBytes = (int64_t)4 << 30;
+
+int64_t bwd_ds_bytes(const wmx_attn_args& a) {
+  int64_t elems = 0;
+  if (a.query_indices) {
+    if (!a.ds_offsets || a.ds_elements <= 0) return 0;
+    if (__builtin_mul_overflow(a.ds_elements, (int64_t)a.q_heads, &elems)) return 0;
+  } else {
+    const int64_t per = (int64_t)a.kv_len * ds_ld(a.q_len);
+    if (__builtin_mul_overflow(per, (int64_t)a.batch * a.q_heads, &elems)) return 0;
+  }
+  // 64 rows of a query row block must stay within 32-bit buffer offsets
+  const int64_t ld = ds_ld(a.query_indices ? a.max_queries : a.q_len);
+  if (elems <= 0 || elems > kMaxDsBytes / 2 || ld * 2 * kTileRows >= ((int64_t)1 << 31)) return 0;
+  return elems * 2;
+}
+
+int64_t bwd_min_workspace_size(const wmx_attn_args& a) { return bwd_acc_bytes(a); }
+
 int64_t bwd_workspace_size(const wmx_attn_args& a) {
-  if (!a.query_indices || a.keys_unique) return 0;
-  return (int64_t)2 * a.batch * a.key_extent * a.kv_heads * a.head_dim * (int64_t)sizeof(float);
+  const int64_t ds = bwd_ds_bytes(a);
+  return ds > 0 ? bwd_ds_offset(a) + ds : bwd_acc_bytes(a);
+}
+
+bool bwd_uses_ds(const wmx_attn_args& a) {
+  const int64_t ds = bwd_ds_bytes(a);
+  return ds > 0 && a.workspace && a.workspace_bytes >= bwd_ds_offset(a) + ds;
 }
 
 template <int D, int MODE>
@@ -626,8 +858,11 @@ static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
-  hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)units), dim3(256), 0, stream,
-                     a);
+  if (bwd_uses_ds(a)) {
+    hipLaunchKernelGGL((attn_bwd_dq_ds_kernel<D, MODE>), dim3((unsigned)units), dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dq_kernel<D, MODE>), dim3((unsigned)units), dim3(256), 0, stream, a);
+  }
   return WMX_OK;
 }
 
@@ -640,15 +875,22 @@ static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
   const dim3 grid((unsigned)units);
+  const bool ds = bwd_uses_ds(a);
   if (MODE == kVarlen && !a.keys_unique) {
-    const int64_t n = bwd_workspace_size(a) / (int64_t)sizeof(float);
+    const int64_t n = bwd_acc_bytes(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,
                        (float*)a.workspace, n);
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true>), grid, dim3(512), 0, stream, a);
+    if (ds) {
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true, true>), grid, dim3(512), 0, stream, a);
+    } else {
+      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true, false>), grid, dim3(512), 0, stream, a);
+    }
     const int64_t total = n / 2;
     hipLaunchKernelGGL(acc_to_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a);
+  } else if (ds) {
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false, true>), grid, dim3(512), 0, stream, a);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false>), grid, dim3(512), 0, stream, a);
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false, false>), grid, dim3(512), 0, stream, a);
   }
   return WMX_OK;
 }
@@ -674,8 +916,14 @@ int launch_bwd_dkv(const wmx_attn_args& a, hipStream_t stream) { return launch_b
 
 int launch_bwd(const wmx_attn_args& a, hipStream_t stream) {
   int rc = launch_bwd_preprocess(a, stream);
-  if (rc == WMX_OK) rc = launch_bwd_dq(a, stream);
-  if (rc == WMX_OK) rc = launch_bwd_dkv(a, stream);
+  if (bwd_uses_ds(a)) {
+    // dQ reads the dS that the dK/dV kernel stores
+    if (rc == WMX_OK) rc = launch_bwd_dkv(a, stream);
+    if (rc == WMX_OK) rc = launch_bwd_dq(a, stream);
+  } else {
+    if (rc == WMX_OK) rc = launch_bwd_dq(a, stream);
+    if (rc == WMX_OK) rc = launch_bwd_dkv(a, stream);
+  }
   return rc;
 }
 
@@ -685,16 +933,20 @@ int launch_bwd(const wmx_attn_args& a, hipStream_t stream) {
 // finds its host stub even where the compiler would not emit one for an
 // instantiation first seen next to a branch it folds away.
 namespace wmx {
-#define WMX_BWD_KERNELS(D)                                                   \
-  template __global__ void attn_bwd_dq_kernel<D, kDense>(const wmx_attn_args);   \
-  template __global__ void attn_bwd_dq_kernel<D, kDoc>(const wmx_attn_args);     \
-  template __global__ void attn_bwd_dq_kernel<D, kVarlen>(const wmx_attn_args);  \
-  template __global__ void attn_bwd_dkv_kernel<D, kDense, false>(const wmx_attn_args); \
-  template __global__ void attn_bwd_dkv_kernel<D, kDoc, false>(const wmx_attn_args);   \
-  template __global__ void attn_bwd_dkv_kernel<D, kVarlen, false>(const wmx_attn_args); \
-  template __global__ void attn_bwd_dkv_kernel<D, kVarlen, true>(const wmx_attn_args);
+#define WMX_BWD_KERNELS_MODE(D, M)                                                 \
+  template __global__ void attn_bwd_dq_kernel<D, M>(const wmx_attn_args);          \
+  template __global__ void attn_bwd_dq_ds_kernel<D, M>(const wmx_attn_args);       \
+  template __global__ void attn_bwd_dkv_kernel<D, M, false, false>(const wmx_attn_args); \
+  template __global__ void attn_bwd_dkv_kernel<D, M, false, true>(const wmx_attn_args);
+#define WMX_BWD_KERNELS(D)                                                          \
+  WMX_BWD_KERNELS_MODE(D, kDense)                                                   \
+  WMX_BWD_KERNELS_MODE(D, kDoc)                                                     \
+  WMX_BWD_KERNELS_MODE(D, kVarlen)                                                  \
+  template __global__ void attn_bwd_dkv_kernel<D, kVarlen, true, false>(const wmx_attn_args); \
+  template __global__ void attn_bwd_dkv_kernel<D, kVarlen, true, true>(const wmx_attn_args);
 WMX_BWD_KERNELS(64)
 WMX_BWD_KERNELS(96)
 WMX_BWD_KERNELS(128)
 #undef WMX_BWD_KERNELS
+#undef WMX_BWD_KERNELS_MODE
 }  // namespace wmx

@@ -209,6 +209,29 @@ struct KeyTiles {
   }
 };
 
+// The key rows alone (K tiles of the dQ kernel that reads a stored dS).
+template <int MODE, int D, int NW>
+__device__ __forceinline__ void issue_key_tile(const KeyTiles<MODE, D, NW>& kt, const wmx_attn_args& a,
+                                               const Problem<MODE>& pb, const TileDMA<D, NW>& dma, int n0,
+                                               bf16* ktile) {
+  if (kt.strided && (MODE != kVarlen || n0 > 0)) {
+    const int nvalid = min(max(kt.reach - n0, 0), kTileRows);
+    const int64_t slot = (int64_t)kt.kfirst + n0;
+    dma.issue_strided(make_rsrc(kt.kslice + slot * kt.kst, nvalid * (int)kt.kst * 2), ktile, kt.koff);
+  } else {
+    dma.issue_gathered1(ktile, [&](int tr, bool& ok, const bf16*& kp) {
+      const int j = n0 + tr;
+      ok = j < kt.reach;
+      if constexpr (MODE == kDense) {
+        if (a.key_mask) ok = ok && a.key_mask[(int64_t)kt.b * a.key_mask_stride + min(j, kt.nk - 1)] != 0;
+      }
+      int kb, ks;
+      pb.key_loc(ok ? j : 0, kb, ks);
+      kp = row_at(a.k, a.k_stride, kb, kt.hk, ks);
+    });
+  }
+}
+
 // The query and output-gradient rows of one problem as 64-row LDS tiles (Q
 // and dO share the row addressing), for any query head. Rows past nq read as
 // zeros. Dense rows and varlen segments with consecutive query slots are

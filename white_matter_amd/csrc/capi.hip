@@ -57,8 +57,9 @@ int check_common(const wmx_attn_args* a, bool backward) {
     if (a->row_offset || a->row_limit) return fail(WMX_E_INVALID, "varlen schedule takes no row offsets");
     if ((a->q_units && a->num_q_units < 0) || (a->k_units && a->num_k_units < 0))
       return fail(WMX_E_INVALID, "negative work-list length");
-  } else if (a->q_units || a->k_units) {
-    return fail(WMX_E_INVALID, "work lists need a varlen schedule");
+    if (a->ds_offsets && a->ds_elements < 0) return fail(WMX_E_INVALID, "negative ds_elements");
+  } else if (a->q_units || a->k_units || a->ds_offsets) {
+    return fail(WMX_E_INVALID, "work lists and dS offsets need a varlen schedule");
   }
   if (a->q_seg && (!a->k_seg || !a->q_start || !a->k_qend))
     return fail(WMX_E_INVALID, "document metadata needs all four arrays");
@@ -72,9 +73,10 @@ int check_common(const wmx_attn_args* a, bool backward) {
     if (!strides_vec8(a->do_stride, 3) || !strides_vec8(a->dq_stride, 3) || !strides_vec8(a->dk_stride, 3) ||
         !strides_vec8(a->dv_stride, 3))
       return fail(WMX_E_INVALID, "gradient strides must be multiples of 8 elements");
-    const int64_t need = wmx::bwd_workspace_size(*a);
-    if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    const int64_t need = wmx::bwd_min_workspace_size(*a);
+    if (need > 0 && (!a->workspace || a->workspace_bytes < need))
       return fail(WMX_E_WORKSPACE, "backward needs %lld workspace bytes", (long long)need);
+    if (a->workspace && !aligned16(a->workspace)) return fail(WMX_E_WORKSPACE, "workspace must be 16-byte aligned");
   }
   return WMX_OK;
 }
@@ -118,6 +120,10 @@ int wmx_attn_bwd_preprocess(const wmx_attn_args* args, void* stream) {
 
 int64_t wmx_attn_bwd_workspace_size(const wmx_attn_args* args) {
   return args ? wmx::bwd_workspace_size(*args) : 0;
+}
+
+int64_t wmx_attn_bwd_min_workspace_size(const wmx_attn_args* args) {
+  return args ? wmx::bwd_min_workspace_size(*args) : 0;
 }
 
 int wmx_attn_bwd(const wmx_attn_args* args, void* stream) {

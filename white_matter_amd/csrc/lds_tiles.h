@@ -80,16 +80,18 @@ struct RowReads {
 };
 
 // This lane's byte offsets for transposed operands (see tile_tr_operand) of
-// the 32-column blocks d < DB; k-step s adds 16 rows, the immediate 4096 s.
+// the 32-column blocks d < DB from column c0 on; k-step s adds 16 rows, the
+// immediate 4096 s. Element e of the operand of k-step s comes from tile row
+// 16 s + 8 (e / 4) + 4 (lane / 32) + e % 4.
 template <int DB>
 struct TrReads {
   int lo[DB], hi[DB];
-  __device__ __forceinline__ void init(int lane) {
+  __device__ __forceinline__ void init(int lane, int c0 = 0) {
     const int li = lane & 15, g = lane >> 4;
     const int row = 4 * (g >> 1) + (li >> 2);
 #pragma unroll
     for (int d = 0; d < DB; ++d) {
-      const int c = 32 * d + 16 * (g & 1) + 4 * (li & 3);
+      const int c = c0 + 32 * d + 16 * (g & 1) + 4 * (li & 3);
       lo[d] = 2 * (tile_elem(row, c >> 3) + (c & 7));
       hi[d] = 2 * (tile_elem(row + 8, c >> 3) + (c & 7));
     }
@@ -172,6 +174,20 @@ struct TileDMA {
     for (int r = 0; r < kInstr; ++r)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst(tile, r), 16, strided_offset(r, row_bytes), 0, 0, 0);
   }
+  // One tile: row(tr, ok, p) returns the address of tile row tr and sets
+  // ok = false for a row that must read as zeros.
+  template <class Row>
+  __device__ __forceinline__ void issue_gathered1(bf16* t0, Row row_at_) const {
+#pragma unroll
+    for (int r = 0; r < kInstr; ++r) {
+      bool ok;
+      const bf16* p0;
+      row_at_(row(r), ok, p0);
+      const int c = chunk16(r);
+      const void* s0 = (ok && c >= 0) ? (const void*)((const char*)p0 + c) : (const void*)kZeroChunk;
+      __builtin_amdgcn_global_load_lds(s0, dst(t0, r), 16, 0, 0);
+    }
+  }
   // Two tiles whose rows are located together: rows(tr, ok, p0, p1) returns
   // the addresses of tile row tr and sets ok = false for a row that must read
   // as zeros.
@@ -192,11 +208,34 @@ struct TileDMA {
   }
 };
 
-// Wait for this wave's outstanding global loads (direct-to-LDS included),
-// then for the whole workgroup.
-__device__ __forceinline__ void dma_barrier() {
-  __builtin_amdgcn_s_waitcnt(0);
-  __syncthreads();
+// Workgroup barriers for data exchanged through LDS. Every wave waits for
+// its own LDS operations and for its vector memory operations except the
+// VM most recent ones (direct-to-LDS loads count as vector memory
+// operations, and they complete in issue order), then the waves meet. The
+// empty asm statements keep the compiler from moving memory accesses across
+// the barrier; no global memory ordering is implied (the kernels exchange
+// data through LDS only). s_waitcnt immediate: vmcnt [3:0] (high bits
+// [15:14] zero), expcnt [6:4] = 7 (no wait), lgkmcnt [11:8] = 0.
+template <int VM = 0>
+__device__ __forceinline__ void lds_sync() {
+  static_assert(VM >= 0 && VM <= 15, "vmcnt immediate");
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0x0070 | VM);
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
+}
+
+// The tile loop's barrier: this wave's loads (the tile about to be read)
+// have landed, and every wave is past its reads of the other buffer.
+__device__ __forceinline__ void dma_barrier() { lds_sync<0>(); }
+
+// Barrier for an LDS hand-over inside a tile step: global loads in flight
+// (the next tile) keep flying (vmcnt left at its maximum, 63).
+__device__ __forceinline__ void lds_barrier() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);
+  __builtin_amdgcn_s_barrier();
+  __asm__ volatile("" ::: "memory");
 }
 
 }  // namespace wmx

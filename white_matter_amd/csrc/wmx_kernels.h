@@ -14,9 +14,24 @@ enum Mode {
   kVarlen = 2,  // packed segments addressed through flat query/key indices
 };
 
+// Backward workspace: fp32 dK/dV accumulators (varlen schedules whose key
+// rows repeat), then from a 256-byte boundary the bf16 dS buffer: per query
+// head and problem (batch row or segment) a block of keys x ld elements,
+// ld = queries rounded up to 128, holding dS^T (element [j * ld + i] for key
+// j and query i).
+__host__ __device__ inline int64_t bwd_acc_bytes(const wmx_attn_args& a) {
+  if (!a.query_indices || a.keys_unique) return 0;
+  return (int64_t)2 * a.batch * a.key_extent * a.kv_heads * a.head_dim * (int64_t)sizeof(float);
+}
+__host__ __device__ inline int64_t bwd_ds_offset(const wmx_attn_args& a) { return (bwd_acc_bytes(a) + 255) & ~(int64_t)255; }
+__host__ __device__ inline int64_t ds_ld(int nq) { return ((int64_t)nq + 127) & ~(int64_t)127; }
+int64_t bwd_ds_bytes(const wmx_attn_args& a);  // 0 when the layout has no dS buffer
+bool bwd_uses_ds(const wmx_attn_args& a);      // the workspace holds the dS buffer
+
 int launch_fwd(const wmx_attn_args& a, hipStream_t stream);
 int launch_bwd_preprocess(const wmx_attn_args& a, hipStream_t stream);
 int64_t bwd_workspace_size(const wmx_attn_args& a);
+int64_t bwd_min_workspace_size(const wmx_attn_args& a);
 int launch_bwd(const wmx_attn_args& a, hipStream_t stream);
 int launch_bwd_dq(const wmx_attn_args& a, hipStream_t stream);
 int launch_bwd_dkv(const wmx_attn_args& a, hipStream_t stream);

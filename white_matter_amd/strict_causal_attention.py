@@ -372,21 +372,25 @@ _TILE = 128  # rows of the kernels' query and key tiles
 _STEP = 64  # rows of the tiles their loops step over
 
 
-def _work_units(metadata: StrictCausalMetadata) -> tuple[torch.Tensor, torch.Tensor]:
-    """The (segment, 128-row tile) units of the query-tiled kernels (forward,
-    dQ) and of the key-tiled kernel (dK/dV), heaviest first, as int32 (n, 2)
-    device tensors cached on the metadata object. A unit's cost is the number
-    of 64-row tiles its loop visits (then its row count): segments are
-    bottom-right causal, so query i of a segment with nq queries and nk keys
-    sees keys 0 .. nk - nq + i; a query tile visits the key tiles up to its
-    last row's bound, a key tile the query tiles from the one holding the
-    first row that sees its first key."""
+def _work_units(metadata: StrictCausalMetadata) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
+    """The kernels' work lists and dS layout, cached on the metadata object:
+    the (segment, tile) units of the query-tiled kernels (forward, dQ: 128
+    rows) and of the key-tiled kernel (dK/dV: 128 keys), heaviest first, as
+    int32 (n, 2) device tensors, and the int64 (num_segments + 1) offsets of
+    the segments' dS blocks (keys x queries rounded up to 128 elements each)
+    with their total. A unit's cost is the number of 64-row tiles its loop
+    visits (then its row count): segments are bottom-right causal, so query i
+    of a segment with nq queries and nk keys sees keys 0 .. nk - nq + i; a
+    query tile visits the key tiles up to its last row's bound, a key tile
+    the query tiles from the one holding the first row that sees its first
+    key."""
     units = metadata.__dict__.get("_units")
     if units is None:
-        q_units, k_units = [], []
+        q_units, k_units, ds_blocks = [], [], []
         for s, (qs, qe, ks, ke) in enumerate(metadata.segments):
             nq, nk = qe - qs, ke - ks
             off = nk - nq
+            ds_blocks.append(nk * (-(-nq // _TILE) * _TILE))
             for t in range(0, -(-nq // _TILE)):
                 rows = min(nq, (t + 1) * _TILE) - t * _TILE
                 reach = min(nk, max(0, off + t * _TILE + rows))
@@ -403,11 +407,15 @@ def _work_units(metadata: StrictCausalMetadata) -> tuple[torch.Tensor, torch.Ten
             flat = [v for _, seg, tile in entries for v in (seg, tile)]
             return torch.tensor(flat, dtype=torch.int32).view(-1, 2).to(device)
 
-        units = metadata.__dict__["_units"] = (table(q_units), table(k_units))
+        offsets = torch.tensor([0] + ds_blocks, dtype=torch.int64).cumsum(0)
+        units = metadata.__dict__["_units"] = (table(q_units), table(k_units), offsets.to(device), int(offsets[-1]))
     return units
 
 
-def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, max_k, flags, q_units=None, k_units=None):
+def _varlen(
+    query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, max_k, flags, q_units=None, k_units=None,
+    ds_offsets=None, ds_elements=0,
+):
     return _kernels.Varlen(
         query_indices=query_indices.contiguous(),
         key_indices=key_indices.contiguous(),
@@ -422,6 +430,8 @@ def _varlen(query, key, query_indices, key_indices, cu_queries, cu_keys, max_q, 
         segment_layout=flags & 15,
         q_units=q_units,
         k_units=k_units,
+        ds_offsets=ds_offsets,
+        ds_elements=ds_elements,
     )
 
 
@@ -443,12 +453,15 @@ def strict_varlen_fwd(
     dkv_gaps: torch.Tensor,
     q_units: torch.Tensor,
     k_units: torch.Tensor,
+    ds_offsets: torch.Tensor,
+    ds_elements: int,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """Packed-segment attention read straight from (B, H, T, D) storage;
     output (B, T, H, D) with zeros for the queries outside every segment
     (`out_gaps`: rows of the (B*T, H*D) view). `dq_gaps` and `dkv_gaps`
-    (see _schedule_gaps) are kept for the backward; `q_units` and `k_units`
-    are the kernels' work lists (see _work_units)."""
+    (see _schedule_gaps) are kept for the backward; `q_units`, `k_units`,
+    `ds_offsets` and `ds_elements` are the kernels' work lists and the
+    backward's dS layout (see _work_units)."""
     q, k, v = (_kernels.operand(t) for t in (query, key, value))
     batch, heads, length, dim = q.shape
     out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
@@ -493,6 +506,8 @@ def strict_varlen_bwd(
     dkv_gaps: torch.Tensor,
     q_units: torch.Tensor,
     k_units: torch.Tensor,
+    ds_offsets: torch.Tensor,
+    ds_elements: int,
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
     """Gradients of strict_varlen_fwd; the rows no segment writes (`dq_gaps`
     of the (B*H*T, D) view of dQ, `dkv_gaps` of the (B*Hkv*N, D) views of dK
@@ -511,7 +526,8 @@ def strict_varlen_bwd(
         dv.view(-1, dim).index_fill_(0, dkv_gaps, 0)
     vis = _kernels.Visibility(
         varlen=_varlen(
-            q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags, q_units, k_units
+            q, k, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags, q_units, k_units,
+            ds_offsets, ds_elements,
         )
     )
     _kernels.backward(q, k, v, o, lse, g, dq, dk, dv, scale, vis)
@@ -528,21 +544,22 @@ def _(query, key, value, *args):
 
 
 def _varlen_setup(ctx, inputs, output):
-    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale, _, dq_gaps, dkv_gaps, qu, ku = inputs
+    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale, _, dq_gaps, dkv_gaps, qu, ku, dso = inputs[:17]
+    ctx.ds_elements = inputs[17]
     ctx.dtypes = (query.dtype, key.dtype, value.dtype)
-    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck, dq_gaps, dkv_gaps, qu, ku)
+    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck, dq_gaps, dkv_gaps, qu, ku, dso)
     ctx.set_materialize_grads(False)  # the LSE output has no gradient: no zero fill for it
 
 
 def _varlen_backward(ctx, dout, dlse):
-    query, key, value, out, lse, qi, ki, cq, ck, dq_gaps, dkv_gaps, qu, ku = ctx.saved_tensors
+    query, key, value, out, lse, qi, ki, cq, ck, dq_gaps, dkv_gaps, qu, ku, dso = ctx.saved_tensors
     if dout is None:
         dout = torch.zeros_like(out)
     dq, dk, dv = strict_varlen_bwd(
         query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.flags, ctx.scale,
-        dq_gaps, dkv_gaps, qu, ku,
+        dq_gaps, dkv_gaps, qu, ku, dso, ctx.ds_elements,
     )
-    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 13
+    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 15
 
 
 strict_varlen_fwd.register_autograd(_varlen_backward, setup_context=_varlen_setup)

@@ -275,8 +275,8 @@ def pmc_summary(dirs) -> dict:
 def main(argv=None) -> int:
     parser = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     parser.add_argument("--gpus", type=int, default=1)
-    parser.add_argument("--steps", type=int, default=20)
-    parser.add_argument("--warmup", type=int, default=3)
+    parser.add_argument("--steps", type=int, default=100)
+    parser.add_argument("--warmup", type=int, default=10)
     parser.add_argument("--kernel-reps", type=int, default=20)
     parser.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
@@ -319,10 +319,12 @@ def main(argv=None) -> int:
     dense_pairs = batch * length * (length - 1) // 2
     flops = 14 * dim * heads * pairs
     leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    # the output gradient is an input of the backward, resident like Q/K/V
+    grad_out = torch.ones(batch, length, heads, dim, device=device, dtype=torch.bfloat16)
 
     def step():
         out = strict_causal_attention(*leaves, metadata=metadata)
-        torch.autograd.grad(out, leaves, torch.ones_like(out))
+        torch.autograd.grad(out, leaves, grad_out)
 
     for _ in range(args.warmup):
         step()
@@ -440,11 +442,13 @@ def cyclic_line(device, stride=4):
     kl, vl = k.clone().requires_grad_(), v.clone().requires_grad_()
     ql = [t.clone().requires_grad_() for t in qs]
 
+    grads = [torch.ones(batch, heads, g.numel(), dim, device=device, dtype=torch.bfloat16) for g in groups]
+
     def full_pass():
         for r in range(stride):
             out = cyclic_attention(ql[r], kl, vl, query_stride=stride, query_offset=r, strict_past=True,
                                    metadata=metas[r], backend="tilelang")
-            torch.autograd.grad(out, (ql[r], kl, vl), torch.ones_like(out))
+            torch.autograd.grad(out, (ql[r], kl, vl), grads[r])
 
     for _ in range(2):
         full_pass()

@@ -469,6 +469,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   __shared__ __attribute__((aligned(16))) float stat_lds[2][2][BMQ];  // lse * log2e, delta
   __shared__ __attribute__((aligned(16))) int qdoc_lds[2][2][BMQ];    // document id, document start
   __shared__ int red_lds[NW];
+  // per key of the workgroup: first query row that sees it, document id,
+  // document query end (kept in LDS rather than in registers)
+  __shared__ int key_lds[3][BNK];
 
   const int group = a.q_heads / a.kv_heads;
 
@@ -578,25 +581,43 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   auto issue_meta = [&](auto bufc, int hq, int m0) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
     if (wave == 0) {
-      const int m = m0 + lane;
-      const bool ok = m < nq;
-      int rb, rt;
-      pb.query_loc(ok ? m : 0, rb, rt);
-      const int64_t idx = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
-      const void* zero = (const void*)kZeroChunk;
-      __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.lse + idx) : zero, (lds_void*)&stat_lds[B][0][0], 4, 0, 0);
-      __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.delta + idx) : zero, (lds_void*)&stat_lds[B][1][0], 4, 0, 0);
-      if constexpr (MODE == kDoc) {
-        const int64_t di = (int64_t)b * a.q_len + m;
-        __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.q_seg + di) : zero, (lds_void*)&qdoc_lds[B][0][0], 4, 0, 0);
-        __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.q_start + di) : zero, (lds_void*)&qdoc_lds[B][1][0], 4, 0, 0);
+      // rows of a dense problem, or of a segment with consecutive query slots,
+      // are consecutive entries of LSE, delta and the document arrays
+      const bool consecutive = MODE != kVarlen || (a.segment_layout & kQueriesConsecutive);
+      if (consecutive) {
+        // one buffer resource per array, this lane's row at byte 4 * lane
+        // (rows past nq fall outside the resource and read as zeros)
+        const int nvalid = min(max(nq - m0, 0), kTileRows) * 4;
+        const int64_t r0 = ((int64_t)qrows.qrow * a.q_heads + hq) * a.q_len + qrows.qfirst + m0;
+        const unsigned off = 4u * lane;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.lse + r0, nvalid), (lds_void*)&stat_lds[B][0][0], 4, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.delta + r0, nvalid), (lds_void*)&stat_lds[B][1][0], 4, off, 0, 0, 0);
+        if constexpr (MODE == kDoc) {
+          const int64_t d0 = (int64_t)b * a.q_len + m0;
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.q_seg + d0, nvalid), (lds_void*)&qdoc_lds[B][0][0], 4, off, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.q_start + d0, nvalid), (lds_void*)&qdoc_lds[B][1][0], 4, off, 0, 0, 0);
+        }
+      } else if constexpr (MODE == kVarlen) {
+        const int m = m0 + lane;
+        const bool ok = m < nq;
+        int rb, rt;
+        pb.query_loc(ok ? m : 0, rb, rt);
+        const int64_t idx = ((int64_t)rb * a.q_heads + hq) * a.q_len + rt;
+        const void* zero = (const void*)kZeroChunk;
+        __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.lse + idx) : zero, (lds_void*)&stat_lds[B][0][0], 4, 0, 0);
+        __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.delta + idx) : zero, (lds_void*)&stat_lds[B][1][0], 4, 0, 0);
       }
     }
   };
 
   // first query row that sees this lane's key (INT_MAX for a dead key): the
-  // causal/offset rule is then one comparison per score
-  const int m_lo = !k_live ? INT_MAX : (slot0 && n == 0) ? 0 : pb.bound.first_row(n, nq);
+  // causal/offset rule is then one comparison per score. Read back from LDS
+  // in each step (published by the first tile barrier).
+  if (!dp_side && half == 0) {
+    key_lds[0][pair * 32 + col] = !k_live ? INT_MAX : (slot0 && n == 0) ? 0 : pb.bound.first_row(n, nq);
+    key_lds[1][pair * 32 + col] = kseg_n;
+    key_lds[2][pair * 32 + col] = kqend_n;
+  }
 
   // One query tile against the pair's 32 keys: the first half runs before
   // the P hand-over barrier, the second after it.
@@ -619,7 +640,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     // every pair of the tile is visible to this pair's keys: no per-element mask
     const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= pair_m_begin &&
                       m0 + BMQ <= nq && pb.bound.lim(m0) >= pair_key0 + 31;
-    const int lo = m_lo - m0, hi = nq - m0;  // rows ml in [lo, hi) see the key
+    const int kl = pair * 32 + (__lane_id() & 31);
+    const int lo = key_lds[0][kl] - m0, hi = nq - m0;  // rows ml in [lo, hi) see the key
+    int kseg = 0, kqend = 0;
+    if constexpr (MODE == kDoc) {
+      kseg = key_lds[1][kl];
+      kqend = key_lds[2][kl];
+    }
 #pragma unroll
     for (int mb = 0; mb < BMQ / 32; ++mb) {
       if (!full) {
@@ -631,7 +658,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
           bool keep = (ml >= lo) & (ml < hi);
           if constexpr (MODE == kDoc) {
             const int qsg = qdoc_lds[B][0][ml], qst = qdoc_lds[B][1][ml];
-            keep = keep & (((qsg == kseg_n) & (n >= qst)) | (kseg_n == -1)) & (m0 + ml < kqend_n);
+            keep = keep & (((qsg == kseg) & (n >= qst)) | (kseg == -1)) & (m0 + ml < kqend);
           }
           tacc[mb][r] = keep ? tacc[mb][r] : kNegInf;
         }

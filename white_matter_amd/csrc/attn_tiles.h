@@ -240,7 +240,8 @@ template <int MODE, int D, int NW = 4>
 struct QueryTiles {
   const bf16 *qslice, *gslice;  // slot 0 of the queries' row, head 0
   int64_t qst, gst, qhs, ghs;   // slot and head strides (elements)
-  int qfirst;                   // strided: query m at slot qfirst + m
+  int qfirst;                   // strided: query m at slot qfirst + m of row qrow
+  int qrow;
   int nq;
   bool strided;
 
@@ -248,9 +249,11 @@ struct QueryTiles {
     nq = pb.nq;
     int qb0 = pb.b;
     qfirst = 0;
+    qrow = pb.b;
     if constexpr (MODE == kVarlen) {
       if (nq > 0) pb.query_loc(0, qb0, qfirst);
     }
+    qrow = qb0;
     qslice = row_at(a.q, a.q_stride, qb0, 0, 0);
     gslice = row_at(a.dout, a.do_stride, qb0, 0, 0);
     qst = a.q_stride[2];

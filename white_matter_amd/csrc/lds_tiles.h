@@ -59,6 +59,11 @@ template <class T>
 __device__ __forceinline__ void opaque(T& x) {
   __asm__ volatile("" : "+v"(x));
 }
+// The same for a wave-uniform value kept in a scalar register.
+template <class T>
+__device__ __forceinline__ void opaque_s(T& x) {
+  __asm__ volatile("" : "+s"(x));
+}
 
 // This lane's byte offsets for the row operands of a 32-row block: row r
 // (= lane % 32), k-steps s < KS. Row blocks 32 rows apart share the swizzle,
@@ -168,8 +173,10 @@ struct TileDMA {
 #pragma unroll
     for (int r = 0; r < kInstr; ++r) __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst(tile, r), 16, off[r], 0, 0, 0);
   }
-  // Offsets formed at issue time (no registers held between tiles).
+  // Offsets formed at issue time (no registers held between tiles: the
+  // opaque row stride keeps the compiler from hoisting them out of the loop).
   __device__ __forceinline__ void issue_strided_rows(const rsrc_t& rs, bf16* tile, int row_bytes) const {
+    opaque_s(row_bytes);
 #pragma unroll
     for (int r = 0; r < kInstr; ++r)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst(tile, r), 16, strided_offset(r, row_bytes), 0, 0, 0);

@@ -124,7 +124,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
     delta = valid_q ? a.delta[r] : 0.f;
   }
 
-  int qseg_i = 0, qstart_i = 0, kt_begin_main = 0;
+  int qseg_i = 0, qstart_i = 0, kt_begin_main = 0, qstart_min_w = 0;
   if constexpr (MODE == kDoc) {
     if (valid_q) {
       qseg_i = a.q_seg[(int64_t)b * a.q_len + i];
@@ -137,6 +137,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
     __syncthreads();
     v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
     kt_begin_main = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v / BN);  // uniform: keeps the tile loop scalar
+    // smallest document start of this wave's rows: no key below it outside tile 0
+    int u = valid_q ? qstart_i : INT_MAX;
+    for (int o = 32; o > 0; o >>= 1) u = min(u, __shfl_xor(u, o));
+    qstart_min_w = __builtin_amdgcn_readfirstlane(u);
   }
   int kt_end = (lim_max_wg + 1 + BN - 1) / BN;
   if (slot0 && kt_end < 1) kt_end = 1;
@@ -239,7 +243,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
       keys.issue(a, pb, dma, n1, B ? k_lds0 : k_lds1, B ? v_lds0 : v_lds1);
       next_meta = load_meta(n1);
     }
-    const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    if constexpr (MODE == kDoc) wave_sees = wave_sees && (n0 == 0 || n0 + BN > qstart_min_w);
     if (wave_sees) {
       bool masked = !((n0 + BN - 1 <= lim_min_wave) && (n0 + BN <= nk));
       if constexpr (MODE == kDense) masked = masked || a.key_mask != nullptr;
@@ -312,7 +317,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
   const bool wave_live = wave_first < nq;
   const int lim_max_wave = pb.bound.lim(min(wave_first + 31, nq - 1));
 
-  int qseg_i = 0, qstart_i = 0, kt_begin_main = 0;
+  int qseg_i = 0, qstart_i = 0, kt_begin_main = 0, qstart_min_w = 0;
   if constexpr (MODE == kDoc) {
     if (valid_q) {
       qseg_i = a.q_seg[(int64_t)b * a.q_len + i];
@@ -325,6 +330,10 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
     __syncthreads();
     v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
     kt_begin_main = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v / BN);  // uniform: keeps the tile loop scalar
+    // smallest document start of this wave's rows: no key below it outside tile 0
+    int u = valid_q ? qstart_i : INT_MAX;
+    for (int o = 32; o > 0; o >>= 1) u = min(u, __shfl_xor(u, o));
+    qstart_min_w = __builtin_amdgcn_readfirstlane(u);
   }
   int kt_end = (lim_max_wg + 1 + BN - 1) / BN;
   if (slot0 && kt_end < 1) kt_end = 1;
@@ -415,7 +424,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
       issue_ds(n1, B ? s_lds0 : s_lds1);
       next_meta = load_meta(n1);
     }
-    const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    if constexpr (MODE == kDoc) wave_sees = wave_sees && (n0 == 0 || n0 + BN > qstart_min_w);
     if (wave_sees) tile_step(n0, B, kcur, scur);
     if (more) store_meta(B ^ 1, next_meta);
   };

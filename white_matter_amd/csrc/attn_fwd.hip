@@ -112,15 +112,22 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
     v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
     kt_begin_main = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v / BN);  // uniform: keeps the tile loop scalar
   }
-  // document of this wave's rows when they all share one (ids are sorted)
-  int qseg_w = 0, qstart_w = 0;
+  // document of this wave's rows when they all share one (ids are sorted),
+  // and the smallest document start of its rows: the wave sees no key below
+  // it outside tile 0 (which holds the only keys of every document, as in
+  // the reference's tile skipping)
+  int qseg_w = 0, qstart_w = 0, qstart_min_w = 0;
   bool q_uniform = false;
   if constexpr (MODE == kDoc) {
     qseg_w = __builtin_amdgcn_readfirstlane(qseg_i);
     q_uniform = __all(!valid_q || qseg_i == qseg_w);
-    int v = valid_q ? qstart_i : INT_MIN;
-    for (int o = 32; o > 0; o >>= 1) v = max(v, __shfl_xor(v, o));
+    int v = valid_q ? qstart_i : INT_MIN, u = valid_q ? qstart_i : INT_MAX;
+    for (int o = 32; o > 0; o >>= 1) {
+      v = max(v, __shfl_xor(v, o));
+      u = min(u, __shfl_xor(u, o));
+    }
     qstart_w = __builtin_amdgcn_readfirstlane(v);  // largest document start of the wave's rows
+    qstart_min_w = __builtin_amdgcn_readfirstlane(u);
   }
 
   // ---- key tile range: tile 0 stays when it holds the shared dummy ----
@@ -251,7 +258,8 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
       keys.issue(a, pb, dma, n1, knext, vnext);
       next_meta = load_meta(n1);
     }
-    const bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    bool wave_sees = wave_live && (n0 <= lim_max_wave || (slot0 && n0 == 0));
+    if constexpr (MODE == kDoc) wave_sees = wave_sees && (n0 == 0 || n0 + BN > qstart_min_w);
     if (wave_sees) {
       // Per-element masks are needed on the causal diagonal, at document
       // boundaries and under a key mask; the wave decides uniformly.

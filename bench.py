@@ -12,7 +12,8 @@ value = 14 * D * Hq * P / step time, P = visible (query, key) pairs counted
 exactly from the metadata (the reference's FLOP convention,
 benchmarks/_flop_counter.py:33-34). Per-kernel averages come from HIP events
 on the launch stream; the dominant kernel gives the roofline object.
-Secondary fields: C4 KV-pool decode GB/s and C3 cyclic fwd+bwd TFLOP/s.
+Secondary fields: C4 KV-pool decode GB/s, C4 prefill forward TFLOP/s, C3 cyclic fwd+bwd
+TFLOP/s (stride 4; strides 2 and 8 and the dummy-slot variant in `cyclic_variants`).
 The CPU baseline times the oracle (float32, dense mask) on a bounded sample.
 """
 
@@ -396,7 +397,9 @@ def main(argv=None) -> int:
 
     if not args.no_secondary:
         line["decode"] = decode_line(device)
+        line["prefill"] = prefill_line(device)
         line["cyclic"] = cyclic_line(device)
+        line["cyclic_variants"] = [cyclic_line(device, 2), cyclic_line(device, 8), cyclic_line(device, 4, dummy=True)]
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(q, k, v, metadata, args.cpu_budget)
@@ -427,17 +430,20 @@ def decode_line(device):
     }
 
 
-def cyclic_line(device, stride=4):
-    """C3: cyclic fwd+bwd over a full pass of `stride` residues, no dummy
-    (strict_past=True), packed documents from prepare_feedback_metadata."""
+def cyclic_line(device, stride=4, dummy=False):
+    """C3: cyclic fwd+bwd over a full pass of `stride` residue calls, packed
+    documents from prepare_feedback_metadata. Without a dummy the bound is
+    strict (strict_past=True); with one, key slot 0 is the dummy (id -1) and
+    the bound is inclusive, as the model calls it."""
     from white_matter_amd import cyclic_attention, prepare_feedback_metadata
 
     batch, heads, length, dim = 8, 16, 2048, 128
     gen = torch.Generator().manual_seed(3)
     docs = geometric_documents(batch, length, 3).to(device)
     groups = [torch.arange(r, length, stride, device=device) for r in range(stride)]
-    metas = prepare_feedback_metadata(docs, groups, length, use_dummy_token=False)
-    k, v = ((torch.randn(batch, heads, length, dim, generator=gen) * dim**-0.5).to(device, torch.bfloat16) for _ in range(2))
+    keys = length + int(dummy)
+    metas = prepare_feedback_metadata(docs, groups, keys, use_dummy_token=dummy)
+    k, v = ((torch.randn(batch, heads, keys, dim, generator=gen) * dim**-0.5).to(device, torch.bfloat16) for _ in range(2))
     qs = [(torch.randn(batch, heads, g.numel(), dim, generator=gen) * dim**-0.5).to(device, torch.bfloat16) for g in groups]
     kl, vl = k.clone().requires_grad_(), v.clone().requires_grad_()
     ql = [t.clone().requires_grad_() for t in qs]
@@ -446,24 +452,55 @@ def cyclic_line(device, stride=4):
 
     def full_pass():
         for r in range(stride):
-            out = cyclic_attention(ql[r], kl, vl, query_stride=stride, query_offset=r, strict_past=True,
+            out = cyclic_attention(ql[r], kl, vl, query_stride=stride, query_offset=r, strict_past=not dummy,
                                    metadata=metas[r], backend="tilelang")
             torch.autograd.grad(out, (ql[r], kl, vl), grads[r])
 
     for _ in range(2):
         full_pass()
     ms = Timer()(full_pass, 10)
-    # visible pairs of a full pass: strict document-causal pairs, sum of L(L-1)/2
+    # visible pairs of a full pass: per document, L(L-1)/2 strict pairs, or
+    # L(L+1)/2 with the dummy (every query also sees slot 0)
     pairs = 0
     for b in range(batch):
         _, counts = torch.unique_consecutive(docs[b].cpu(), return_counts=True)
-        pairs += int((counts * (counts - 1) // 2).sum())
+        pairs += int((counts * (counts + (1 if dummy else -1)) // 2).sum())
     tflops = 14 * dim * heads * pairs / (ms * 1e-3) / 1e12
+    bound = "dummy slot, inclusive" if dummy else "strict_past"
     return {
-        "workload": f"C3 cyclic stride {stride} full pass, strict_past, geometric documents, fwd+bwd",
+        "workload": f"C3 cyclic stride {stride} full pass, {bound}, geometric documents, fwd+bwd",
         "ms_per_pass": round(ms, 4),
         "tflops": round(tflops, 2),
         "frac_mfma": round(tflops / PEAK_BF16_TFLOPS, 4),
+    }
+
+
+def prefill_line(device, seed=1, batch=32, heads=16, dim=128, chunk=256):
+    """C4 prefill: a chunk of 256 new queries per row after a cached prefix
+    P_b ~ U{512..8192} (query_start = P as a tensor, kv_lengths = P + 256),
+    forward only, FLOPs 4*D*Hq*sum_b sum_i (P_b + i)."""
+    from white_matter_amd import strict_causal_attention
+
+    gen = torch.Generator().manual_seed(seed)
+    prefix = torch.from_numpy(np.random.default_rng(seed).integers(512, 8192, size=batch, endpoint=True))
+    capacity = int(prefix.max()) + chunk
+    q = (torch.randn(batch, heads, chunk, dim, generator=gen) * dim**-0.5).to(device, torch.bfloat16)
+    k = torch.empty(batch, heads, capacity, dim, device=device, dtype=torch.bfloat16).normal_(0, dim**-0.5)
+    v = torch.empty_like(k).normal_(0, dim**-0.5)
+    start, lengths = prefix.to(device), (prefix + chunk).to(device)
+    with torch.no_grad():
+        fn = lambda: strict_causal_attention(q, k, v, query_start=start, kv_lengths=lengths)  # noqa: E731
+        for _ in range(3):
+            fn()
+        ms = Timer()(fn, 20)
+    pairs = int(prefix.sum()) * chunk + batch * chunk * (chunk - 1) // 2
+    tflops = 4 * dim * heads * pairs / (ms * 1e-3) / 1e12
+    return {
+        "workload": f"C4 prefill B={batch} H=Hkv={heads} D={dim}, {chunk} new queries after a cached prefix ~U[512,8192], fwd",
+        "ms": round(ms, 4),
+        "tflops": round(tflops, 2),
+        "frac_mfma": round(tflops / PEAK_BF16_TFLOPS, 4),
+        "pairs": pairs,
     }
 
 

@@ -122,10 +122,12 @@ typedef struct wmx_attn_args {
                                  slots of one row; bit 1: its keys 1.. are consecutive
                                  slots following key 1 (key 0 may be the dummy) */
   float softmax_scale;
-  /* Optional varlen work lists, [count][2] int32 (segment, 128-row tile), in
-   * the order the kernels should take them (heaviest first). With them the
-   * kernels visit exactly these units; without them every (segment, tile
-   * < max / 128) pair, most of which are empty for short segments. */
+  /* Optional work lists, [count][2] int32 (segment or batch row, 128-row
+   * tile), in the order the kernels should take them (heaviest first). With
+   * them the kernels visit exactly these units; without them every (segment,
+   * tile < max / 128) pair, most of which are empty for short segments, or
+   * every (batch row, tile) pair from the last tile down. k_units needs a
+   * varlen schedule. */
   const int32_t* q_units;     /* query tiles: forward and dQ */
   const int32_t* k_units;     /* key tiles: dK/dV */
   int32_t num_q_units;

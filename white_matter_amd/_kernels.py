@@ -89,6 +89,7 @@ class Visibility:
     key_mask: torch.Tensor | None = None  # bool (B, Tk)
     documents: tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor] | None = None
     varlen: Varlen | None = None
+    q_units: torch.Tensor | None = None  # int32 (n, 2) (batch row, query tile), heaviest first (dense)
 
     def fill(self, args: _native.AttnArgs) -> None:
         args.query_stride = self.query_stride
@@ -101,6 +102,8 @@ class Visibility:
             args.key_mask_stride = self.key_mask.stride(0)
         if self.documents is not None:
             args.q_seg, args.k_seg, args.q_start, args.k_qend = (t.data_ptr() for t in self.documents)
+        if self.q_units is not None:
+            args.q_units, args.num_q_units = self.q_units.data_ptr(), self.q_units.shape[0]
         if self.varlen is not None:
             s = self.varlen
             args.query_indices = s.query_indices.data_ptr()
@@ -120,6 +123,29 @@ class Visibility:
                 args.k_units, args.num_k_units = s.k_units.data_ptr(), s.k_units.shape[0]
             if s.ds_offsets is not None:
                 args.ds_offsets, args.ds_elements = s.ds_offsets.data_ptr(), s.ds_elements
+
+
+QUERY_TILE = 128  # query rows per forward / dQ workgroup
+KEY_STEP = 64  # key rows per step of their tile loops
+
+
+def dense_units(
+    batch: int, q_len: int, kv_len: int, query_offset: int, row_offset: torch.Tensor | None,
+    row_limit: torch.Tensor | None, device: torch.device,
+) -> torch.Tensor:
+    """Work list of a dense problem with per-row bounds: the (batch row,
+    128-row query tile) pairs ordered by the number of 64-key tiles they
+    visit, largest first, computed on the device (no host synchronisation).
+    Query i of row b sees key slots j <= min(offset_b + i, limit_b)."""
+    tiles = -(-q_len // QUERY_TILE)
+    last = torch.clamp(torch.arange(tiles, device=device) * QUERY_TILE + QUERY_TILE - 1, max=q_len - 1)
+    off = row_offset.to(torch.int64)[:, None] if row_offset is not None else torch.full((batch, 1), query_offset, device=device)
+    bound = off + last[None, :]
+    if row_limit is not None:
+        bound = torch.minimum(bound, row_limit.to(torch.int64)[:, None])
+    steps = (bound.clamp(-1, kv_len - 1) + KEY_STEP) // KEY_STEP
+    order = torch.argsort(steps.flatten(), descending=True, stable=True)
+    return torch.stack((order // tiles, order % tiles), 1).to(torch.int32)
 
 
 def _base_args(q, k, v, o, lse, scale: float, vis: Visibility, q_len: int) -> _native.AttnArgs:

@@ -54,7 +54,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
   // ---- the work units: (batch row or segment, query tile, head) ----
   const int qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
   const unsigned outer = MODE == kVarlen ? (unsigned)a.num_segments : (unsigned)a.batch;
-  const int32_t* list = MODE == kVarlen ? a.q_units : nullptr;
+  const int32_t* list = a.q_units;  // (batch row or segment, tile) pairs, heaviest first
   const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
 
   // this workgroup's unit: 128 query rows of one (batch row or segment, query head)
@@ -303,7 +303,7 @@ template <int D, int MODE>
 static int launch_fwd_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + kFwdBM - 1) / kFwdBM;
   const int64_t outer = MODE == kVarlen ? a.num_segments : a.batch;
-  const int64_t per_head = (MODE == kVarlen && a.q_units) ? a.num_q_units : qtiles * outer;
+  const int64_t per_head = a.q_units ? a.num_q_units : qtiles * outer;
   const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;

@@ -55,12 +55,12 @@ int check_common(const wmx_attn_args* a, bool backward) {
     if (a->q_seg) return fail(WMX_E_INVALID, "varlen schedule and document metadata are exclusive");
     if (a->key_mask) return fail(WMX_E_INVALID, "varlen schedule and key_mask are exclusive");
     if (a->row_offset || a->row_limit) return fail(WMX_E_INVALID, "varlen schedule takes no row offsets");
-    if ((a->q_units && a->num_q_units < 0) || (a->k_units && a->num_k_units < 0))
-      return fail(WMX_E_INVALID, "negative work-list length");
+    if (a->k_units && a->num_k_units < 0) return fail(WMX_E_INVALID, "negative work-list length");
     if (a->ds_offsets && a->ds_elements < 0) return fail(WMX_E_INVALID, "negative ds_elements");
-  } else if (a->q_units || a->k_units || a->ds_offsets) {
-    return fail(WMX_E_INVALID, "work lists and dS offsets need a varlen schedule");
+  } else if (a->k_units || a->ds_offsets) {
+    return fail(WMX_E_INVALID, "key work lists and dS offsets need a varlen schedule");
   }
+  if (a->q_units && a->num_q_units < 0) return fail(WMX_E_INVALID, "negative work-list length");
   if (a->q_seg && (!a->k_seg || !a->q_start || !a->k_qend))
     return fail(WMX_E_INVALID, "document metadata needs all four arrays");
   if (a->q_seg && a->key_mask) return fail(WMX_E_INVALID, "document metadata and key_mask are exclusive");

@@ -248,6 +248,9 @@ def strict_dense_fwd(
     out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
     lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
     vis = _dense_visibility(query_offset, row_offset, row_limit, key_mask, keep_slot0)
+    if row_offset is not None or row_limit is not None:
+        # ragged rows (cached prefixes): heaviest tiles first
+        vis.q_units = _kernels.dense_units(batch, length, k.shape[2], query_offset, row_offset, row_limit, q.device)
     _kernels.forward(q, k, v, out.transpose(1, 2), lse, scale, vis)
     return out, lse
 

@@ -641,10 +641,12 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     const bf16* rows = DP ? (B ? g_lds1 : g_lds0) : (B ? q_lds1 : q_lds0);  // dO rows for dP, Q rows for S
     rrd.refresh();
 #pragma unroll
-    for (int mb = 0; mb < BMQ / 32; ++mb) {
-      tacc[mb] = f32x16{};
+    for (int mb = 0; mb < BMQ / 32; ++mb) tacc[mb] = f32x16{};
+    // k-step major: the two halves' operand reads interleave
 #pragma unroll
-      for (int s = 0; s < KS; ++s) tacc[mb] = mfma32(rrd.get(rows, s, mb), kvf[s], tacc[mb]);
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int mb = 0; mb < BMQ / 32; ++mb) tacc[mb] = mfma32(rrd.get(rows, s, mb), kvf[s], tacc[mb]);
     }
     if constexpr (DP) return;
     // every pair of the tile is visible to this pair's keys: no per-element mask

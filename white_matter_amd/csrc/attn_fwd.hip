@@ -177,10 +177,13 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
     vrd.refresh();
     f32x16 sacc[BN / 32];
 #pragma unroll
-    for (int nb = 0; nb < BN / 32; ++nb) {
-      sacc[nb] = f32x16{};
+    for (int nb = 0; nb < BN / 32; ++nb) sacc[nb] = f32x16{};
+    // k-step major: the two blocks' operand reads interleave, so each read
+    // has the other block's product to hide behind
 #pragma unroll
-      for (int s = 0; s < KS; ++s) sacc[nb] = mfma32(krd.get(kt, s, nb), qf[s], sacc[nb]);
+    for (int s = 0; s < KS; ++s) {
+#pragma unroll
+      for (int nb = 0; nb < BN / 32; ++nb) sacc[nb] = mfma32(krd.get(kt, s, nb), qf[s], sacc[nb]);
     }
 
     if (masked) {

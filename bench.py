@@ -13,7 +13,8 @@ exactly from the metadata (the reference's FLOP convention,
 benchmarks/_flop_counter.py:33-34). Per-kernel averages come from HIP events
 on the launch stream; the dominant kernel gives the roofline object.
 Secondary fields: C4 KV-pool decode GB/s, C4 prefill forward TFLOP/s, C3 cyclic fwd+bwd
-TFLOP/s (stride 4; strides 2 and 8 and the dummy-slot variant in `cyclic_variants`).
+TFLOP/s (stride 4; strides 2 and 8 and the dummy-slot variant in `cyclic_variants`),
+and the fused KV-pool store GB/s beside the reference's eager steps.
 The CPU baseline times the oracle (float32, dense mask) on a bounded sample.
 """
 
@@ -283,6 +284,11 @@ def main(argv=None) -> int:
     parser.add_argument("--no-cpu-baseline", action="store_true")
     parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
     parser.add_argument(
+        "--only",
+        choices=("decode", "prefill", "cyclic", "kv_store"),
+        help="print one secondary line as JSON and exit (for profiling that path alone)",
+    )
+    parser.add_argument(
         "--copy-calibration",
         action="store_true",
         help="first run one elementwise copy (torch.neg) of 256 MiB, the known-size kernel that scales FETCH_SIZE/WRITE_SIZE",
@@ -307,6 +313,10 @@ def main(argv=None) -> int:
     from white_matter_amd import strict_causal_attention
 
     device = torch.device("cuda:0")
+    if args.only:
+        lines = {"decode": decode_line, "prefill": prefill_line, "cyclic": cyclic_line, "kv_store": kv_store_line}
+        print(json.dumps({args.only: lines[args.only](device)}), flush=True)
+        return 0
     if args.copy_calibration:
         # one elementwise kernel that reads and writes exactly CALIBRATION_BYTES
         src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=device)
@@ -400,6 +410,7 @@ def main(argv=None) -> int:
         line["prefill"] = prefill_line(device)
         line["cyclic"] = cyclic_line(device)
         line["cyclic_variants"] = [cyclic_line(device, 2), cyclic_line(device, 8), cyclic_line(device, 4, dummy=True)]
+        line["kv_store"] = kv_store_line(device)
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(q, k, v, metadata, args.cpu_budget)
@@ -501,6 +512,59 @@ def prefill_line(device, seed=1, batch=32, heads=16, dim=128, chunk=256):
         "tflops": round(tflops, 2),
         "frac_mfma": round(tflops / PEAK_BF16_TFLOPS, 4),
         "pairs": pairs,
+    }
+
+
+def kv_store_line(device, batch=8, channels=8, heads=16, tokens=2048, dim=64, seed=5):
+    """KV-pool store at the 24-layer model's pool shape (8 channels, 16 heads
+    of 64): bf16 keys/values straight from the per-channel projection (the
+    (C, B*T, H*D) product viewed as (B, C, H, T, D), no copy), fp32 RoPE
+    tables, written into a (B, C, H, T+1, D) pool after the dummy slot. Bytes:
+    keys and values read once and written once, cos/sin and the weights read
+    once, the slots. The reference's eager steps (rms_norm, weight, RoPE,
+    casts, two index_copy_) are timed beside it on the same GPU."""
+    import torch.nn.functional as F
+
+    from white_matter_amd import kv_pool
+
+    gen = torch.Generator().manual_seed(seed)
+    shape = (channels, batch, tokens, heads, dim)
+    k_proj = torch.randn(*shape, generator=gen).to(device, torch.bfloat16)
+    v_proj = torch.randn(*shape, generator=gen).to(device, torch.bfloat16)
+    key, value = (t.permute(1, 0, 3, 2, 4) for t in (k_proj, v_proj))  # (B, C, H, T, D) views
+    weight = (1 + 0.1 * torch.randn(channels, dim, generator=gen)).to(device)
+    angle = torch.rand(batch, tokens, dim // 2, generator=gen).to(device) * 100
+    cos, sin = torch.cat((angle, angle), -1).cos(), torch.cat((angle, angle), -1).sin()
+    keys = torch.zeros(batch, channels, heads, tokens + 1, dim, device=device, dtype=torch.bfloat16)
+    values = torch.zeros_like(keys)
+    slots = torch.arange(1, tokens + 1, device=device)
+
+    def fused():
+        kv_pool.write_pool(key, value, weight, cos, sin, keys, values, slots)
+
+    def eager():
+        normed = F.rms_norm(key, (dim,), None, 1e-6) * weight.view(1, channels, 1, 1, dim).to(key.dtype)
+        c, s = cos[:, None, None].to(key.dtype), sin[:, None, None].to(key.dtype)
+        k = ((normed * c) + (torch.cat((-normed[..., dim // 2 :], normed[..., : dim // 2]), -1) * s)).to(value.dtype)
+        keys.index_copy_(3, slots, k)
+        values.index_copy_(3, slots, value)
+
+    with torch.no_grad():
+        for fn in (fused, eager):
+            for _ in range(3):
+                fn()
+        ms = Timer()(fused, 50)
+        eager_ms = Timer()(eager, 10)
+    elements = batch * channels * heads * tokens * dim
+    moved = elements * 2 * 4 + 2 * batch * tokens * dim * 4 + channels * dim * 4 + tokens * 8
+    gbps = moved / (ms * 1e-3) / 1e9
+    return {
+        "workload": f"KV-pool store B={batch} C={channels} H={heads} T={tokens} D={dim}, bf16 projection views, fp32 RoPE",
+        "ms": round(ms, 4),
+        "gbps": round(gbps, 1),
+        "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
+        "bytes": moved,
+        "eager_reference_ms": round(eager_ms, 4),
     }
 
 

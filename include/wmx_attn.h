@@ -177,10 +177,59 @@ typedef struct wmx_decode_args {
   float softmax_scale;
 } wmx_decode_args;
 
+/*
+ * KV-pool store: the step that writes a group's keys and values into the
+ * pool (reference modules/kv_pool.py:163-172 `_apply_k_norm_rope` and the
+ * `.to(V.dtype)` cast of :216, then blocks/_execution/cyclic.py:448-458
+ * `_write_pool`'s two index_copy_ along the token axis). For every row
+ * (b, c, h, t):
+ *   x  = key[b, c, h, t, :]
+ *   y  = r(x * rsqrt(mean(x^2) + eps))            (the mean in fp32)
+ *   y  = r(y * r(w[c, :]))
+ *   k' = r(r(y * r(cos[b, t, :])) + r(rot(y) * r(sin[b, t, :])))
+ *        rot(y) = (-y[D/2:], y[:D/2])
+ *   key_pool[b, c, h, slots[t], :]   = bf16(k')
+ *   value_pool[b, c, h, slots[t], :] = bf16(value[b, c, h, t, :])
+ * where r() rounds to the key dtype (identity for fp32), as the reference
+ * evaluates each step in the key dtype. Slots must be distinct; a slot
+ * outside [0, N) is not written. value and value_pool may both be NULL
+ * (keys only).
+ */
+enum { WMX_DTYPE_F32 = 0, WMX_DTYPE_BF16 = 1 };
+
+typedef struct wmx_kv_store_args {
+  const void* key;           /* (B, C, H, T, D), dtype key_dtype */
+  const void* value;         /* (B, C, H, T, D), dtype value_dtype, or NULL */
+  const void* k_norm_weight; /* (C, D) contiguous, dtype weight_dtype */
+  const void* cos;           /* (B, T, D), dtype rope_dtype */
+  const void* sin;           /* same shape and strides as cos */
+  void* key_pool;            /* bf16 (B, C, H, N, D) */
+  void* value_pool;          /* bf16 (B, C, H, N, D), or NULL */
+  const int64_t* slots;      /* (T) pool slot of token t, in [0, N) */
+  /* element strides; head_dim stride is 1 */
+  int64_t key_stride[4];     /* [batch, channel, head, token] */
+  int64_t value_stride[4];
+  int64_t key_pool_stride[4];
+  int64_t value_pool_stride[4];
+  int64_t rope_stride[2];    /* [batch, token] */
+  int32_t key_dtype;         /* WMX_DTYPE_F32 or WMX_DTYPE_BF16 */
+  int32_t value_dtype;
+  int32_t weight_dtype;
+  int32_t rope_dtype;
+  int32_t batch;
+  int32_t channels;
+  int32_t heads;
+  int32_t tokens;
+  int32_t head_dim;          /* 64 or 128 */
+  int32_t pool_slots;        /* N */
+  float eps;
+} wmx_kv_store_args;
+
 /* Library identity and struct layout checks for FFI bindings. */
 int wmx_abi_version(void);
 size_t wmx_attn_args_size(void);
 size_t wmx_decode_args_size(void);
+size_t wmx_kv_store_args_size(void);
 const char* wmx_last_error(void);
 
 /* Forward: o and lse. (see replaced interfaces above) */
@@ -220,6 +269,12 @@ int32_t wmx_decode_num_splits(const wmx_decode_args* args);
 
 /* Single-query decode forward. */
 int wmx_decode(const wmx_decode_args* args, void* stream);
+
+/* KV-pool store (see wmx_kv_store_args): one pass over the group's keys and
+ * values, writing the pool slots. Replaces the reference's eager sequence of
+ * rms_norm, weight, RoPE, casts and index_copy_ (modules/kv_pool.py:163-172,
+ * 216; blocks/_execution/cyclic.py:448-458). */
+int wmx_kv_pool_store(const wmx_kv_store_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -5,6 +5,8 @@ src/white_matter/ops/) used to check the gfx950 kernels and the host code:
 
   oracle.metadata   numpy restatements of the three metadata builders
   oracle.attention  float64 explicit-softmax attention under the reference's masks
+  oracle.kv_pool    the KV-pool key norm, RoPE and pool write with the
+                    reference's rounding points
 
 Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may
 import this package, and only as the checker or the timed CPU baseline; the
@@ -21,5 +23,7 @@ Pinning (each function is checked against more than its own formula):
     equality of attention through the schedule with a per-query loop that
     never builds a schedule (tests/unit/test_strict_causal_attention.py:16-39);
   - attention: PyTorch's math SDPA (the reference's own call), a per-query
-    loop, equal-score and exact-zero invariants, float64 at 1e-12.
+    loop, equal-score and exact-zero invariants, float64 at 1e-12;
+  - kv_pool: the same steps written with PyTorch's F.rms_norm and tensor ops
+    in the key dtype on the CPU, and RoPE rotation invariants.
 """

@@ -1,0 +1,100 @@
+"""The fused KV-pool store (wmx_kv_pool_store) against the float64 oracle
+with the reference's rounding points, and against the reference's eager
+PyTorch steps on the GPU. Keys: the bf16 bar (max-abs <= 1e-2 * max(1,
+max|ref|), relative L2 <= 5e-3) and >= 99% bit-exact: the rms mean is
+summed in another order, so a rare rounding step lands one ulp apart (and
+RoPE's sum can cancel, which magnifies that ulp relative to the result);
+values: exact."""
+
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import kv_pool as ref
+from tests.numerics import assert_bf16_close
+from white_matter_amd import kv_pool
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+def _inputs(key_dtype, value_dtype, weight_dtype, rope_dtype, dim, shape=(2, 3, 2, 37), seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    b, c, h, t = shape
+    key = (torch.randn(b, c, h, t, dim, generator=gen) * 1.7).to(key_dtype)
+    value = torch.randn(b, c, h, t, dim, generator=gen).to(value_dtype)
+    weight = (1 + 0.2 * torch.randn(c, dim, generator=gen)).to(weight_dtype)
+    angle = torch.rand(b, t, dim // 2, generator=gen) * 20.0
+    angle = torch.cat((angle, angle), -1)
+    return key, value, weight, angle.cos().to(rope_dtype), angle.sin().to(rope_dtype)
+
+
+def _ulp_close(actual, expected):
+    actual, expected = actual.double().cpu(), expected.double().cpu()
+    assert_bf16_close(actual, expected, what="kv store keys")
+    assert (actual == expected).double().mean() >= 0.99
+
+
+@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize(
+    "dtypes",
+    [
+        (torch.bfloat16, torch.bfloat16, torch.float32, torch.float32),
+        (torch.bfloat16, torch.bfloat16, torch.bfloat16, torch.bfloat16),
+        (torch.float32, torch.float32, torch.float32, torch.float32),
+        (torch.float32, torch.bfloat16, torch.bfloat16, torch.float32),
+    ],
+)
+def test_store_matches_oracle(dim, dtypes):
+    key, value, weight, cos, sin = _inputs(*dtypes, dim)
+    pool_slots = 50
+    keys = torch.full((2, 3, 2, pool_slots, dim), 3.0, dtype=torch.bfloat16)
+    values = keys.clone()
+    slots = torch.randperm(pool_slots, generator=torch.Generator().manual_seed(1))[:37]
+    exp_k, exp_v = ref.write_pool(key, value, weight, cos, sin, keys, values, slots, 1e-6)
+    pk, pv = keys.to(DEV), values.to(DEV)
+    with torch.no_grad():
+        kv_pool.write_pool(key.to(DEV), value.to(DEV), weight.to(DEV), cos.to(DEV), sin.to(DEV), pk, pv, slots.to(DEV))
+    torch.cuda.synchronize()
+    assert torch.equal(pv.cpu(), exp_v)
+    untouched = [i for i in range(pool_slots) if i not in slots.tolist()]
+    assert torch.equal(pk.cpu()[:, :, :, untouched], exp_k[:, :, :, untouched])
+    _ulp_close(pk.cpu()[:, :, :, slots], exp_k[:, :, :, slots])
+
+
+def test_pool_views_keys_only_and_out_of_range_slots():
+    """Channel views of a larger pool (the decoder cache layout), the keys-only
+    form, and a slot past the pool that is not written."""
+    key, value, weight, cos, sin = _inputs(torch.bfloat16, torch.bfloat16, torch.float32, torch.float32, 64, (2, 2, 2, 9))
+    big = torch.zeros(2, 5, 2, 16, 64, dtype=torch.bfloat16, device=DEV)
+    view = big[:, 1:3]  # (B, C=2, H, N, D) view with the larger channel stride
+    slots = torch.tensor([0, 2, 4, 6, 8, 10, 12, 14, 16])  # 16 is outside the pool
+    with torch.no_grad():
+        kv_pool.write_pool(key.to(DEV), None, weight.to(DEV), cos.to(DEV), sin.to(DEV), view, None, slots.to(DEV))
+    torch.cuda.synchronize()
+    k = ref.k_norm_rope(key, weight, cos, sin, 1e-6).bfloat16()
+    _ulp_close(view[:, :, :, 0:16:2].cpu(), k[:, :, :, :8])
+    assert (big[:, 1:3, :, 1::2] == 0).all() and (big[:, 0] == 0).all() and (big[:, 3:] == 0).all()
+    with torch.no_grad():
+        direct = kv_pool.k_norm_rope(key.to(DEV), weight.to(DEV), cos.to(DEV), sin.to(DEV))
+    _ulp_close(direct, k)
+
+
+def test_matches_reference_eager_sequence_on_gpu():
+    """The reference's eager steps (kv_pool.py:163-172, 216; cyclic.py:448-458)
+    on the GPU, bf16 keys: the fused store is within the bf16 tolerance."""
+    key, value, weight, cos, sin = (t.to(DEV) for t in _inputs(torch.bfloat16, torch.bfloat16, torch.float32, torch.float32, 128, (2, 4, 2, 64)))
+    slots = torch.arange(64, device=DEV) * 2
+    keys = torch.zeros(2, 4, 2, 128, 128, dtype=torch.bfloat16, device=DEV)
+    values = torch.zeros_like(keys)
+    normed = F.rms_norm(key, (128,), None, 1e-6) * weight.view(1, 4, 1, 1, 128).to(key.dtype)
+    c, s = cos[:, None, None].to(key.dtype), sin[:, None, None].to(key.dtype)
+    eager = (normed * c + torch.cat((-normed[..., 64:], normed[..., :64]), -1) * s).to(torch.bfloat16)
+    ek, ev = keys.clone(), values.clone()
+    ek.index_copy_(3, slots, eager)
+    ev.index_copy_(3, slots, value)
+    with torch.no_grad():
+        kv_pool.write_pool(key, value, weight, cos, sin, keys, values, slots)
+    assert torch.equal(values, ev)
+    assert_bf16_close(keys.double().cpu(), ek.double().cpu(), what="kv store vs eager")
+    assert (keys[:, :, :, slots] == ek[:, :, :, slots]).float().mean() > 0.95

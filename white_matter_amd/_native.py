@@ -112,6 +112,41 @@ class DecodeArgs(ctypes.Structure):
     ]
 
 
+_c_i64_4 = ctypes.c_int64 * 4
+DTYPE_F32, DTYPE_BF16 = 0, 1
+
+
+class KvStoreArgs(ctypes.Structure):
+    """Mirror of wmx_kv_store_args."""
+
+    _fields_ = [
+        ("key", _vp),
+        ("value", _vp),
+        ("k_norm_weight", _vp),
+        ("cos", _vp),
+        ("sin", _vp),
+        ("key_pool", _vp),
+        ("value_pool", _vp),
+        ("slots", _vp),
+        ("key_stride", _c_i64_4),
+        ("value_stride", _c_i64_4),
+        ("key_pool_stride", _c_i64_4),
+        ("value_pool_stride", _c_i64_4),
+        ("rope_stride", _c_i64_2),
+        ("key_dtype", ctypes.c_int32),
+        ("value_dtype", ctypes.c_int32),
+        ("weight_dtype", ctypes.c_int32),
+        ("rope_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("tokens", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("pool_slots", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+    ]
+
+
 EXPORTS = (
     "wmx_abi_version",
     "wmx_attn_args_size",
@@ -127,6 +162,8 @@ EXPORTS = (
     "wmx_decode_workspace_size",
     "wmx_decode_num_splits",
     "wmx_decode",
+    "wmx_kv_store_args_size",
+    "wmx_kv_pool_store",
 )
 
 
@@ -158,12 +195,17 @@ def load() -> ctypes.CDLL:
     lib.wmx_decode_workspace_size.restype = ctypes.c_int64
     lib.wmx_decode_num_splits.argtypes = [ctypes.POINTER(DecodeArgs)]
     lib.wmx_decode_num_splits.restype = ctypes.c_int32
+    lib.wmx_kv_store_args_size.restype = ctypes.c_size_t
+    lib.wmx_kv_pool_store.argtypes = [ctypes.POINTER(KvStoreArgs), _vp]
+    lib.wmx_kv_pool_store.restype = ctypes.c_int
     if lib.wmx_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI {lib.wmx_abi_version()}, expected {ABI_VERSION}")
     if lib.wmx_attn_args_size() != ctypes.sizeof(AttnArgs):
         raise RuntimeError("wmx_attn_args layout differs between the library and the binding")
     if lib.wmx_decode_args_size() != ctypes.sizeof(DecodeArgs):
         raise RuntimeError("wmx_decode_args layout differs between the library and the binding")
+    if lib.wmx_kv_store_args_size() != ctypes.sizeof(KvStoreArgs):
+        raise RuntimeError("wmx_kv_store_args layout differs between the library and the binding")
     return lib
 
 
@@ -225,3 +267,8 @@ def decode_workspace_size(args: DecodeArgs) -> int:
 def decode(args: DecodeArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_decode(ctypes.byref(args), _stream(device)), "wmx_decode")
+
+
+def kv_pool_store(args: KvStoreArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_kv_pool_store(ctypes.byref(args), _stream(device)), "wmx_kv_pool_store")

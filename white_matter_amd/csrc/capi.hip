@@ -148,6 +148,30 @@ int wmx_attn_bwd_dkv(const wmx_attn_args* args, void* stream) {
   return launched(wmx::launch_bwd_dkv(*args, (hipStream_t)stream));
 }
 
+int wmx_kv_pool_store(const wmx_kv_store_args* a, void* stream) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->head_dim != 64 && a->head_dim != 128)
+    return fail(WMX_E_UNSUPPORTED, "kv store head_dim %d is not 64 or 128", a->head_dim);
+  if (a->batch < 0 || a->channels < 0 || a->heads < 0 || a->tokens < 0 || a->pool_slots < 0)
+    return fail(WMX_E_INVALID, "negative shape");
+  for (int dt : {a->key_dtype, a->value_dtype, a->weight_dtype, a->rope_dtype})
+    if (dt != WMX_DTYPE_F32 && dt != WMX_DTYPE_BF16) return fail(WMX_E_INVALID, "dtype must be WMX_DTYPE_F32 or WMX_DTYPE_BF16");
+  if (!(a->eps >= 0.f)) return fail(WMX_E_INVALID, "eps must be >= 0");
+  if ((int64_t)a->batch * a->channels * a->heads * a->tokens == 0) return WMX_OK;
+  if (!a->key || !a->k_norm_weight || !a->cos || !a->sin || !a->key_pool || !a->slots)
+    return fail(WMX_E_INVALID, "kv store pointer is NULL");
+  if (!a->value != !a->value_pool) return fail(WMX_E_INVALID, "value and value_pool are given together");
+  if (!aligned16(a->key) || !aligned16(a->value) || !aligned16(a->k_norm_weight) || !aligned16(a->cos) ||
+      !aligned16(a->sin) || !aligned16(a->key_pool) || !aligned16(a->value_pool) || !aligned8(a->slots))
+    return fail(WMX_E_INVALID, "kv store operands must be 16-byte aligned");
+  if (!strides_vec8(a->key_stride, 4) || !strides_vec8(a->value_stride, 4) || !strides_vec8(a->key_pool_stride, 4) ||
+      !strides_vec8(a->value_pool_stride, 4) || !strides_vec8(a->rope_stride, 2))
+    return fail(WMX_E_INVALID, "kv store strides must be multiples of 8 elements");
+  return launched(wmx::launch_kv_store(*a, (hipStream_t)stream));
+}
+
+size_t wmx_kv_store_args_size(void) { return sizeof(wmx_kv_store_args); }
+
 int64_t wmx_decode_workspace_size(const wmx_decode_args* args) {
   return args ? wmx::decode_workspace_size(*args) : 0;
 }

@@ -1,0 +1,166 @@
+// KV-pool store for gfx950: K-norm, weight, RoPE, casts and the pool slot
+// scatter in one pass over the group's keys and values (the eager reference
+// sequence modules/kv_pool.py:163-172,216 and blocks/_execution/cyclic.py:
+// 448-458 makes about eight passes over the keys). HBM-bound: each thread
+// moves 8 consecutive elements of a row with 16-byte accesses.
+#include "wmx_kernels.h"
+
+namespace wmx {
+
+namespace {
+
+// Round to bf16 (nearest even) and back: the reference's per-op rounding
+// when the keys are bf16.
+__device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
+
+// Eight consecutive elements as fp32 from an fp32 or bf16 array. STREAM marks
+// data read exactly once (the keys and values): a non-temporal load, which
+// keeps it from displacing the cos/sin rows that every channel re-reads.
+template <bool STREAM = false>
+__device__ __forceinline__ void load8(const void* base, int64_t off, bool bf16_src, float (&v)[8]) {
+  auto ld = [](const auto* p) { return STREAM ? __builtin_nontemporal_load(p) : *p; };
+  if (bf16_src) {
+    const u32x4 w = ld(reinterpret_cast<const u32x4*>((const bf16*)base + off));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = bf16_lo(w[e]);
+      v[2 * e + 1] = bf16_hi(w[e]);
+    }
+  } else {
+    const f32x4 a = ld(reinterpret_cast<const f32x4*>((const float*)base + off));
+    const f32x4 b = ld(reinterpret_cast<const f32x4*>((const float*)base + off + 4));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = a[e];
+      v[4 + e] = b[e];
+    }
+  }
+}
+
+// Pool rows are written once and not read back by this kernel: non-temporal.
+__device__ __forceinline__ void store8_bf16(void* base, int64_t off, const float (&v)[8]) {
+  const u32x4 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                   pack_bf16x2(v[6], v[7])};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>((bf16*)base + off));
+}
+
+}  // namespace
+
+// Value source: none (keys only), fp32 or bf16.
+enum ValueKind { kNoValue = 0, kValueF32 = 1, kValueBF16 = 2 };
+
+// One (b, c, t) per D/8 consecutive lanes (token-fastest, so neighbouring
+// lanes read and write neighbouring rows); each thread then walks the heads,
+// U at a time with all their loads issued before any is used (no branch
+// between them: the last group repeats its final head instead of testing),
+// so cos, sin, the norm weight and the slot are read once per token instead
+// of once per row. KEY_BF16 selects the reference's rounding after every
+// step.
+template <int D, bool KEY_BF16, int VALUE>
+__global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a, int64_t tokens_total) {
+  // Every product and sum is rounded on its own, as the eager sequence does:
+  // a fused multiply-add would skip the rounding of y * cos.
+#pragma clang fp contract(off)
+  constexpr int L = D / 8;  // lanes per row
+  constexpr int U = 4;      // heads in flight per thread
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t r = gid / L;
+  const int l = (int)(gid % L);  // this lane's elements: 8 l .. 8 l + 7
+  // A row's L lanes are aligned and share r, so they leave together and the
+  // shuffles below never read a lane that has left.
+  if (r >= tokens_total) return;
+  const int t = (int)(r % a.tokens);
+  const int64_t bc = r / a.tokens;
+  const int c = (int)(bc % a.channels);
+  const int b = (int)(bc / a.channels);
+  const int64_t slot = a.slots[t];
+  if (slot < 0 || slot >= a.pool_slots) return;  // out-of-range slots are not written
+  const int d0 = 8 * l;
+  auto rnd = [](float x) { return KEY_BF16 ? round_bf16(x) : x; };
+
+  float w[8], cs[8], sn[8];
+  load8(a.k_norm_weight, (int64_t)c * D + d0, a.weight_dtype == WMX_DTYPE_BF16, w);
+  const int64_t ro = (int64_t)b * a.rope_stride[0] + (int64_t)t * a.rope_stride[1] + d0;
+  load8(a.cos, ro, a.rope_dtype == WMX_DTYPE_BF16, cs);
+  load8(a.sin, ro, a.rope_dtype == WMX_DTYPE_BF16, sn);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    w[e] = rnd(w[e]);
+    cs[e] = rnd(cs[e]);
+    sn[e] = rnd(sn[e]);
+  }
+  const bool low = d0 < D / 2;  // rotate_half: element d pairs with d +- D/2, held by lane l ^ (L / 2)
+  const int64_t key_row = (int64_t)b * a.key_stride[0] + (int64_t)c * a.key_stride[1] + (int64_t)t * a.key_stride[3] + d0;
+  const int64_t kpool_row =
+      (int64_t)b * a.key_pool_stride[0] + (int64_t)c * a.key_pool_stride[1] + slot * a.key_pool_stride[3] + d0;
+  const int64_t value_row =
+      (int64_t)b * a.value_stride[0] + (int64_t)c * a.value_stride[1] + (int64_t)t * a.value_stride[3] + d0;
+  const int64_t vpool_row =
+      (int64_t)b * a.value_pool_stride[0] + (int64_t)c * a.value_pool_stride[1] + slot * a.value_pool_stride[3] + d0;
+
+  for (int h0 = 0; h0 < a.heads; h0 += U) {
+    float x[U][8], v[U][8];
+    int hu[U];
+#pragma unroll
+    for (int u = 0; u < U; ++u) hu[u] = min(h0 + u, a.heads - 1);
+#pragma unroll
+    for (int u = 0; u < U; ++u) load8<true>(a.key, key_row + hu[u] * a.key_stride[2], KEY_BF16, x[u]);
+    if constexpr (VALUE != kNoValue) {
+#pragma unroll
+      for (int u = 0; u < U; ++u) load8<true>(a.value, value_row + hu[u] * a.value_stride[2], VALUE == kValueBF16, v[u]);
+    }
+    __builtin_amdgcn_sched_barrier(0);  // keep every load of the group ahead of the first use
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+      float ss = 0.f;
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(x[u][e], x[u][e], ss);
+#pragma unroll
+      for (int o = L / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+      const float inv = 1.f / sqrtf(ss / (float)D + a.eps);
+      float y[8], out[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = rnd(rnd(x[u][e] * inv) * w[e]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float other = __shfl_xor(y[e], L / 2);
+        const float rot = low ? -other : other;
+        out[e] = rnd(rnd(y[e] * cs[e]) + rnd(rot * sn[e]));
+      }
+      if (h0 + u < a.heads) {
+        store8_bf16(a.key_pool, kpool_row + hu[u] * a.key_pool_stride[2], out);
+        if constexpr (VALUE != kNoValue) store8_bf16(a.value_pool, vpool_row + hu[u] * a.value_pool_stride[2], v[u]);
+      }
+    }
+  }
+}
+
+template <int D, bool KEY_BF16>
+void launch_kv_store_d(const wmx_kv_store_args& a, int64_t rows, dim3 grid, hipStream_t stream) {
+  if (!a.value)
+    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kNoValue>), grid, dim3(256), 0, stream, a, rows);
+  else if (a.value_dtype == WMX_DTYPE_BF16)
+    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kValueBF16>), grid, dim3(256), 0, stream, a, rows);
+  else
+    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kValueF32>), grid, dim3(256), 0, stream, a, rows);
+}
+
+int launch_kv_store(const wmx_kv_store_args& a, hipStream_t stream) {
+  const int64_t rows = (int64_t)a.batch * a.channels * a.tokens;  // each thread walks the heads
+  if (rows == 0 || a.heads == 0) return WMX_OK;
+  const int64_t threads = rows * (a.head_dim / 8);
+  const dim3 grid((unsigned)((threads + 255) / 256));
+  const bool kb = a.key_dtype == WMX_DTYPE_BF16;
+  if (a.head_dim == 64) {
+    if (kb) launch_kv_store_d<64, true>(a, rows, grid, stream);
+    else launch_kv_store_d<64, false>(a, rows, grid, stream);
+  } else if (a.head_dim == 128) {
+    if (kb) launch_kv_store_d<128, true>(a, rows, grid, stream);
+    else launch_kv_store_d<128, false>(a, rows, grid, stream);
+  } else {
+    return WMX_E_UNSUPPORTED;
+  }
+  return WMX_OK;
+}
+
+}  // namespace wmx

@@ -38,5 +38,6 @@ int launch_bwd_dkv(const wmx_attn_args& a, hipStream_t stream);
 int64_t decode_workspace_size(const wmx_decode_args& a);
 int decode_num_splits(const wmx_decode_args& a);
 int launch_decode(const wmx_decode_args& a, hipStream_t stream);
+int launch_kv_store(const wmx_kv_store_args& a, hipStream_t stream);
 
 }  // namespace wmx

@@ -14,7 +14,8 @@ benchmarks/_flop_counter.py:33-34). Per-kernel averages come from HIP events
 on the launch stream; the dominant kernel gives the roofline object.
 Secondary fields: C4 KV-pool decode GB/s, C4 prefill forward TFLOP/s, C3 cyclic fwd+bwd
 TFLOP/s (stride 4; strides 2 and 8 and the dummy-slot variant in `cyclic_variants`),
-and the fused KV-pool store GB/s beside the reference's eager steps.
+the fused KV-pool store GB/s beside the reference's eager steps, and the
+packed-document schedule builder's latency beside the torch sequence.
 The CPU baseline times the oracle (float32, dense mask) on a bounded sample.
 """
 
@@ -285,7 +286,7 @@ def main(argv=None) -> int:
     parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
     parser.add_argument(
         "--only",
-        choices=("decode", "prefill", "cyclic", "kv_store"),
+        choices=("decode", "prefill", "cyclic", "kv_store", "metadata"),
         help="print one secondary line as JSON and exit (for profiling that path alone)",
     )
     parser.add_argument(
@@ -314,7 +315,13 @@ def main(argv=None) -> int:
 
     device = torch.device("cuda:0")
     if args.only:
-        lines = {"decode": decode_line, "prefill": prefill_line, "cyclic": cyclic_line, "kv_store": kv_store_line}
+        lines = {
+            "decode": decode_line,
+            "prefill": prefill_line,
+            "cyclic": cyclic_line,
+            "kv_store": kv_store_line,
+            "metadata": metadata_line,
+        }
         print(json.dumps({args.only: lines[args.only](device)}), flush=True)
         return 0
     if args.copy_calibration:
@@ -411,6 +418,7 @@ def main(argv=None) -> int:
         line["cyclic"] = cyclic_line(device)
         line["cyclic_variants"] = [cyclic_line(device, 2), cyclic_line(device, 8), cyclic_line(device, 4, dummy=True)]
         line["kv_store"] = kv_store_line(device)
+        line["metadata"] = metadata_line(device)
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(q, k, v, metadata, args.cpu_budget)
@@ -512,6 +520,39 @@ def prefill_line(device, seed=1, batch=32, heads=16, dim=128, chunk=256):
         "tflops": round(tflops, 2),
         "frac_mfma": round(tflops / PEAK_BF16_TFLOPS, 4),
         "pairs": pairs,
+    }
+
+
+def metadata_line(device, batch=8, length=2048, reps=20):
+    """Packed-document schedule for the C2 documents (8 rows of 2048 slots,
+    geometric lengths): prepare_strict_causal_metadata as a caller sees it
+    (returns with the host segment list), through the HIP builder, through the
+    reference's torch sequence on the same GPU, and that sequence on the host
+    CPU (the reference's CPU path)."""
+    from white_matter_amd import prepare_strict_causal_metadata
+    from white_matter_amd.strict_causal_attention import _torch_schedule
+
+    docs = geometric_documents(batch, length, 0)
+    on_gpu = docs.to(device)
+
+    def wall(fn, n):
+        fn()
+        torch.cuda.synchronize()
+        t0 = time.perf_counter()
+        for _ in range(n):
+            fn()
+        torch.cuda.synchronize()
+        return (time.perf_counter() - t0) * 1e3 / n
+
+    hip_ms = wall(lambda: prepare_strict_causal_metadata(on_gpu, length), reps)
+    torch_ms = wall(lambda: _torch_schedule(on_gpu, length, 0, None, False), reps)
+    cpu_ms = wall(lambda: _torch_schedule(docs, length, 0, None, False), 5)
+    return {
+        "workload": f"prepare_strict_causal_metadata, C2 documents B={batch} T={length}, host segment list included",
+        "hip_ms": round(hip_ms, 4),
+        "torch_on_gpu_ms": round(torch_ms, 4),
+        "torch_on_cpu_ms": round(cpu_ms, 4),
+        "cpu_threads": torch.get_num_threads(),
     }
 
 

@@ -225,11 +225,51 @@ typedef struct wmx_kv_store_args {
   float eps;
 } wmx_kv_store_args;
 
+/*
+ * Packed-document schedule builder on the device: the reference's
+ * prepare_strict_causal_metadata (ops/strict_causal_attention.py:75-155),
+ * whose torch sequence synchronises with the host at every data-dependent
+ * size (the position check, three nonzero, repeat_interleave). Here two
+ * kernels (one workgroup per batch row) share one workspace:
+ *   wmx_strict_meta_count  per-slot ranks, run-start ranks and the rank -> slot
+ *                          map, the row's valid queries compacted, and
+ *                          counts[b] = {valid queries, segments, keys,
+ *                          1 if a query position lies outside [0, extent)};
+ *   wmx_strict_meta_fill   (after the caller has read counts, checked the flag
+ *                          and allocated the outputs) query_indices,
+ *                          key_indices, cu_queries and cu_keys, rows in order.
+ * Outputs are bit-identical to the reference's: query i of row b is
+ * b * query_length + i; key index b * (extent + use_dummy) + slot (+1 past
+ * the dummy, which is slot 0 and every segment's first key).
+ */
+enum { WMX_DTYPE_I32 = 2, WMX_DTYPE_I64 = 3 };
+
+typedef struct wmx_strict_meta_args {
+  const void* document_ids;   /* (B, extent) of doc_dtype, rows doc_stride elements apart */
+  const int64_t* query_start; /* (B) first query slot per row, or NULL: query_start_scalar */
+  const int64_t* kv_lengths;  /* (B) or NULL */
+  void* workspace;            /* wmx_strict_meta_workspace_size bytes, 16-byte aligned */
+  int64_t* counts;            /* (B, 4), written by count, read by fill */
+  int64_t* query_indices;     /* fill: sum of counts[:, 0] */
+  int64_t* key_indices;       /* fill: sum of counts[:, 2] */
+  int32_t* cu_queries;        /* fill: sum of counts[:, 1] + 1 */
+  int32_t* cu_keys;           /* fill: sum of counts[:, 1] + 1 */
+  int64_t doc_stride;
+  int64_t query_start_scalar;
+  int64_t workspace_bytes;
+  int32_t doc_dtype;          /* WMX_DTYPE_I32 or WMX_DTYPE_I64 */
+  int32_t batch;
+  int32_t extent;
+  int32_t query_length;
+  int32_t use_dummy;          /* 0 or 1 */
+} wmx_strict_meta_args;
+
 /* Library identity and struct layout checks for FFI bindings. */
 int wmx_abi_version(void);
 size_t wmx_attn_args_size(void);
 size_t wmx_decode_args_size(void);
 size_t wmx_kv_store_args_size(void);
+size_t wmx_strict_meta_args_size(void);
 const char* wmx_last_error(void);
 
 /* Forward: o and lse. (see replaced interfaces above) */
@@ -275,6 +315,13 @@ int wmx_decode(const wmx_decode_args* args, void* stream);
  * rms_norm, weight, RoPE, casts and index_copy_ (modules/kv_pool.py:163-172,
  * 216; blocks/_execution/cyclic.py:448-458). */
 int wmx_kv_pool_store(const wmx_kv_store_args* args, void* stream);
+
+/* Packed-document schedule (see wmx_strict_meta_args): replaces the torch
+ * sequence of prepare_strict_causal_metadata (reference
+ * ops/strict_causal_attention.py:75-155). */
+int64_t wmx_strict_meta_workspace_size(const wmx_strict_meta_args* args);
+int wmx_strict_meta_count(const wmx_strict_meta_args* args, void* stream);
+int wmx_strict_meta_fill(const wmx_strict_meta_args* args, void* stream);
 
 #ifdef __cplusplus
 }

@@ -147,6 +147,33 @@ class KvStoreArgs(ctypes.Structure):
     ]
 
 
+DTYPE_I32, DTYPE_I64 = 2, 3
+
+
+class StrictMetaArgs(ctypes.Structure):
+    """Mirror of wmx_strict_meta_args."""
+
+    _fields_ = [
+        ("document_ids", _vp),
+        ("query_start", _vp),
+        ("kv_lengths", _vp),
+        ("workspace", _vp),
+        ("counts", _vp),
+        ("query_indices", _vp),
+        ("key_indices", _vp),
+        ("cu_queries", _vp),
+        ("cu_keys", _vp),
+        ("doc_stride", ctypes.c_int64),
+        ("query_start_scalar", ctypes.c_int64),
+        ("workspace_bytes", ctypes.c_int64),
+        ("doc_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("extent", ctypes.c_int32),
+        ("query_length", ctypes.c_int32),
+        ("use_dummy", ctypes.c_int32),
+    ]
+
+
 EXPORTS = (
     "wmx_abi_version",
     "wmx_attn_args_size",
@@ -164,6 +191,10 @@ EXPORTS = (
     "wmx_decode",
     "wmx_kv_store_args_size",
     "wmx_kv_pool_store",
+    "wmx_strict_meta_args_size",
+    "wmx_strict_meta_workspace_size",
+    "wmx_strict_meta_count",
+    "wmx_strict_meta_fill",
 )
 
 
@@ -198,6 +229,12 @@ def load() -> ctypes.CDLL:
     lib.wmx_kv_store_args_size.restype = ctypes.c_size_t
     lib.wmx_kv_pool_store.argtypes = [ctypes.POINTER(KvStoreArgs), _vp]
     lib.wmx_kv_pool_store.restype = ctypes.c_int
+    lib.wmx_strict_meta_args_size.restype = ctypes.c_size_t
+    lib.wmx_strict_meta_workspace_size.argtypes = [ctypes.POINTER(StrictMetaArgs)]
+    lib.wmx_strict_meta_workspace_size.restype = ctypes.c_int64
+    for name in ("wmx_strict_meta_count", "wmx_strict_meta_fill"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(StrictMetaArgs), _vp]
+        getattr(lib, name).restype = ctypes.c_int
     if lib.wmx_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI {lib.wmx_abi_version()}, expected {ABI_VERSION}")
     if lib.wmx_attn_args_size() != ctypes.sizeof(AttnArgs):
@@ -206,6 +243,8 @@ def load() -> ctypes.CDLL:
         raise RuntimeError("wmx_decode_args layout differs between the library and the binding")
     if lib.wmx_kv_store_args_size() != ctypes.sizeof(KvStoreArgs):
         raise RuntimeError("wmx_kv_store_args layout differs between the library and the binding")
+    if lib.wmx_strict_meta_args_size() != ctypes.sizeof(StrictMetaArgs):
+        raise RuntimeError("wmx_strict_meta_args layout differs between the library and the binding")
     return lib
 
 
@@ -272,3 +311,17 @@ def decode(args: DecodeArgs, device: torch.device) -> None:
 def kv_pool_store(args: KvStoreArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_kv_pool_store(ctypes.byref(args), _stream(device)), "wmx_kv_pool_store")
+
+
+def strict_meta_workspace_size(args: StrictMetaArgs) -> int:
+    return int(load().wmx_strict_meta_workspace_size(ctypes.byref(args)))
+
+
+def strict_meta_count(args: StrictMetaArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_strict_meta_count(ctypes.byref(args), _stream(device)), "wmx_strict_meta_count")
+
+
+def strict_meta_fill(args: StrictMetaArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_strict_meta_fill(ctypes.byref(args), _stream(device)), "wmx_strict_meta_fill")

@@ -91,6 +91,23 @@ int launched(int rc) {
   return WMX_OK;
 }
 
+int check_strict_meta(const wmx_strict_meta_args* a, bool fill) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->batch < 0 || a->extent < 0 || a->query_length < 0) return fail(WMX_E_INVALID, "negative shape");
+  if (a->use_dummy != 0 && a->use_dummy != 1) return fail(WMX_E_INVALID, "use_dummy must be 0 or 1");
+  if (a->doc_dtype != WMX_DTYPE_I32 && a->doc_dtype != WMX_DTYPE_I64)
+    return fail(WMX_E_INVALID, "document_ids must be WMX_DTYPE_I32 or WMX_DTYPE_I64");
+  if (a->batch == 0) return WMX_OK;
+  if ((a->extent > 0 && !a->document_ids) || !a->counts) return fail(WMX_E_INVALID, "document_ids/counts pointer is NULL");
+  if (a->doc_stride < a->extent) return fail(WMX_E_INVALID, "doc_stride is smaller than extent");
+  const int64_t need = wmx::strict_meta_workspace_size(*a);
+  if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+    return fail(WMX_E_WORKSPACE, "schedule builder needs %lld workspace bytes", (long long)need);
+  if (fill && (!a->query_indices || !a->key_indices || !a->cu_queries || !a->cu_keys))
+    return fail(WMX_E_INVALID, "fill needs query_indices, key_indices, cu_queries and cu_keys");
+  return WMX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -171,6 +188,23 @@ int wmx_kv_pool_store(const wmx_kv_store_args* a, void* stream) {
 }
 
 size_t wmx_kv_store_args_size(void) { return sizeof(wmx_kv_store_args); }
+
+size_t wmx_strict_meta_args_size(void) { return sizeof(wmx_strict_meta_args); }
+
+
+int64_t wmx_strict_meta_workspace_size(const wmx_strict_meta_args* a) {
+  return a ? wmx::strict_meta_workspace_size(*a) : 0;
+}
+
+int wmx_strict_meta_count(const wmx_strict_meta_args* a, void* stream) {
+  if (const int rc = check_strict_meta(a, false)) return rc;
+  return launched(wmx::launch_strict_meta(*a, false, (hipStream_t)stream));
+}
+
+int wmx_strict_meta_fill(const wmx_strict_meta_args* a, void* stream) {
+  if (const int rc = check_strict_meta(a, true)) return rc;
+  return launched(wmx::launch_strict_meta(*a, true, (hipStream_t)stream));
+}
 
 int64_t wmx_decode_workspace_size(const wmx_decode_args* args) {
   return args ? wmx::decode_workspace_size(*args) : 0;

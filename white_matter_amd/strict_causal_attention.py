@@ -98,7 +98,25 @@ def prepare_strict_causal_metadata(
     plus the dummy. Consecutive valid queries share a segment while they stay
     in one run and each sees exactly one more key than the previous one; a
     segment's keys are the visible set of its last query, dummy first.
+
+    Integer ids on a ROCm device are scheduled by the HIP builder
+    (wmx_strict_meta_count / _fill): one host synchronisation, to size the
+    outputs. Elsewhere the same steps run as torch operations.
     """
+    if document_ids.is_cuda and not document_ids.is_floating_point() and document_ids.dtype != torch.bool:
+        return _device_schedule(document_ids, query_length, query_start, kv_lengths, use_dummy_token)
+    return _torch_schedule(document_ids, query_length, query_start, kv_lengths, use_dummy_token)
+
+
+def _torch_schedule(
+    document_ids: torch.Tensor,
+    query_length: int,
+    query_start: int | torch.Tensor,
+    kv_lengths: torch.Tensor | None,
+    use_dummy_token: bool,
+) -> StrictCausalMetadata:
+    """prepare_strict_causal_metadata as torch operations on the ids' device
+    (the reference's formulation; synchronises at each data-dependent size)."""
     batch, extent = document_ids.shape
     device = document_ids.device
     offset = int(use_dummy_token)
@@ -157,6 +175,72 @@ def prepare_strict_causal_metadata(
     key_indices = seg_row[owner] * key_extent + key_slot
     metadata = StrictCausalMetadata(
         query_indices, key_indices, cu_queries.int(), cu_keys.int(), query_length, key_extent, key_extent
+    )
+    for tensor in (metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys):
+        torch._dynamo.mark_dynamic(tensor, 0)
+    return metadata
+
+
+def _device_schedule(
+    document_ids: torch.Tensor,
+    query_length: int,
+    query_start: int | torch.Tensor,
+    kv_lengths: torch.Tensor | None,
+    use_dummy_token: bool,
+) -> StrictCausalMetadata:
+    """prepare_strict_causal_metadata through the HIP builder: a count pass,
+    one read of the per-row counts (validation and output sizes), a fill pass."""
+    from . import _native
+
+    batch, extent = document_ids.shape
+    device = document_ids.device
+    offset = int(use_dummy_token)
+    key_extent = extent + offset
+    ids = document_ids if document_ids.dtype in (torch.int32, torch.int64) else document_ids.long()
+    if ids.stride(-1) != 1 or (batch > 1 and ids.stride(0) < extent):
+        ids = ids.contiguous()
+    a = _native.StrictMetaArgs()
+    a.document_ids = ids.data_ptr()
+    a.doc_stride = ids.stride(0) if batch > 1 else extent
+    a.doc_dtype = _native.DTYPE_I32 if ids.dtype == torch.int32 else _native.DTYPE_I64
+    keep = [ids]
+    if isinstance(query_start, torch.Tensor):
+        start = torch.as_tensor(query_start, device=device, dtype=torch.long).expand(batch).contiguous()
+        keep.append(start)
+        a.query_start = start.data_ptr()
+    else:
+        a.query_start_scalar = int(query_start)
+    if kv_lengths is not None:
+        kv = kv_lengths.to(device=device, dtype=torch.long).expand(batch).contiguous()
+        keep.append(kv)
+        a.kv_lengths = kv.data_ptr()
+    a.batch, a.extent, a.query_length, a.use_dummy = batch, extent, query_length, offset
+    workspace = torch.empty(max(_native.strict_meta_workspace_size(a), 16), device=device, dtype=torch.uint8)
+    counts = torch.zeros(batch, 4, device=device, dtype=torch.long)
+    a.workspace, a.workspace_bytes, a.counts = workspace.data_ptr(), workspace.numel(), counts.data_ptr()
+    _native.strict_meta_count(a, device)
+    host = counts.cpu()  # the one synchronisation: validation and output sizes
+    if bool((host[:, 3] != 0).any()):
+        raise ValueError("document_ids must label every query position")
+    n_queries, n_segments, n_keys = (int(x) for x in host[:, :3].sum(0))
+    if max(n_queries, n_keys) >= 2**31:
+        raise ValueError("the schedule holds 2**31 or more queries or keys (cu_queries/cu_keys are int32)")
+    if n_queries == 0:
+        empty = torch.empty(0, device=device, dtype=torch.long)
+        cu = torch.zeros(1, device=device, dtype=torch.int32)
+        return StrictCausalMetadata(empty, empty, cu, cu, query_length, key_extent, key_extent)
+    query_indices = torch.empty(n_queries, device=device, dtype=torch.long)
+    key_indices = torch.empty(n_keys, device=device, dtype=torch.long)
+    cu_queries = torch.empty(n_segments + 1, device=device, dtype=torch.int32)
+    cu_keys = torch.empty(n_segments + 1, device=device, dtype=torch.int32)
+    a.query_indices, a.key_indices = query_indices.data_ptr(), key_indices.data_ptr()
+    a.cu_queries, a.cu_keys = cu_queries.data_ptr(), cu_keys.data_ptr()
+    _native.strict_meta_fill(a, device)
+    del keep, workspace, counts  # the stream orders the fill before any reuse of this memory
+    cq, ck = torch.stack((cu_queries, cu_keys)).tolist()  # one copy for the host segment list
+    segments = tuple((cq[s], cq[s + 1], ck[s], ck[s + 1]) for s in range(n_segments))
+    metadata = StrictCausalMetadata(
+        query_indices, key_indices, cu_queries, cu_keys, query_length, key_extent, key_extent, segments
     )
     for tensor in (metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys):
         torch._dynamo.mark_dynamic(tensor, 0)

@@ -15,7 +15,8 @@ on the launch stream; the dominant kernel gives the roofline object.
 Secondary fields: C4 KV-pool decode GB/s, C4 prefill forward TFLOP/s, C3 cyclic fwd+bwd
 TFLOP/s (stride 4; strides 2 and 8 and the dummy-slot variant in `cyclic_variants`),
 the fused KV-pool store GB/s beside the reference's eager steps, and the
-packed-document schedule builder's latency beside the torch sequence.
+packed-document schedule builder's latency beside the torch sequence, and
+the captured decode loop's per-token time beside eager launches.
 The CPU baseline times the oracle (float32, dense mask) on a bounded sample.
 """
 
@@ -286,7 +287,7 @@ def main(argv=None) -> int:
     parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
     parser.add_argument(
         "--only",
-        choices=("decode", "prefill", "cyclic", "kv_store", "metadata"),
+        choices=("decode", "prefill", "cyclic", "kv_store", "metadata", "decode_loop"),
         help="print one secondary line as JSON and exit (for profiling that path alone)",
     )
     parser.add_argument(
@@ -321,6 +322,7 @@ def main(argv=None) -> int:
             "cyclic": cyclic_line,
             "kv_store": kv_store_line,
             "metadata": metadata_line,
+            "decode_loop": decode_loop_line,
         }
         print(json.dumps({args.only: lines[args.only](device)}), flush=True)
         return 0
@@ -419,6 +421,7 @@ def main(argv=None) -> int:
         line["cyclic_variants"] = [cyclic_line(device, 2), cyclic_line(device, 8), cyclic_line(device, 4, dummy=True)]
         line["kv_store"] = kv_store_line(device)
         line["metadata"] = metadata_line(device)
+        line["decode_loop"] = decode_loop_line(device)
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(q, k, v, metadata, args.cpu_budget)
@@ -520,6 +523,55 @@ def prefill_line(device, seed=1, batch=32, heads=16, dim=128, chunk=256):
         "tflops": round(tflops, 2),
         "frac_mfma": round(tflops / PEAK_BF16_TFLOPS, 4),
         "pairs": pairs,
+    }
+
+
+def decode_loop_line(device, batch=8, heads=16, kv_heads=8, channels=8, dim=64, layers=24, prefix=1024, tokens=128):
+    """Cached decoding at the 24-layer model's shape: per token, 24 layers each
+    attend from (B, 16, 1, 64) queries to one of 8 pool channels (B, 8, N, 64),
+    then the token's keys/values are K-normed, rotated and stored, and the
+    slot counter advances. 128 tokens after a 1024-token prefix, replayed from
+    one DecodeLoop graph, beside the same launches issued eagerly. Bytes per
+    token: every layer's K and V reads of its channel up to the current
+    length, the queries, outputs and the store."""
+    from white_matter_amd import DecodeLoop
+
+    gen = torch.Generator().manual_seed(9)
+    capacity = prefix + 1 + tokens
+    folded = channels * kv_heads
+    keys = torch.empty(batch, folded, capacity, dim, device=device, dtype=torch.bfloat16).normal_(0, 1)
+    values = torch.empty_like(keys).normal_(0, 1)
+    length = torch.tensor([prefix + 1], device=device)
+    weight = torch.ones(channels, dim, device=device)
+    angle = torch.arange(capacity, device=device)[:, None].float() * torch.logspace(0, -4, dim // 2, device=device)[None]
+    angle = torch.cat((angle, angle), -1)
+    loop = DecodeLoop(keys, values, length, [layer % channels for layer in range(layers)], weight, angle.cos(), angle.sin(),
+                      query_heads=heads)
+    loop.query.copy_(torch.randn(loop.query.shape, generator=gen).to(device, torch.bfloat16))
+    loop.new_key.copy_(torch.randn(loop.new_key.shape, generator=gen).to(device, torch.bfloat16))
+    loop.new_value.copy_(torch.randn(loop.new_value.shape, generator=gen).to(device, torch.bfloat16))
+    start = length.clone()
+
+    def run(fn):
+        length.copy_(start)
+        loop.seen = prefix + 1
+        torch.cuda.synchronize()
+        return Timer()(fn, tokens)
+
+    with torch.inference_mode():
+        graph_ms = run(loop)
+        eager_ms = run(loop.step)
+    lengths = sum(prefix + t for t in range(tokens)) / tokens  # keys seen per token (dummy included)
+    per_token = layers * (2 * batch * kv_heads * lengths * dim * 2 + 2 * batch * heads * dim * 2)
+    per_token += 4 * batch * folded * dim * 2
+    return {
+        "workload": f"decode loop: {layers} layers, Q ({batch},{heads},1,{dim}) over {channels} pool channels "
+        f"({batch},{kv_heads},N,{dim}), {tokens} tokens after a {prefix}-token prefix, store included",
+        "graph_ms_per_token": round(graph_ms, 4),
+        "eager_ms_per_token": round(eager_ms, 4),
+        "gbps": round(per_token / (graph_ms * 1e-3) / 1e9, 1),
+        "frac_hbm": round(per_token / (graph_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+        "bytes_per_token": int(per_token),
     }
 
 

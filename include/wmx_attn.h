@@ -65,9 +65,12 @@ enum {
  * Varlen mode (query_indices != NULL): segment s holds queries
  * query_indices[cu_queries[s] : cu_queries[s+1]] (flat b * query_extent + t)
  * and keys key_indices[cu_keys[s] : cu_keys[s+1]] (flat b * key_extent + slot);
- * local key j is visible to local query i iff j <= (nk - nq) + i
- * (bottom-right causal). Output rows not named by any segment are left
- * untouched, so callers zero-fill o/dq/dk/dv first.
+ * local key j is visible to local query i iff
+ * j <= (nk - 1) - query_stride * (nq - 1 - i): the segment's last query sees
+ * all its keys, each earlier query query_stride fewer (bottom-right causal at
+ * query_stride 1; strided cyclic queries of one document above 1; query_offset
+ * is unused). Output rows not named by any segment are left untouched, so
+ * callers zero-fill o/dq/dk/dv first.
  */
 typedef struct wmx_attn_args {
   const void* q;

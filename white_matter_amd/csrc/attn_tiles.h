@@ -104,7 +104,9 @@ struct Problem {
       if (nk > 0)
         krows.init(a.key_indices + ks, nk, a.key_extent, a.segment_layout & kKeysConsecutive,
                    a.segment_layout & kKeysOneRow, true);
-      bound = Bounds{nk - nq, INT_MAX, 1, nk};
+      // query i sees keys 0 .. nk - 1 - stride * (nq - 1 - i): the last query
+      // sees every key of the segment (bottom-right causal at stride 1)
+      bound = Bounds{(int64_t)nk - 1 - (int64_t)a.query_stride * (nq - 1), INT_MAX, a.query_stride, nk};
     } else {
       nq = a.q_len;
       nk = a.kv_len;

@@ -459,32 +459,35 @@ _TILE = 128  # rows of the kernels' query and key tiles
 _STEP = 64  # rows of the tiles their loops step over
 
 
-def _work_units(metadata: StrictCausalMetadata) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
-    """The kernels' work lists and dS layout, cached on the metadata object:
-    the (segment, tile) units of the query-tiled kernels (forward, dQ: 128
-    rows) and of the key-tiled kernel (dK/dV: 128 keys), heaviest first, as
-    int32 (n, 2) device tensors, and the int64 (num_segments + 1) offsets of
-    the segments' dS blocks (keys x queries rounded up to 128 elements each)
-    with their total. A unit's cost is the number of 64-row tiles its loop
-    visits (then its row count): segments are bottom-right causal, so query i
-    of a segment with nq queries and nk keys sees keys 0 .. nk - nq + i; a
-    query tile visits the key tiles up to its last row's bound, a key tile
-    the query tiles from the one holding the first row that sees its first
-    key."""
-    units = metadata.__dict__.get("_units")
+def _work_units(
+    metadata: StrictCausalMetadata, stride: int = 1
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
+    """The kernels' work lists and dS layout, cached on the metadata object per
+    query stride: the (segment, tile) units of the query-tiled kernels
+    (forward, dQ: 128 rows) and of the key-tiled kernel (dK/dV: 128 keys),
+    heaviest first, as int32 (n, 2) device tensors, and the int64
+    (num_segments + 1) offsets of the segments' dS blocks (keys x queries
+    rounded up to 128 elements each) with their total. A unit's cost is the
+    number of 64-row tiles its loop visits (then its row count): query i of a
+    segment with nq queries and nk keys sees keys 0 .. nk - 1 - stride *
+    (nq - 1 - i) (bottom-right causal at stride 1); a query tile visits the
+    key tiles up to its last row's bound, a key tile the query tiles from the
+    one holding the first row that sees its first key."""
+    by_stride = metadata.__dict__.setdefault("_units", {})
+    units = by_stride.get(stride)
     if units is None:
         q_units, k_units, ds_blocks = [], [], []
         for s, (qs, qe, ks, ke) in enumerate(metadata.segments):
             nq, nk = qe - qs, ke - ks
-            off = nk - nq
+            off = nk - 1 - stride * (nq - 1)  # bound of local query 0
             ds_blocks.append(nk * (-(-nq // _TILE) * _TILE))
             for t in range(0, -(-nq // _TILE)):
                 rows = min(nq, (t + 1) * _TILE) - t * _TILE
-                reach = min(nk, max(0, off + t * _TILE + rows))
+                reach = min(nk, max(0, off + stride * (t * _TILE + rows - 1) + 1))
                 q_units.append(((-(-reach // _STEP), rows), s, t))
             for t in range(0, -(-nk // _TILE)):
                 keys = min(nk, (t + 1) * _TILE) - t * _TILE
-                first = max(0, t * _TILE - off)
+                first = max(0, -(-(t * _TILE - off) // stride))
                 steps = -(-(nq - first // _STEP * _STEP) // _STEP) if first < nq else 0
                 k_units.append(((steps, keys), s, t))
         device = metadata.query_indices.device
@@ -495,7 +498,7 @@ def _work_units(metadata: StrictCausalMetadata) -> tuple[torch.Tensor, torch.Ten
             return torch.tensor(flat, dtype=torch.int32).view(-1, 2).to(device)
 
         offsets = torch.tensor([0] + ds_blocks, dtype=torch.int64).cumsum(0)
-        units = metadata.__dict__["_units"] = (table(q_units), table(k_units), offsets.to(device), int(offsets[-1]))
+        units = by_stride[stride] = (table(q_units), table(k_units), offsets.to(device), int(offsets[-1]))
     return units
 
 

@@ -223,7 +223,7 @@ typedef struct wmx_kv_store_args {
   int32_t channels;
   int32_t heads;
   int32_t tokens;
-  int32_t head_dim;          /* 64 or 128 */
+  int32_t head_dim;          /* 64, 96 or 128 */
   int32_t pool_slots;        /* N */
   float eps;
 } wmx_kv_store_args;

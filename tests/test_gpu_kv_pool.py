@@ -35,7 +35,7 @@ def _ulp_close(actual, expected):
     assert (actual == expected).double().mean() >= 0.99
 
 
-@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dim", [64, 96, 128])
 @pytest.mark.parametrize(
     "dtypes",
     [

@@ -35,7 +35,7 @@ def _inputs(dtype, dim=64, seed=0, shape=(2, 3, 2, 5)):
 
 
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
-@pytest.mark.parametrize("dim", [64, 128])
+@pytest.mark.parametrize("dim", [64, 96, 128])
 def test_oracle_matches_pytorch_steps(dtype, dim):
     key, weight, cos, sin = _inputs(dtype, dim)
     expected = _torch_steps(key, weight, cos, sin, 1e-6).double()

@@ -167,8 +167,8 @@ int wmx_attn_bwd_dkv(const wmx_attn_args* args, void* stream) {
 
 int wmx_kv_pool_store(const wmx_kv_store_args* a, void* stream) {
   if (!a) return fail(WMX_E_INVALID, "args is NULL");
-  if (a->head_dim != 64 && a->head_dim != 128)
-    return fail(WMX_E_UNSUPPORTED, "kv store head_dim %d is not 64 or 128", a->head_dim);
+  if (a->head_dim != 64 && a->head_dim != 96 && a->head_dim != 128)
+    return fail(WMX_E_UNSUPPORTED, "kv store head_dim %d is not 64, 96 or 128", a->head_dim);
   if (a->batch < 0 || a->channels < 0 || a->heads < 0 || a->tokens < 0 || a->pool_slots < 0)
     return fail(WMX_E_INVALID, "negative shape");
   for (int dt : {a->key_dtype, a->value_dtype, a->weight_dtype, a->rope_dtype})

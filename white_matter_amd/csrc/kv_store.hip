@@ -61,8 +61,9 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
   // Every product and sum is rounded on its own, as the eager sequence does:
   // a fused multiply-add would skip the rounding of y * cos.
 #pragma clang fp contract(off)
-  constexpr int L = D / 8;  // lanes per row
-  constexpr int U = 4;      // heads in flight per thread
+  constexpr int LD = D / 8;                    // lanes holding data
+  constexpr int L = LD <= 8 ? 8 : 16;          // lanes per row (a power of two; D = 96 leaves 4 idle)
+  constexpr int U = 4;                         // heads in flight per thread
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   const int64_t r = gid / L;
   const int l = (int)(gid % L);  // this lane's elements: 8 l .. 8 l + 7
@@ -76,11 +77,14 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
   const int64_t slot = a.slots[t];
   if (slot < 0 || slot >= a.pool_slots) return;  // out-of-range slots are not written
   const int d0 = 8 * l;
+  // idle lanes (D = 96) take part in the shuffles with zeros and store nothing
+  const bool data = l < LD;
+  const int dl = data ? d0 : 0;
   auto rnd = [](float x) { return KEY_BF16 ? round_bf16(x) : x; };
 
   float w[8], cs[8], sn[8];
-  load8(a.k_norm_weight, (int64_t)c * D + d0, a.weight_dtype == WMX_DTYPE_BF16, w);
-  const int64_t ro = (int64_t)b * a.rope_stride[0] + (int64_t)t * a.rope_stride[1] + d0;
+  load8(a.k_norm_weight, (int64_t)c * D + dl, a.weight_dtype == WMX_DTYPE_BF16, w);
+  const int64_t ro = (int64_t)b * a.rope_stride[0] + (int64_t)t * a.rope_stride[1] + dl;
   load8(a.cos, ro, a.rope_dtype == WMX_DTYPE_BF16, cs);
   load8(a.sin, ro, a.rope_dtype == WMX_DTYPE_BF16, sn);
 #pragma unroll
@@ -89,14 +93,16 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
     cs[e] = rnd(cs[e]);
     sn[e] = rnd(sn[e]);
   }
-  const bool low = d0 < D / 2;  // rotate_half: element d pairs with d +- D/2, held by lane l ^ (L / 2)
-  const int64_t key_row = (int64_t)b * a.key_stride[0] + (int64_t)c * a.key_stride[1] + (int64_t)t * a.key_stride[3] + d0;
+  // rotate_half: element d pairs with d +- D/2, held by the lane LD/2 away
+  const bool low = d0 < D / 2;
+  const int partner = (int)(gid & 63) + (low ? LD / 2 : -(LD / 2));  // lane in the wave
+  const int64_t key_row = (int64_t)b * a.key_stride[0] + (int64_t)c * a.key_stride[1] + (int64_t)t * a.key_stride[3] + dl;
   const int64_t kpool_row =
-      (int64_t)b * a.key_pool_stride[0] + (int64_t)c * a.key_pool_stride[1] + slot * a.key_pool_stride[3] + d0;
+      (int64_t)b * a.key_pool_stride[0] + (int64_t)c * a.key_pool_stride[1] + slot * a.key_pool_stride[3] + dl;
   const int64_t value_row =
-      (int64_t)b * a.value_stride[0] + (int64_t)c * a.value_stride[1] + (int64_t)t * a.value_stride[3] + d0;
+      (int64_t)b * a.value_stride[0] + (int64_t)c * a.value_stride[1] + (int64_t)t * a.value_stride[3] + dl;
   const int64_t vpool_row =
-      (int64_t)b * a.value_pool_stride[0] + (int64_t)c * a.value_pool_stride[1] + slot * a.value_pool_stride[3] + d0;
+      (int64_t)b * a.value_pool_stride[0] + (int64_t)c * a.value_pool_stride[1] + slot * a.value_pool_stride[3] + dl;
 
   for (int h0 = 0; h0 < a.heads; h0 += U) {
     float x[U][8], v[U][8];
@@ -115,6 +121,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
       float ss = 0.f;
 #pragma unroll
       for (int e = 0; e < 8; ++e) ss = fmaf(x[u][e], x[u][e], ss);
+      if (!data) ss = 0.f;
 #pragma unroll
       for (int o = L / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
       const float inv = 1.f / sqrtf(ss / (float)D + a.eps);
@@ -123,11 +130,11 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
       for (int e = 0; e < 8; ++e) y[e] = rnd(rnd(x[u][e] * inv) * w[e]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float other = __shfl_xor(y[e], L / 2);
+        const float other = __shfl(y[e], data ? partner : 0);
         const float rot = low ? -other : other;
         out[e] = rnd(rnd(y[e] * cs[e]) + rnd(rot * sn[e]));
       }
-      if (h0 + u < a.heads) {
+      if (data && h0 + u < a.heads) {
         store8_bf16(a.key_pool, kpool_row + hu[u] * a.key_pool_stride[2], out);
         if constexpr (VALUE != kNoValue) store8_bf16(a.value_pool, vpool_row + hu[u] * a.value_pool_stride[2], v[u]);
       }
@@ -148,12 +155,15 @@ void launch_kv_store_d(const wmx_kv_store_args& a, int64_t rows, dim3 grid, hipS
 int launch_kv_store(const wmx_kv_store_args& a, hipStream_t stream) {
   const int64_t rows = (int64_t)a.batch * a.channels * a.tokens;  // each thread walks the heads
   if (rows == 0 || a.heads == 0) return WMX_OK;
-  const int64_t threads = rows * (a.head_dim / 8);
+  const int64_t threads = rows * (a.head_dim <= 64 ? 8 : 16);  // lanes per row, as in the kernel
   const dim3 grid((unsigned)((threads + 255) / 256));
   const bool kb = a.key_dtype == WMX_DTYPE_BF16;
   if (a.head_dim == 64) {
     if (kb) launch_kv_store_d<64, true>(a, rows, grid, stream);
     else launch_kv_store_d<64, false>(a, rows, grid, stream);
+  } else if (a.head_dim == 96) {
+    if (kb) launch_kv_store_d<96, true>(a, rows, grid, stream);
+    else launch_kv_store_d<96, false>(a, rows, grid, stream);
   } else if (a.head_dim == 128) {
     if (kb) launch_kv_store_d<128, true>(a, rows, grid, stream);
     else launch_kv_store_d<128, false>(a, rows, grid, stream);

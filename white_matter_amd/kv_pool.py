@@ -52,15 +52,15 @@ def write_pool(
     key/value (B, C, H, T, D) float32 or bfloat16 (the KV pool's projected
     channels), k_norm_weight (C, D), cos/sin (B, T, D) (the group's position
     embeddings), keys/values bf16 pool tensors or views (B, C, H, N, D),
-    slots (T,) int64 distinct pool slots. head_dim 64 or 128.
+    slots (T,) int64 distinct pool slots. head_dim 64, 96 or 128.
     """
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (key, value, k_norm_weight, cos, sin)):
         raise RuntimeError("write_pool is forward-only; use the reference's eager sequence under autograd")
     if key.ndim != 5 or (value is not None and value.shape != key.shape):
         raise ValueError("key and value must be (B, C, H, T, D) of one shape")
     batch, channels, heads, tokens, dim = key.shape
-    if dim not in (64, 128):
-        raise ValueError(f"head_dim {dim} is not supported (64 or 128)")
+    if dim not in (64, 96, 128):
+        raise ValueError(f"head_dim {dim} is not supported (64, 96 or 128)")
     if k_norm_weight.shape != (channels, dim):
         raise ValueError("k_norm_weight must be (C, D)")
     if cos.shape != (batch, tokens, dim) or sin.shape != cos.shape or sin.dtype != cos.dtype:

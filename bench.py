@@ -116,9 +116,10 @@ def kernel_times(q, k, v, metadata, reps):
     alone through the C ABI between HIP events on the current stream, in the
     backward's order (dK/dV stores the dS that dQ reads)."""
     from white_matter_amd import _kernels, _native
-    from white_matter_amd.strict_causal_attention import _schedule_flags, _work_units
+    from white_matter_amd.strict_causal_attention import _covering_schedule, _schedule_flags, _work_units
 
     batch, heads, length, dim = q.shape
+    metadata = _covering_schedule(metadata, batch, length, k.shape[2])  # the schedule the operator runs
     max_q, max_k, flags = _schedule_flags(metadata)
     varlen = _kernels.Varlen(
         metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,

@@ -318,3 +318,23 @@ def test_dense_work_list_orders_tiles_by_steps():
 
         costs = [steps(b, t) for b, t in units.tolist()]
         assert costs == sorted(costs, reverse=True)
+
+
+@pytest.mark.parametrize("dummy", [False, True])
+def test_covering_schedule_adds_rows_not_pairs(dummy):
+    """The schedule the kernels run covers every query and key row (idle query
+    runs as segments without keys, idle key runs as segments without queries)
+    and implies exactly the user schedule's visible pairs."""
+    from white_matter_amd.strict_causal_attention import _covering_schedule
+
+    docs = torch.tensor([[0, 0, 0, 1, 1, -1, 2, 2, 2, 2], [5, 5, 6, 6, 6, 6, 6, 7, -1, -1]])
+    length, extent = 10, 10 + int(dummy)
+    schedule = prepare_strict_causal_metadata(docs, length, use_dummy_token=dummy)
+    cover = _covering_schedule(schedule, 2, length, extent)
+    as_dict = lambda m: {k: _np(getattr(m, k)) for k in ("query_indices", "key_indices", "cu_queries", "cu_keys")} | {  # noqa: E731
+        "key_extent": extent
+    }
+    assert torch.equal(ref.schedule_keep(as_dict(cover), 2, length, extent), ref.schedule_keep(as_dict(schedule), 2, length, extent))
+    assert sorted(_np(cover.query_indices).tolist()) == list(range(2 * length))
+    assert set(_np(cover.key_indices).tolist()) == set(range(2 * extent))
+    assert _covering_schedule(schedule, 2, length, extent) is cover  # cached per call shape

@@ -161,7 +161,7 @@ def _build_packed_schedule(qseg, kseg, qstart, kqend, q_len: int, k_len: int, st
     infinite LSE, zero dQ) and runs of keys that no query sees form segments
     without queries (zero dK/dV). Returns a StrictCausalMetadata, the string
     "empty" when no query sees a key, or None."""
-    from .strict_causal_attention import StrictCausalMetadata
+    from .strict_causal_attention import StrictCausalMetadata, _runs
 
     device = qseg.device
     qseg, kseg, qstart, kqend = (t.long() for t in (qseg, kseg, qstart, kqend))
@@ -226,19 +226,8 @@ def _build_packed_schedule(qseg, kseg, qstart, kqend, q_len: int, k_len: int, st
     edges.index_put_((seg_row[has_real], last_key[has_real] + 1), -torch.ones_like(first_key[has_real]), accumulate=True)
     covered = (edges[:, :k_len].cumsum(1) > 0) | dummy
 
-    def runs(mask: torch.Tensor, width: int) -> tuple[torch.Tensor, torch.Tensor]:
-        """Flat indices of the set entries and the lengths of their runs of
-        consecutive entries within one row."""
-        at = mask.flatten().nonzero().flatten()
-        if at.numel() == 0:
-            return at, at
-        starts = torch.ones_like(at, dtype=torch.bool)
-        starts[1:] = (at[1:] != at[:-1] + 1) | (at[1:] % width == 0)
-        first = starts.nonzero().flatten()
-        return at, torch.diff(torch.cat((first, first.new_full((1,), at.numel()))))
-
-    idle_q, idle_q_runs = runs(~valid, q_len)
-    idle_k, idle_k_runs = runs(~covered, k_len)
+    idle_q, idle_q_runs = _runs(~valid)
+    idle_k, idle_k_runs = _runs(~covered)
     nq = torch.cat((torch.diff(cu_queries), idle_q_runs, torch.zeros_like(idle_k_runs)))
     nk = torch.cat((keys, torch.zeros_like(idle_q_runs), idle_k_runs))
     cu_queries = torch.cat((nq.new_zeros(1), nq.cumsum(0)))

@@ -459,6 +459,54 @@ _TILE = 128  # rows of the kernels' query and key tiles
 _STEP = 64  # rows of the tiles their loops step over
 
 
+def _runs(mask: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """Flat indices of the set entries of a (rows, width) mask, and the lengths
+    of their runs of consecutive entries within one row."""
+    width = mask.shape[1]
+    at = mask.flatten().nonzero().flatten()
+    if at.numel() == 0:
+        return at, at
+    starts = torch.ones_like(at, dtype=torch.bool)
+    starts[1:] = (at[1:] != at[:-1] + 1) | (at[1:] % width == 0)
+    first = starts.nonzero().flatten()
+    return at, torch.diff(torch.cat((first, first.new_full((1,), at.numel()))))
+
+
+def _covering_schedule(metadata: StrictCausalMetadata, batch: int, length: int, key_extent: int) -> StrictCausalMetadata:
+    """The schedule the kernels run: `metadata` plus, for the rows it leaves
+    out, runs of queries as segments without keys (the kernels write a zero
+    output, infinite LSE and zero dQ for them) and runs of key rows as
+    segments without queries (zero dK/dV), so every output row is written by
+    a kernel and no fill is launched. Cached on the metadata per call shape."""
+    cache = metadata.__dict__.setdefault("_covering", {})
+    shape = (batch, length, key_extent)
+    cover = cache.get(shape)
+    if cover is None:
+        device = metadata.query_indices.device
+        seen_q = torch.zeros(batch * length, dtype=torch.bool, device=device)
+        seen_q[metadata.query_indices] = True
+        seen_k = torch.zeros(batch * key_extent, dtype=torch.bool, device=device)
+        seen_k[metadata.key_indices] = True
+        idle_q, q_runs = _runs(~seen_q.view(batch, length))
+        idle_k, k_runs = _runs(~seen_k.view(batch, key_extent))
+        if idle_q.numel() == 0 and idle_k.numel() == 0:
+            cover = metadata
+        else:
+            nq = torch.cat((torch.diff(metadata.cu_queries.long()), q_runs, torch.zeros_like(k_runs)))
+            nk = torch.cat((torch.diff(metadata.cu_keys.long()), torch.zeros_like(q_runs), k_runs))
+            cover = StrictCausalMetadata(
+                torch.cat((metadata.query_indices, idle_q)),
+                torch.cat((metadata.key_indices, idle_k)),
+                torch.cat((nq.new_zeros(1), nq.cumsum(0))).int(),
+                torch.cat((nk.new_zeros(1), nk.cumsum(0))).int(),
+                metadata.max_queries,
+                metadata.max_keys,
+                metadata.key_extent,
+            )
+        cache[shape] = cover
+    return cover
+
+
 def _work_units(
     metadata: StrictCausalMetadata, stride: int = 1
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
@@ -758,10 +806,12 @@ def _hip_attention(query, key, value, query_start, kv_lengths, use_dummy_token, 
         max_q, max_k, flags = _schedule_flags(metadata)
         if metadata.max_queries != length or top_q >= batch * length or top_k >= batch * key.shape[2]:
             raise ValueError("metadata was prepared for other query/key shapes")
-        gaps = _schedule_gaps(metadata, batch, length, heads, key.shape[2], key.shape[1])
+        cover = _covering_schedule(metadata, batch, length, key.shape[2])
+        max_q, max_k, flags = _schedule_flags(cover)
+        gaps = _schedule_gaps(cover, batch, length, heads, key.shape[2], key.shape[1])
         out, _ = strict_varlen_fwd(
-            q, k, v, metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
-            max_q, max_k, flags, scale, *gaps, *_work_units(metadata),
+            q, k, v, cover.query_indices, cover.key_indices, cover.cu_queries, cover.cu_keys,
+            max_q, max_k, flags, scale, *gaps, *_work_units(cover),
         )
     else:
         row_offset = row_limit = None

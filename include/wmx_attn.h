@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 3
+#define WMX_ABI_VERSION 4
 
 enum {
   WMX_OK = 0,
@@ -142,6 +142,11 @@ typedef struct wmx_attn_args {
    * NULL: varlen backward passes recompute dQ without a dS buffer. */
   const int64_t* ds_offsets;
   int64_t ds_elements;
+  /* Forward query rows per workgroup: 0 or 128 (4 waves), or 256 (8 waves:
+   * each key/value tile serves twice the rows, for few query tiles over long
+   * key ranges such as a chunk after a cached prefix). q_units tiles count in
+   * these rows. The backward kernels are unaffected. */
+  int32_t query_tile;
 } wmx_attn_args;
 
 /*

@@ -275,3 +275,32 @@ def test_kernel_matches_bf16_pipeline(count, prefix, dim, scaled):
     for name, a, e in zip(("out", "dq", "dk", "dv"), (out.transpose(1, 2), *grads), expected):
         err = ((a.double().cpu() - e).norm() / e.norm()).item()
         assert err <= 1.5e-3, f"{name}: {err:.3e}"
+
+
+@pytest.mark.parametrize("ragged", [False, True])
+def test_prefill_wide_query_tile(ragged):
+    """A chunk of 200 queries after a prefix of about 1000 keys runs 256-row
+    forward workgroups (keys >= 4x queries): against the float64 oracle, and
+    equal to the 128-row workgroups on the same inputs up to accumulation
+    order."""
+    from white_matter_amd import _kernels
+
+    gen = torch.Generator().manual_seed(31)
+    count, capacity = 200, 1300
+    prefix = torch.tensor([1000, 871]) if ragged else torch.tensor([1000, 1000])
+    q = torch.randn(2, 4, count, 64, generator=gen).to(DEV, torch.bfloat16)
+    k = torch.randn(2, 2, capacity, 64, generator=gen).to(DEV, torch.bfloat16)
+    v = torch.randn(2, 2, capacity, 64, generator=gen).to(DEV, torch.bfloat16)
+    start = prefix.to(DEV) if ragged else 1000
+    with torch.no_grad():
+        out = strict_causal_attention(q, k, v, query_start=start, kv_lengths=(prefix + count).to(DEV))
+    expected = ref.per_query_strict(q.cpu(), k.cpu(), v.cpu(), prefix, False, lengths=prefix + count)
+    assert_bf16_close(out, expected, what="wide-tile prefill")
+    # the same call through 128-row workgroups
+    o128 = torch.empty(2, count, 4, 64, device=DEV, dtype=torch.bfloat16)
+    lse = torch.empty(2, 4, count, device=DEV, dtype=torch.float32)
+    row_offset = (prefix.to(DEV) - 1).to(torch.int32) if ragged else None
+    row_limit = (prefix + count - 1).to(DEV, torch.int32)
+    vis = _kernels.Visibility(query_offset=999, row_offset=row_offset, row_limit=row_limit)
+    _kernels.forward(q, k, v, o128.transpose(1, 2), lse, 64**-0.5, vis)
+    assert_bf16_close(out.double(), o128.double(), max_abs=2e-3, rel_l2=1e-3, what="256 vs 128 rows")

@@ -90,6 +90,7 @@ class Visibility:
     documents: tuple[torch.Tensor, torch.Tensor, torch.Tensor, torch.Tensor] | None = None
     varlen: Varlen | None = None
     q_units: torch.Tensor | None = None  # int32 (n, 2) (batch row, query tile), heaviest first (dense)
+    query_tile: int = 0  # forward rows per workgroup: 0/128, or 256 (q_units then count 256-row tiles)
 
     def fill(self, args: _native.AttnArgs) -> None:
         args.query_stride = self.query_stride
@@ -102,6 +103,7 @@ class Visibility:
             args.key_mask_stride = self.key_mask.stride(0)
         if self.documents is not None:
             args.q_seg, args.k_seg, args.q_start, args.k_qend = (t.data_ptr() for t in self.documents)
+        args.query_tile = self.query_tile
         if self.q_units is not None:
             args.q_units, args.num_q_units = self.q_units.data_ptr(), self.q_units.shape[0]
         if self.varlen is not None:
@@ -131,14 +133,14 @@ KEY_STEP = 64  # key rows per step of their tile loops
 
 def dense_units(
     batch: int, q_len: int, kv_len: int, query_offset: int, row_offset: torch.Tensor | None,
-    row_limit: torch.Tensor | None, device: torch.device,
+    row_limit: torch.Tensor | None, device: torch.device, tile: int = QUERY_TILE,
 ) -> torch.Tensor:
     """Work list of a dense problem with per-row bounds: the (batch row,
-    128-row query tile) pairs ordered by the number of 64-key tiles they
+    `tile`-row query tile) pairs ordered by the number of 64-key tiles they
     visit, largest first, computed on the device (no host synchronisation).
     Query i of row b sees key slots j <= min(offset_b + i, limit_b)."""
-    tiles = -(-q_len // QUERY_TILE)
-    last = torch.clamp(torch.arange(tiles, device=device) * QUERY_TILE + QUERY_TILE - 1, max=q_len - 1)
+    tiles = -(-q_len // tile)
+    last = torch.clamp(torch.arange(tiles, device=device) * tile + tile - 1, max=q_len - 1)
     off = row_offset.to(torch.int64)[:, None] if row_offset is not None else torch.full((batch, 1), query_offset, device=device)
     bound = off + last[None, :]
     if row_limit is not None:

@@ -17,7 +17,7 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -81,6 +81,7 @@ class AttnArgs(ctypes.Structure):
         ("num_k_units", ctypes.c_int32),
         ("ds_offsets", _vp),
         ("ds_elements", ctypes.c_int64),
+        ("query_tile", ctypes.c_int32),
     ]
 
 

@@ -1,7 +1,7 @@
 // Flash-style attention forward for gfx950 (CDNA4), bf16 in, fp32 accumulate.
 //
-// One workgroup = 4 wave64s = 128 query rows of one (batch row or varlen
-// segment, query head); each wave owns 32 query rows. Key/value tiles of 64
+// One workgroup = NW wave64s (4, or 8 for query_tile 256) = 32 NW query rows
+// of one (batch row or varlen segment, query head); each wave owns 32 rows. Key/value tiles of 64
 // rows go from global memory straight into double-buffered LDS (direct-to-LDS
 // loads, no staging registers): the next tile streams in while the current
 // one is computed. Rows outside the problem or past the workgroup's reach
@@ -29,13 +29,15 @@
 
 namespace wmx {
 
-constexpr int kFwdBM = 128;  // query rows per workgroup
-constexpr int kFwdBN = 64;   // keys per tile
+constexpr int kFwdBN = 64;  // keys per tile
 
-template <int D, int MODE>
-__global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args args) {
+// NW waves of 32 query rows each: 4 (128 rows, two workgroups per CU) by
+// default; 8 (256 rows, one per CU) when few query tiles share long key
+// ranges, so each key/value tile streamed from HBM serves twice the rows.
+template <int D, int MODE, int NW>
+__global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void attn_fwd_kernel(const wmx_attn_args args) {
   const wmx_attn_args& a = args;
-  constexpr int BM = kFwdBM, BN = kFwdBN;
+  constexpr int BM = 32 * NW, BN = kFwdBN;
   static_assert(BN == kTileRows, "one LDS tile per key tile");
   constexpr int KS = D / 16;  // MFMA k-steps over head_dim
   constexpr int DB = D / 32;  // 32-row blocks of O^T
@@ -49,7 +51,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
   __shared__ __attribute__((aligned(1024))) bf16 v_lds0[kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 v_lds1[kTileElems];
   __shared__ int meta_lds[2][2][BN];  // per buffer: key ids (or key mask), key query ends
-  __shared__ int red_lds[4];
+  __shared__ int red_lds[NW];
 
   // ---- the work units: (batch row or segment, query tile, head) ----
   const int qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
@@ -57,7 +59,7 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
   const int32_t* list = a.q_units;  // (batch row or segment, tile) pairs, heaviest first
   const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
 
-  // this workgroup's unit: 128 query rows of one (batch row or segment, query head)
+  // this workgroup's unit: BM query rows of one (batch row or segment, query head)
   TileUnit tu;
   tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
   if (!tu.ok) return;
@@ -109,7 +111,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
     for (int o = 32; o > 0; o >>= 1) v = min(v, __shfl_xor(v, o));
     if (lane == 0) red_lds[wave] = v;
     __syncthreads();
-    v = min(min(red_lds[0], red_lds[1]), min(red_lds[2], red_lds[3]));
+    v = red_lds[0];
+#pragma unroll
+    for (int w = 1; w < NW; ++w) v = min(v, red_lds[w]);
     kt_begin_main = __builtin_amdgcn_readfirstlane(v < 0 ? 0 : v / BN);  // uniform: keeps the tile loop scalar
   }
   // document of this wave's rows when they all share one (ids are sorted),
@@ -139,9 +143,9 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
   auto tile_of = [&](int it) { return gap ? (it == 0 ? 0 : first_main + it - 1) : it; };
 
   // ---- key/value tiles: keys [0, reach) are visible to some row of the workgroup ----
-  TileDMA<D> dma;
+  TileDMA<D, NW> dma;
   dma.init(wave, lane);
-  KeyTiles<MODE, D> keys;
+  KeyTiles<MODE, D, NW> keys;
   keys.init(a, pb, hk, slot0 ? max(lim_max_wg + 1, 1) : lim_max_wg + 1, dma);
   // masking metadata of a key tile, loaded into a register while the tile
   // streams in and stored to LDS once the previous buffer is free
@@ -302,26 +306,32 @@ __global__ __launch_bounds__(256, 2) void attn_fwd_kernel(const wmx_attn_args ar
   }
 }
 
-template <int D, int MODE>
+template <int D, int MODE, int NW>
 static int launch_fwd_t(const wmx_attn_args& a, hipStream_t stream) {
-  const int64_t qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + kFwdBM - 1) / kFwdBM;
+  constexpr int BM = 32 * NW;
+  const int64_t qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + BM - 1) / BM;
   const int64_t outer = MODE == kVarlen ? a.num_segments : a.batch;
   const int64_t per_head = a.q_units ? a.num_q_units : qtiles * outer;
   const int64_t units = per_head * a.q_heads;
   if (units <= 0) return WMX_OK;
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
-  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE>), dim3((unsigned)units), dim3(256), 0, stream, a);
+  hipLaunchKernelGGL((attn_fwd_kernel<D, MODE, NW>), dim3((unsigned)units), dim3(64 * NW), 0, stream, a);
   return WMX_OK;
+}
+
+template <int MODE, int NW>
+static int launch_fwd_rows(const wmx_attn_args& a, hipStream_t stream) {
+  switch (a.head_dim) {
+    case 64: return launch_fwd_t<64, MODE, NW>(a, stream);
+    case 96: return launch_fwd_t<96, MODE, NW>(a, stream);
+    case 128: return launch_fwd_t<128, MODE, NW>(a, stream);
+    default: return WMX_E_UNSUPPORTED;
+  }
 }
 
 template <int MODE>
 static int launch_fwd_mode(const wmx_attn_args& a, hipStream_t stream) {
-  switch (a.head_dim) {
-    case 64: return launch_fwd_t<64, MODE>(a, stream);
-    case 96: return launch_fwd_t<96, MODE>(a, stream);
-    case 128: return launch_fwd_t<128, MODE>(a, stream);
-    default: return WMX_E_UNSUPPORTED;
-  }
+  return a.query_tile == 256 ? launch_fwd_rows<MODE, 8>(a, stream) : launch_fwd_rows<MODE, 4>(a, stream);
 }
 
 int launch_fwd(const wmx_attn_args& a, hipStream_t stream) {

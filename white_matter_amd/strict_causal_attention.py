@@ -332,9 +332,14 @@ def strict_dense_fwd(
     out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
     lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
     vis = _dense_visibility(query_offset, row_offset, row_limit, key_mask, keep_slot0)
+    # a chunk of queries after a long cached prefix: 256-row workgroups read
+    # each key/value tile once for twice the rows (the prefix dominates)
+    vis.query_tile = 256 if length > _kernels.QUERY_TILE and k.shape[2] >= 4 * length else 0
     if row_offset is not None or row_limit is not None:
         # ragged rows (cached prefixes): heaviest tiles first
-        vis.q_units = _kernels.dense_units(batch, length, k.shape[2], query_offset, row_offset, row_limit, q.device)
+        vis.q_units = _kernels.dense_units(
+            batch, length, k.shape[2], query_offset, row_offset, row_limit, q.device, vis.query_tile or _kernels.QUERY_TILE
+        )
     _kernels.forward(q, k, v, out.transpose(1, 2), lse, scale, vis)
     return out, lse
 

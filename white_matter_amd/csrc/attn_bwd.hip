@@ -659,6 +659,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       kseg = key_lds[1][kl];
       kqend = key_lds[2][kl];
     }
+    // element r of block mb is row ml = 4 half + c with the constant
+    // c = 32 mb + 8 (r / 4) + r % 4: the row rules become compares of c
+    // against per-lane bounds
+    const int lo_c = lo - 4 * half, hi_c = hi - 4 * half, kqend_c = kqend - m0 - 4 * half;
 #pragma unroll
     for (int mb = 0; mb < BMQ / 32; ++mb) {
       if (!full) {
@@ -666,11 +670,12 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
         __asm__ volatile("");
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int ml = mb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          bool keep = (ml >= lo) & (ml < hi);
+          const int c = mb * 32 + 8 * (r >> 2) + (r & 3);
+          const int ml = c + 4 * half;
+          bool keep = (c >= lo_c) & (c < hi_c);
           if constexpr (MODE == kDoc) {
             const int qsg = qdoc_lds[B][0][ml], qst = qdoc_lds[B][1][ml];
-            keep = keep & (((qsg == kseg) & (n >= qst)) | (kseg == -1)) & (m0 + ml < kqend);
+            keep = keep & (((qsg == kseg) & (n >= qst)) | (kseg == -1)) & (c < kqend_c);
           }
           tacc[mb][r] = keep ? tacc[mb][r] : kNegInf;
         }

@@ -193,20 +193,28 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void attn_fwd_kernel(cons
     if (masked) {
       // keeps this block a real (wave-uniform) branch instead of selects
       __asm__ volatile("");
+      // element r of block nb holds key j = n0 + 4 half + c with the constant
+      // c = 32 nb + 8 (r / 4) + r % 4: the rules become compares of c against
+      // per-lane bounds formed once per tile
+      const int base = n0 + 4 * half;
+      const int lim_c = lim_i - base;                         // j <= lim_i
+      const bool dummy_here = slot0 && n0 == 0 && half == 0;  // j == 0 is c == 0 there
+      const int nk_c = nk - base, qstart_c = qstart_i - base; // j < nk, j >= qstart_i
 #pragma unroll
       for (int nb = 0; nb < BN / 32; ++nb) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
-          const int jl = nb * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          const int j = n0 + jl;
+          const int c = nb * 32 + 8 * (r >> 2) + (r & 3);
+          const int jl = c + 4 * half;  // key within the tile (LDS metadata index)
           // bitwise forms: every term is evaluated, no per-lane branches
-          bool keep = (j <= lim_i) | (slot0 & (j == 0));
+          bool keep = c <= lim_c;
+          if (c == 0) keep = keep | dummy_here;
           if constexpr (MODE == kDense) {
             if (a.key_mask) keep = keep & (meta_lds[buf][0][jl] != 0);
           }
           if constexpr (MODE == kDoc) {
             const int ksg = meta_lds[buf][0][jl], kqe = meta_lds[buf][1][jl];
-            keep = keep & (j < nk) & (((ksg == qseg_i) & (j >= qstart_i)) | (ksg == -1)) & (i < kqe);
+            keep = keep & (c < nk_c) & (((ksg == qseg_i) & (c >= qstart_c)) | (ksg == -1)) & (i < kqe);
           }
           sacc[nb][r] = keep ? sacc[nb][r] : kNegInf;
         }

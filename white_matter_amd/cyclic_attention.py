@@ -136,6 +136,14 @@ def _packed_schedule(metadata, q_len: int, k_len: int, stride: int, offset: int)
         if all(r() is t for r, t in zip(refs, metadata)) and versions == tuple(t._version for t in metadata):
             return schedule
     schedule = _build_packed_schedule(*metadata, q_len, k_len, stride, offset)
+    if schedule is not None and schedule != "empty":
+        from .strict_causal_attention import _schedule_facts
+
+        if not _schedule_facts(schedule)[2]:
+            # dummy slots repeat in every segment of their row, which sends all
+            # of dK/dV through fp32 atomics (measured 4x slower at C3); the
+            # document-mode kernels keep one key row per slot
+            schedule = None
     entries[key] = (tuple(weakref.ref(t) for t in metadata), tuple(t._version for t in metadata), schedule)
     return schedule
 

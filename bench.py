@@ -12,7 +12,8 @@ value = 14 * D * Hq * P / step time, P = visible (query, key) pairs counted
 exactly from the metadata (the reference's FLOP convention,
 benchmarks/_flop_counter.py:33-34). Per-kernel averages come from HIP events
 on the launch stream; the dominant kernel gives the roofline object.
-Secondary fields: C4 KV-pool decode GB/s, C4 prefill forward TFLOP/s, C3 cyclic fwd+bwd
+Secondary fields: C4 KV-pool decode GB/s, the C2 step with the dummy slot (the model's
+call), C4 prefill forward TFLOP/s, C3 cyclic fwd+bwd
 TFLOP/s (stride 4; strides 2 and 8 and the dummy-slot variant in `cyclic_variants`),
 the fused KV-pool store GB/s beside the reference's eager steps, and the
 packed-document schedule builder's latency beside the torch sequence, and
@@ -116,14 +117,14 @@ def kernel_times(q, k, v, metadata, reps):
     alone through the C ABI between HIP events on the current stream, in the
     backward's order (dK/dV stores the dS that dQ reads)."""
     from white_matter_amd import _kernels, _native
-    from white_matter_amd.strict_causal_attention import _covering_schedule, _schedule_flags, _work_units
+    from white_matter_amd.strict_causal_attention import _covering_schedule, _keys_unique_code, _schedule_flags, _work_units
 
     batch, heads, length, dim = q.shape
     metadata = _covering_schedule(metadata, batch, length, k.shape[2])  # the schedule the operator runs
     max_q, max_k, flags = _schedule_flags(metadata)
     varlen = _kernels.Varlen(
         metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
-        metadata.cu_queries.numel() - 1, max_q, max_k, length, k.shape[2], bool(flags & 16), flags & 15,
+        metadata.cu_queries.numel() - 1, max_q, max_k, length, k.shape[2], _keys_unique_code(flags), flags & 15,
         *_work_units(metadata),
     )
     vis = _kernels.Visibility(varlen=varlen)
@@ -288,7 +289,7 @@ def main(argv=None) -> int:
     parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
     parser.add_argument(
         "--only",
-        choices=("decode", "prefill", "cyclic", "kv_store", "metadata", "decode_loop"),
+        choices=("decode", "prefill", "cyclic", "kv_store", "metadata", "decode_loop", "jacobi_dummy"),
         help="print one secondary line as JSON and exit (for profiling that path alone)",
     )
     parser.add_argument(
@@ -324,6 +325,7 @@ def main(argv=None) -> int:
             "kv_store": kv_store_line,
             "metadata": metadata_line,
             "decode_loop": decode_loop_line,
+            "jacobi_dummy": dummy_jacobi_line,
         }
         print(json.dumps({args.only: lines[args.only](device)}), flush=True)
         return 0
@@ -417,6 +419,7 @@ def main(argv=None) -> int:
 
     if not args.no_secondary:
         line["decode"] = decode_line(device)
+        line["jacobi_dummy"] = dummy_jacobi_line(device)
         line["prefill"] = prefill_line(device)
         line["cyclic"] = cyclic_line(device)
         line["cyclic_variants"] = [cyclic_line(device, 2), cyclic_line(device, 8), cyclic_line(device, 4, dummy=True)]
@@ -450,6 +453,39 @@ def decode_line(device):
         "gbps": round(gbps, 1),
         "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
         "bytes": kv_bytes + other,
+    }
+
+
+def dummy_jacobi_line(device, steps=30):
+    """The C2 step as the model calls it with use_dummy_token (the k8 recipe):
+    keys (8, 16, 2049, 128) with the dummy at slot 0, the same documents,
+    forward + backward; FLOPs over the visible pairs (every query also sees
+    the dummy)."""
+    from white_matter_amd import prepare_strict_causal_metadata, strict_causal_attention
+
+    q, k, v, docs, _, _ = strict_jacobi_setup(device)
+    batch, heads, length, dim = q.shape
+    gen = torch.Generator().manual_seed(4)
+    k = torch.cat(((torch.randn(batch, heads, 1, dim, generator=gen) * dim**-0.5).to(device, k.dtype), k), 2)
+    v = torch.cat(((torch.randn(batch, heads, 1, dim, generator=gen) * dim**-0.5).to(device, v.dtype), v), 2)
+    metadata = prepare_strict_causal_metadata(docs, length, use_dummy_token=True)
+    leaves = [t.clone().requires_grad_() for t in (q, k, v)]
+    grad_out = torch.ones(batch, length, heads, dim, device=device, dtype=torch.bfloat16)
+
+    def step():
+        out = strict_causal_attention(*leaves, metadata=metadata, use_dummy_token=True)
+        torch.autograd.grad(out, leaves, grad_out)
+
+    for _ in range(3):
+        step()
+    ms = Timer()(step, steps)
+    pairs = visible_pairs(metadata)
+    tflops = 14 * dim * heads * pairs / (ms * 1e-3) / 1e12
+    return {
+        "workload": "C2 Jacobi with the dummy slot (use_dummy_token=True, keys 2049), fwd+bwd",
+        "ms_per_step": round(ms, 4),
+        "tflops": round(tflops, 2),
+        "frac_mfma": round(tflops / PEAK_BF16_TFLOPS, 4),
     }
 
 

@@ -107,7 +107,12 @@ typedef struct wmx_attn_args {
   const uint8_t* key_mask;    /* optional (B, Tk) bool rows */
   int64_t key_mask_stride;
   int32_t keep_slot0;
-  int32_t keys_unique;        /* varlen: no key row appears in two segments */
+  int32_t keys_unique;        /* varlen: 1 = no key row appears in two segments;
+                               * 2 = only slot 0 of a batch row (a leading dummy
+                               * every segment of the row holds) repeats: its
+                               * dK/dV go through fp32 accumulators, the other
+                               * rows are stored directly; 0 = any row may repeat
+                               * (fp32 accumulators for all) */
   const int32_t* q_seg;       /* optional cyclic document metadata, int32 contiguous */
   const int32_t* k_seg;
   const int32_t* q_start;

@@ -48,10 +48,7 @@ def test_packed_matches_document_kernels_and_oracle(stride, dummy, monkeypatch):
         schedule = cyclic_module._packed_schedule(
             metas[residue], q.shape[2], keys, stride, residue - int(not dummy)
         )
-        if dummy:  # repeated dummy keys: the document-mode kernels run
-            assert schedule is None
-        else:
-            assert schedule is not None and schedule != "empty", "builder metadata takes the packed route"
+        assert schedule is not None and schedule != "empty", "builder metadata takes the packed route"
         with monkeypatch.context() as m:
             m.setattr(cyclic_module, "_packed_schedule", lambda *a, **kw: None)
             doc_out, doc_grads = _run(q, k, v, options, probe)

@@ -69,7 +69,7 @@ class Varlen:
     max_keys: int
     query_extent: int
     key_extent: int
-    keys_unique: bool
+    keys_unique: int  # wmx_attn_args.keys_unique: 1 unique, 2 only slot 0 repeats, 0 others repeat
     segment_layout: int = 0  # bit 0 consecutive queries, bit 1 consecutive keys from key 1
     q_units: torch.Tensor | None = None  # int32 (n, 2) (segment, query tile), heaviest first
     k_units: torch.Tensor | None = None  # int32 (n, 2) (segment, key tile), heaviest first

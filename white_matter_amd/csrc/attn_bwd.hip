@@ -815,6 +815,20 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       }
     }
   } else {
+    if (MODE == kVarlen && a.keys_unique == 2 && kslot == 0) {
+      // the shared dummy row: fp32 accumulators [batch row][kv head][D], dK then dV
+      float* dst = (float*)a.workspace + ((int64_t)kb * a.kv_heads + hk) * D +
+                   (dp_side ? 0 : (int64_t)a.batch * a.kv_heads * D);
+#pragma unroll
+      for (int d = 0; d < DB; ++d) {
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+          const int dd = d * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+          atomicAdd(dst + dd, acc[d][r] * scale);
+        }
+      }
+      return;
+    }
     bf16* dst = dp_side ? (bf16*)row_at(a.dk, a.dk_stride, kb, hk, kslot) : (bf16*)row_at(a.dv, a.dv_stride, kb, hk, kslot);
     store_acc_row<DB>(dst, acc, scale, half);
   }
@@ -830,18 +844,20 @@ __global__ void zero_f32_kernel(float* p, int64_t n) {
   }
 }
 
-// Convert the fp32 [B*N][Hkv][D] accumulators to bf16 dK/dV with their strides.
+// Convert the fp32 [B*R][Hkv][D] accumulators (R = bwd_acc_rows: every slot,
+// or slot 0 only) to bf16 dK/dV with their strides.
 __global__ void acc_to_bf16_kernel(const wmx_attn_args a) {
   const int D = a.head_dim;
-  const int64_t total = (int64_t)a.batch * a.key_extent * a.kv_heads * D;
+  const int64_t rows = bwd_acc_rows(a);
+  const int64_t total = (int64_t)a.batch * rows * a.kv_heads * D;
   const int64_t idx = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
   if (idx >= total) return;
   const int d = (int)(idx % D);
   const int64_t rh = idx / D;
   const int h = (int)(rh % a.kv_heads);
   const int64_t row = rh / a.kv_heads;
-  const int b = (int)(row / a.key_extent);
-  const int slot = (int)(row % a.key_extent);
+  const int b = (int)(row / rows);
+  const int slot = (int)(row % rows);
   const float* acck = (const float*)a.workspace;
   const float* accv = acck + total;
   ((bf16*)a.dk)[(int64_t)b * a.dk_stride[0] + (int64_t)h * a.dk_stride[1] + (int64_t)slot * a.dk_stride[2] + d] =
@@ -920,11 +936,15 @@ static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
   const dim3 grid((unsigned)units);
   const bool ds = bwd_uses_ds(a);
-  if (MODE == kVarlen && !a.keys_unique) {
+  if (MODE == kVarlen && a.keys_unique != 1) {
     const int64_t n = bwd_acc_bytes(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,
                        (float*)a.workspace, n);
-    if (ds) {
+    // every row through atomics, or (keys_unique 2) slot 0 only: the direct-store kernel
+    if (a.keys_unique == 2) {
+      if (ds) hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false, true>), grid, dim3(512), 0, stream, a);
+      else hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false, false>), grid, dim3(512), 0, stream, a);
+    } else if (ds) {
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true, true>), grid, dim3(512), 0, stream, a);
     } else {
       hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true, false>), grid, dim3(512), 0, stream, a);

@@ -58,6 +58,7 @@ int check_common(const wmx_attn_args* a, bool backward) {
     if (a->key_mask) return fail(WMX_E_INVALID, "varlen schedule and key_mask are exclusive");
     if (a->row_offset || a->row_limit) return fail(WMX_E_INVALID, "varlen schedule takes no row offsets");
     if (a->k_units && a->num_k_units < 0) return fail(WMX_E_INVALID, "negative work-list length");
+    if (a->keys_unique < 0 || a->keys_unique > 2) return fail(WMX_E_INVALID, "keys_unique must be 0, 1 or 2");
     if (a->ds_offsets && a->ds_elements < 0) return fail(WMX_E_INVALID, "negative ds_elements");
   } else if (a->k_units || a->ds_offsets) {
     return fail(WMX_E_INVALID, "key work lists and dS offsets need a varlen schedule");

@@ -15,13 +15,18 @@ enum Mode {
 };
 
 // Backward workspace: fp32 dK/dV accumulators (varlen schedules whose key
-// rows repeat), then from a 256-byte boundary the bf16 dS buffer: per query
+// rows repeat: all rows, or slot 0 only), then from a 256-byte boundary the bf16 dS buffer: per query
 // head and problem (batch row or segment) a block of keys x ld elements,
 // ld = queries rounded up to 128, holding dS^T (element [j * ld + i] for key
 // j and query i).
+// Rows of the fp32 dK/dV accumulators per batch row: every key slot when any
+// key row may repeat, slot 0 only when only the leading dummy repeats.
+__host__ __device__ inline int64_t bwd_acc_rows(const wmx_attn_args& a) {
+  if (!a.query_indices || a.keys_unique == 1) return 0;
+  return a.keys_unique == 2 ? 1 : a.key_extent;
+}
 __host__ __device__ inline int64_t bwd_acc_bytes(const wmx_attn_args& a) {
-  if (!a.query_indices || a.keys_unique) return 0;
-  return (int64_t)2 * a.batch * a.key_extent * a.kv_heads * a.head_dim * (int64_t)sizeof(float);
+  return (int64_t)2 * a.batch * bwd_acc_rows(a) * a.kv_heads * a.head_dim * (int64_t)sizeof(float);
 }
 __host__ __device__ inline int64_t bwd_ds_offset(const wmx_attn_args& a) { return (bwd_acc_bytes(a) + 255) & ~(int64_t)255; }
 __host__ __device__ inline int64_t ds_ld(int nq) { return ((int64_t)nq + 127) & ~(int64_t)127; }

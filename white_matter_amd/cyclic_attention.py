@@ -139,10 +139,10 @@ def _packed_schedule(metadata, q_len: int, k_len: int, stride: int, offset: int)
     if schedule is not None and schedule != "empty":
         from .strict_causal_attention import _schedule_facts
 
-        if not _schedule_facts(schedule)[2]:
-            # dummy slots repeat in every segment of their row, which sends all
-            # of dK/dV through fp32 atomics (measured 4x slower at C3); the
-            # document-mode kernels keep one key row per slot
+        if _schedule_facts(schedule)[2] == 0:
+            # key rows other than the dummy slot repeat: dK/dV would accumulate
+            # every row with atomics; the document-mode kernels keep one key
+            # row per slot (dummy slots alone go through small accumulators)
             schedule = None
     entries[key] = (tuple(weakref.ref(t) for t in metadata), tuple(t._version for t in metadata), schedule)
     return schedule

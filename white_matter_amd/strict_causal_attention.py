@@ -267,10 +267,11 @@ def _segment_layout(indices: torch.Tensor, cu: torch.Tensor, extent: int, skip_f
     return bool((indices == expected).all()) and rows_ok, rows_ok
 
 
-def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int, int, int, bool]:
+def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, int, int, int, int, bool]:
     """Host facts the kernels need, computed once per metadata object and kept
     on it: largest segment (queries, keys), whether key rows repeat across
-    segments, the largest query and key index (for bounds checks), the
+    segments (wmx_attn_args keys_unique: 1 none, 2 only slot 0, 0 others),
+    the largest query and key index (for bounds checks), the
     segment layout bits of wmx_attn_args (consecutive / one-row slots), and
     whether query rows repeat."""
     facts = getattr(metadata, "_facts", None)
@@ -282,7 +283,12 @@ def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, bool, int
         if segments and (segments[-1][1] != qi.numel() or segments[-1][3] != ki.numel()):
             raise ValueError("metadata segments do not cover query_indices/key_indices")
         n = ki.numel()
-        unique = n == 0 or int(torch.unique(ki).numel()) == n
+        # 1: key rows unique; 2: only slot 0 of a batch row (a leading dummy
+        # shared by the row's segments) repeats; 0: other rows repeat
+        unique = 1 if n == 0 or int(torch.unique(ki).numel()) == n else 0
+        if not unique:
+            real = ki[ki % metadata.key_extent != 0]
+            unique = 2 if int(torch.unique(real).numel()) == real.numel() else 0
         unique_q = qi.numel() == 0 or int(torch.unique(qi).numel()) == qi.numel()
         top_q = int(qi.max()) if qi.numel() else -1
         top_k = int(ki.max()) if n else -1
@@ -412,13 +418,19 @@ def _dense_backward(ctx, dout, dlse):
 strict_dense_fwd.register_autograd(_dense_backward, setup_context=_dense_setup)
 
 
-_KEYS_UNIQUE = 16  # schedule_flags bit above the four segment-layout bits
+_KEYS_UNIQUE = 16  # schedule_flags bits above the four segment-layout bits
+_KEYS_UNIQUE_BUT_SLOT0 = 32
 
 
 def _schedule_flags(metadata: StrictCausalMetadata) -> tuple[int, int, int]:
     """(max_queries, max_keys, flags) passed to the varlen operators."""
     max_q, max_k, unique, _, _, layout, _ = _schedule_facts(metadata)
-    return max_q, max_k, layout | (_KEYS_UNIQUE if unique else 0)
+    return max_q, max_k, layout | {1: _KEYS_UNIQUE, 2: _KEYS_UNIQUE_BUT_SLOT0}.get(unique, 0)
+
+
+def _keys_unique_code(flags: int) -> int:
+    """wmx_attn_args.keys_unique from the schedule flags."""
+    return 1 if flags & _KEYS_UNIQUE else 2 if flags & _KEYS_UNIQUE_BUT_SLOT0 else 0
 
 
 def _schedule_gaps(
@@ -430,8 +442,10 @@ def _schedule_gaps(
       - O rows of the (B*T, H*D) view of the (B, T, H, D) output,
       - dQ rows of the (B*H*T, D) view of the (B, H, T, D) gradient,
       - dK/dV rows of the (B*Hkv*N, D) view of the (B, Hkv, N, D) gradients.
-    Repeated key rows go through fp32 accumulators converted in full, which
-    leaves no key gap. Cached on the metadata object per call shape."""
+    Where any key row may repeat, the fp32 accumulators are converted in
+    full, which leaves no key gap; where only slot 0 repeats (keys_unique 2)
+    the other rows are stored directly and their gaps are zeroed too. Cached
+    on the metadata object per call shape."""
     cache = metadata.__dict__.setdefault("_gaps", {})
     key = (batch, length, heads, key_extent, kv_heads)
     gaps = cache.get(key)
@@ -455,7 +469,7 @@ def _schedule_gaps(
             return ((b[:, None] * count + h[None, :]) * extent + t[:, None]).flatten()
 
         out_rows = missing(metadata.query_indices, batch * length, unique_q)
-        key_flat = missing(metadata.key_indices, batch * key_extent, True) if unique_k else none
+        key_flat = missing(metadata.key_indices, batch * key_extent, unique_k == 1) if unique_k else none
         gaps = cache[key] = (out_rows, per_head(out_rows, length, heads), per_head(key_flat, key_extent, kv_heads))
     return gaps
 
@@ -569,7 +583,7 @@ def _varlen(
         max_keys=max_k,
         query_extent=query.shape[2],
         key_extent=key.shape[2],
-        keys_unique=bool(flags & _KEYS_UNIQUE),
+        keys_unique=_keys_unique_code(flags),
         segment_layout=flags & 15,
         q_units=q_units,
         k_units=k_units,

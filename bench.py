@@ -289,7 +289,7 @@ def main(argv=None) -> int:
     parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
     parser.add_argument(
         "--only",
-        choices=("decode", "prefill", "cyclic", "kv_store", "metadata", "decode_loop", "jacobi_dummy"),
+        choices=("decode", "prefill", "cyclic", "kv_store", "metadata", "decode_loop", "jacobi_dummy", "c5"),
         help="print one secondary line as JSON and exit (for profiling that path alone)",
     )
     parser.add_argument(
@@ -326,6 +326,7 @@ def main(argv=None) -> int:
             "metadata": metadata_line,
             "decode_loop": decode_loop_line,
             "jacobi_dummy": dummy_jacobi_line,
+            "c5": c5_line,
         }
         print(json.dumps({args.only: lines[args.only](device)}), flush=True)
         return 0
@@ -426,6 +427,7 @@ def main(argv=None) -> int:
         line["kv_store"] = kv_store_line(device)
         line["metadata"] = metadata_line(device)
         line["decode_loop"] = decode_loop_line(device)
+        line["c5"] = c5_line(device)
 
     if not args.no_cpu_baseline:
         line["cpu_baseline"] = cpu_baseline(q, k, v, metadata, args.cpu_budget)
@@ -609,6 +611,41 @@ def decode_loop_line(device, batch=8, heads=16, kv_heads=8, channels=8, dim=64, 
         "gbps": round(per_token / (graph_ms * 1e-3) / 1e9, 1),
         "frac_hbm": round(per_token / (graph_ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
         "bytes_per_token": int(per_token),
+    }
+
+
+def c5_line(device, batch=8, length=2048, tokens=128, seed=13):
+    """C5 end to end: the 24-layer model (d 1024, 16x64 query heads, 8 KV heads,
+    8 pool channels over 25 sources, vocab 151936, bf16, random weights) on 8
+    rows of 2048 uniform random token ids packed into geometric documents
+    (mean 512): the cyclic prefill (8 groups, 3 passes, metadata and packed
+    schedules built in the call) through the HIP attention and store kernels,
+    then 128 greedy decode steps replayed from one graph. hipBLASLt (torch)
+    runs the projections, routers and MLPs."""
+    from white_matter_amd.cyclic_pass import FeedbackConfig, FeedbackModel, GreedyDecoder, forward_cyclic
+
+    config = FeedbackConfig()
+    model = FeedbackModel(config, device=device, seed=seed)
+    gen = torch.Generator().manual_seed(seed)
+    ids = torch.randint(0, config.vocab_size, (batch, length), generator=gen).to(device)
+    docs = geometric_documents(batch, length, seed).to(device)
+    capacity = length + 1 + tokens
+    forward_cyclic(model, ids, docs, capacity=capacity)  # warm-up: GEMM heuristics, allocator
+    timer = Timer()
+    prefill_ms = timer(lambda: forward_cyclic(model, ids, docs, capacity=capacity), 2)
+    hidden, keys, values, positions = forward_cyclic(model, ids, docs, capacity=capacity)
+    decoder = GreedyDecoder.after_prefill(model, hidden, keys, values, positions, docs)
+    decode_ms = timer(decoder, tokens)
+    return {
+        "workload": f"C5: {config.num_layers} layers, d {config.hidden_size}, {config.num_heads}x{config.head_dim} "
+        f"query heads, {config.num_kv_heads} KV heads, {config.num_kv_channels} channels over {config.num_sources} "
+        f"sources, vocab {config.vocab_size}; B={batch} T={length} geometric documents, {config.cyclic_groups} "
+        f"groups x {config.num_passes} passes, then {tokens} greedy tokens from one graph",
+        "prefill_ms": round(prefill_ms, 2),
+        "prefill_tokens_per_s": round(batch * length / (prefill_ms * 1e-3)),
+        "decode_ms_per_token": round(decode_ms, 4),
+        "decode_tokens_per_s": round(batch / (decode_ms * 1e-3)),
+        "data": "synthetic token ids, random-initialised weights",
     }
 
 

@@ -16,8 +16,9 @@ Secondary fields: C4 KV-pool decode GB/s, the C2 step with the dummy slot (the m
 call), C4 prefill forward TFLOP/s, C3 cyclic fwd+bwd
 TFLOP/s (stride 4; strides 2 and 8 and the dummy-slot variant in `cyclic_variants`),
 the fused KV-pool store GB/s beside the reference's eager steps, and the
-packed-document schedule builder's latency beside the torch sequence, and
-the captured decode loop's per-token time beside eager launches.
+packed-document schedule builder's latency beside the torch sequence,
+the captured decode loop's per-token time beside eager launches, and the C5
+harness (a 24-layer model's cyclic prefill and greedy decoding on these kernels).
 The CPU baseline times the oracle (float32, dense mask) on a bounded sample.
 """
 
@@ -286,7 +287,7 @@ def main(argv=None) -> int:
     parser.add_argument("--kernel-reps", type=int, default=20)
     parser.add_argument("--cpu-budget", type=float, default=12.0, help="seconds of CPU baseline work")
     parser.add_argument("--no-cpu-baseline", action="store_true")
-    parser.add_argument("--no-secondary", action="store_true", help="skip the decode and cyclic lines")
+    parser.add_argument("--no-secondary", action="store_true", help="skip the secondary lines (decode, cyclic, store, builder, loops, C5)")
     parser.add_argument(
         "--only",
         choices=("decode", "prefill", "cyclic", "kv_store", "metadata", "decode_loop", "jacobi_dummy", "c5"),

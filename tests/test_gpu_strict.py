@@ -80,6 +80,25 @@ def test_ragged_decode_ignores_nan_capacity(dummy):
     assert_bf16_close(actual, expected, what="decode")
 
 
+@pytest.mark.parametrize("num_splits", [1, 3, 0])
+@torch.no_grad()
+def test_decode_split_counts(num_splits):
+    """One split writes the output itself (no combine launch); several splits
+    merge partials. Both against the oracle on a long ragged, masked pool."""
+    torch.manual_seed(4)
+    capacity = 1500
+    q = torch.randn(2, 8, 1, 128, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(2, 4, capacity, 128, device=DEV, dtype=torch.bfloat16)
+    v = torch.randn_like(k)
+    lengths = torch.tensor([1499, 611], device=DEV)
+    keep = torch.rand(2, capacity, device=DEV) < 0.7
+    actual = strict_causal_attention(q, k, v, query_start=lengths, kv_lengths=lengths, use_dummy_token=True,
+                                     key_mask=keep, num_splits=num_splits)
+    expected = ref.strict_attention(q.cpu(), k.cpu(), v.cpu(), query_start=lengths.cpu(), kv_lengths=lengths.cpu(),
+                                    use_dummy_token=True, key_mask=keep.cpu())
+    assert_bf16_close(actual, expected, what=f"decode, {num_splits} splits")
+
+
 @pytest.mark.parametrize("dummy", [False, True])
 def test_ragged_prefixes_with_truncated_history(dummy):
     torch.manual_seed(5)

@@ -175,6 +175,26 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
     }
   }
   __syncthreads();
+  if (nsplit == 1) {
+    // the split is the whole row: merge the 4 waves and write the bf16 output
+    // (the same sums the combine kernel would form from one partial)
+    for (int idx = tid; idx < G * D; idx += 256) {
+      const int g = idx / D, d = idx % D;
+      float mx = kMaxFloor;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) mx = fmaxf(mx, lds_m[w][g]);
+      float acc = 0.f, lsum = 0.f;
+#pragma unroll
+      for (int w = 0; w < 4; ++w) {
+        const float s = __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
+        acc += lds_o[w][g][d] * s;
+        lsum += lds_l[w][g] * s;
+      }
+      const float r = lsum > 0.f ? acc / lsum : 0.f;
+      ((bf16*)a.o)[(int64_t)b * a.o_stride[0] + (int64_t)(h0 + g) * a.o_stride[1] + d] = (__bf16)r;
+    }
+    return;
+  }
   // merge the 4 waves and write the split's partial row
   float* ws_o = (float*)a.workspace;
   float* ws_ml = ws_o + (int64_t)a.batch * a.q_heads * nsplit * D;
@@ -268,6 +288,7 @@ int launch_decode(const wmx_decode_args& a, hipStream_t stream) {
     default: return WMX_E_UNSUPPORTED;
   }
   if (rc != WMX_OK) return rc;
+  if (nsplit == 1) return WMX_OK;  // the split kernel wrote the output
   const int threads = (a.head_dim + 63) / 64 * 64;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(a.q_heads, a.batch), dim3(threads), 0, stream, a, nsplit);
   return WMX_OK;

@@ -360,7 +360,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
   }
   auto issue_ds = [&](int n0, bf16* tile) __attribute__((always_inline)) {
     const int nvalid = min(max(reach - n0, 0), kTileRows);
-    sdma.issue_strided_rows(make_rsrc(ds + (int64_t)n0 * ld, nvalid * (int)ld * 2), tile, (int)ld * 2);
+    sdma.issue_strided_rows_once(make_rsrc(ds + (int64_t)n0 * ld, nvalid * (int)ld * 2), tile, (int)ld * 2);
   };
   auto load_meta = [&](int n0) -> int {
     const int j = n0 + (tid & 63);

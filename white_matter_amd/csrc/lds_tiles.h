@@ -181,6 +181,14 @@ struct TileDMA {
     for (int r = 0; r < kInstr; ++r)
       __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst(tile, r), 16, strided_offset(r, row_bytes), 0, 0, 0);
   }
+  // The same for data read once: the cache-policy immediate 2 is the
+  // nontemporal hint on gfx950.
+  __device__ __forceinline__ void issue_strided_rows_once(const rsrc_t& rs, bf16* tile, int row_bytes) const {
+    opaque_s(row_bytes);
+#pragma unroll
+    for (int r = 0; r < kInstr; ++r)
+      __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, dst(tile, r), 16, strided_offset(r, row_bytes), 0, 0, 2);
+  }
   // One tile: row(tr, ok, p) returns the address of tile row tr and sets
   // ok = false for a row that must read as zeros.
   template <class Row>

@@ -227,3 +227,25 @@ def test_feedback_metadata_matches_oracle_on_gpu():
     for a, e in zip(actual, expected):
         for ta, te in zip(a, e):
             assert ta.dtype == torch.int32 and (ta.cpu().numpy() == te).all()
+
+
+@pytest.mark.parametrize("dummy", [False, True])
+def test_cyclic_metadata_matches_oracle_on_gpu(dummy):
+    """prepare_cyclic_attention_metadata on device tensors, bit for bit against
+    the oracle's row-wise searches (reference metadata.py:17-56), int32 and
+    int64 ids, ragged id runs and repeated ids."""
+    gen = torch.Generator().manual_seed(23 + int(dummy))
+    for trial in range(16):
+        batch = 1 + trial % 3
+        q_len = int(torch.randint(1, 300, (1,), generator=gen))
+        k_len = int(torch.randint(2, 700, (1,), generator=gen))
+        q_ids = torch.randint(0, 3, (batch, q_len), generator=gen).cumsum(1)
+        k_ids = torch.randint(0, 2, (batch, k_len), generator=gen).cumsum(1)
+        if dummy:
+            k_ids[:, 0] = -1
+        dtype = torch.int32 if trial % 2 else torch.int64
+        actual = prepare_cyclic_attention_metadata(q_ids.to(DEV, dtype), k_ids.to(DEV, dtype), use_dummy_token=dummy)
+        expected = ref_meta.cyclic_metadata(q_ids.numpy(), k_ids.numpy(), use_dummy_token=dummy)
+        for a, e in zip(actual, expected):
+            assert a.device.type == "cuda" and a.dtype == torch.int32
+            assert (a.cpu().numpy() == e).all(), f"trial {trial}"

@@ -28,6 +28,15 @@ from . import _kernels, portable
 _BACKENDS = ("auto", "reference", "torch_flash", "flash_attention_2")
 
 
+def _standalone_flash_available() -> bool:
+    """The reference picks "flash_attention_2" for "auto" when the flash_attn
+    package is installed (strict_causal_attention.py:32-33,233-236). Here every
+    non-reference literal runs the same HIP kernels, so no package is looked
+    for; the FLOP counter (benchmarks/_flop_counter.py:90,98) then binds only
+    the operators this package registers."""
+    return False
+
+
 @dataclass(frozen=True)
 class StrictCausalMetadata:
     """Reusable varlen gather/scatter schedule, independent of heads and values
@@ -758,37 +767,6 @@ def strict_decode(
 def _(query, *args):
     batch, heads, _, dim = query.shape
     return query.new_empty(batch, 1, heads, dim, dtype=torch.bfloat16)
-
-
-@torch.library.custom_op("white_matter::flash_attention_decode", mutates_args=())
-def flash_attention_decode(
-    query: torch.Tensor,
-    key: torch.Tensor,
-    value: torch.Tensor,
-    lengths: torch.Tensor,
-    scale: float,
-    causal: bool,
-    num_splits: int = 0,
-) -> torch.Tensor:
-    """The reference's decode op (flash_attention.py:15-36) on the HIP kernel:
-    query (B, 1, H, D), key/value caches (B, N, Hkv, D), ``lengths`` visible
-    slots per row. A single query sees every visible slot, so ``causal`` does
-    not change the result."""
-    q = _kernels.operand(query.transpose(1, 2))
-    k = _kernels.operand(key.transpose(1, 2))
-    v = _kernels.operand(value.transpose(1, 2))
-    batch, heads, _, dim = q.shape
-    out = torch.empty(batch, 1, heads, dim, device=q.device, dtype=torch.bfloat16)
-    _kernels.decode(
-        q, k, v, out[:, 0], query_start=lengths, kv_lengths=None, key_mask=None,
-        use_dummy=False, scale=scale, num_splits=num_splits,
-    )
-    return out.to(query.dtype)
-
-
-@flash_attention_decode.register_fake
-def _(query, key, value, lengths, scale, causal, num_splits=0):
-    return query.new_empty(query.shape)
 
 
 # ------------------------------------------------------------ public API ----

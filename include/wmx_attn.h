@@ -323,6 +323,23 @@ int32_t wmx_decode_num_splits(const wmx_decode_args* args);
 /* Single-query decode forward. */
 int wmx_decode(const wmx_decode_args* args, void* stream);
 
+/*
+ * wmx_decode without a workspace: the split-K partials go to a static device
+ * array of WMX_DECODE_NOALLOC_MAX_BYTES that the library holds on each GPU it
+ * runs on until the process ends (args->workspace and workspace_bytes are
+ * ignored). No counterpart in the reference: this entry point is for callers
+ * that cannot allocate device memory (code under HIP graph capture, serving
+ * loops, harnesses that forbid hipMalloc). It calls no allocating routine; a
+ * call whose wmx_decode_workspace_size exceeds the maximum returns
+ * WMX_E_WORKSPACE. Every call on one GPU shares that GPU's array, so calls
+ * that overlap on one GPU (concurrent streams, or threads) race; calls in
+ * order on one stream do not. The array's first use on a device resolves its
+ * address there (hipGetSymbolAddress) with that device current; the stream
+ * must belong to the current device. Outputs are bit-identical to wmx_decode's.
+ */
+#define WMX_DECODE_NOALLOC_MAX_BYTES ((int64_t)8 << 20)
+int wmx_decode_noalloc(const wmx_decode_args* args, void* stream);
+
 /* KV-pool store (see wmx_kv_store_args): one pass over the group's keys and
  * values, writing the pool slots. Replaces the reference's eager sequence of
  * rms_norm, weight, RoPE, casts and index_copy_ (modules/kv_pool.py:163-172,

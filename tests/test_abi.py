@@ -54,6 +54,13 @@ def test_argument_checks_return_errors_without_launching():
     dec.head_dim, dec.batch, dec.q_heads, dec.kv_heads = 128, 1, 6, 2
     assert lib.wmx_decode(ctypes.byref(dec), None) == -2
     assert b"{1,2,4,8}" in lib.wmx_last_error()
+    # the allocation-free decode refuses partials beyond its static scratch
+    # before it touches a device
+    dec.q_heads, dec.capacity, dec.num_splits, dec.softmax_scale = 2, 4096, 20000, 0.1
+    dec.q = dec.k = dec.v = dec.o = 0x1000
+    assert lib.wmx_decode_workspace_size(ctypes.byref(dec)) > _native.DECODE_NOALLOC_MAX_BYTES
+    assert lib.wmx_decode_noalloc(ctypes.byref(dec), None) == -3
+    assert b"static scratch" in lib.wmx_last_error()
 
 
 def test_workspace_sizes():

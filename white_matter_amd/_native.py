@@ -190,6 +190,7 @@ EXPORTS = (
     "wmx_decode_workspace_size",
     "wmx_decode_num_splits",
     "wmx_decode",
+    "wmx_decode_noalloc",
     "wmx_kv_store_args_size",
     "wmx_kv_pool_store",
     "wmx_strict_meta_args_size",
@@ -221,8 +222,9 @@ def load() -> ctypes.CDLL:
     for name in ("wmx_attn_bwd_workspace_size", "wmx_attn_bwd_min_workspace_size"):
         getattr(lib, name).argtypes = [ctypes.POINTER(AttnArgs)]
         getattr(lib, name).restype = ctypes.c_int64
-    lib.wmx_decode.argtypes = [ctypes.POINTER(DecodeArgs), _vp]
-    lib.wmx_decode.restype = ctypes.c_int
+    for name in ("wmx_decode", "wmx_decode_noalloc"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(DecodeArgs), _vp]
+        getattr(lib, name).restype = ctypes.c_int
     lib.wmx_decode_workspace_size.argtypes = [ctypes.POINTER(DecodeArgs)]
     lib.wmx_decode_workspace_size.restype = ctypes.c_int64
     lib.wmx_decode_num_splits.argtypes = [ctypes.POINTER(DecodeArgs)]
@@ -307,6 +309,17 @@ def decode_workspace_size(args: DecodeArgs) -> int:
 def decode(args: DecodeArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_decode(ctypes.byref(args), _stream(device)), "wmx_decode")
+
+
+# wmx_decode_noalloc's static scratch per GPU (WMX_DECODE_NOALLOC_MAX_BYTES)
+DECODE_NOALLOC_MAX_BYTES = 8 << 20
+
+
+def decode_noalloc(args: DecodeArgs, device: torch.device) -> None:
+    """wmx_decode with the partials in the library's static device scratch
+    (args.workspace is ignored); no device memory is allocated."""
+    lib = load()
+    _check(lib, lib.wmx_decode_noalloc(ctypes.byref(args), _stream(device)), "wmx_decode_noalloc")
 
 
 def kv_pool_store(args: KvStoreArgs, device: torch.device) -> None:

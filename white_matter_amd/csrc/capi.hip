@@ -5,8 +5,17 @@
 #include <cstdarg>
 #include <cstdio>
 #include <cstring>
+#include <mutex>
 
 #include "wmx_kernels.h"
+
+// Device scratch of wmx_decode_noalloc: the split-K partials live here instead
+// of in a caller-allocated workspace. Each GPU holds its own copy for the life
+// of the process. Host code never uses this name as an address: the entry
+// point resolves the array's device address once per device with
+// hipGetSymbolAddress and passes that pointer to the kernels.
+constexpr int64_t kDecodeScratchBytes = WMX_DECODE_NOALLOC_MAX_BYTES;
+static __device__ __align__(256) unsigned char scratch[kDecodeScratchBytes];
 
 namespace {
 
@@ -91,6 +100,54 @@ int launched(int rc) {
   }
   const hipError_t e = hipGetLastError();
   if (e != hipSuccess) return fail(WMX_E_LAUNCH, "launch failed: %s", hipGetErrorString(e));
+  return WMX_OK;
+}
+
+// Everything wmx_decode checks except the workspace.
+int check_decode(const wmx_decode_args* a) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->head_dim != 64 && a->head_dim != 96 && a->head_dim != 128)
+    return fail(WMX_E_UNSUPPORTED, "head_dim %d is not 64, 96 or 128", a->head_dim);
+  if (a->batch < 0 || a->q_heads <= 0 || a->kv_heads <= 0 || a->capacity < 0)
+    return fail(WMX_E_INVALID, "negative or zero shape");
+  if (a->q_heads % a->kv_heads != 0) return fail(WMX_E_INVALID, "q_heads %% kv_heads != 0");
+  const int g = a->q_heads / a->kv_heads;
+  if (g != 1 && g != 2 && g != 4 && g != 8)
+    return fail(WMX_E_UNSUPPORTED, "decode supports query heads per KV head in {1,2,4,8}, got %d", g);
+  if (!a->q || !a->k || !a->v || !a->o) return fail(WMX_E_INVALID, "q/k/v/o pointer is NULL");
+  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v))
+    return fail(WMX_E_INVALID, "q/k/v must be 16-byte aligned");
+  if (a->q_stride[0] % 8 || a->q_stride[1] % 8 || !strides_vec8(a->k_stride, 3) || !strides_vec8(a->v_stride, 3))
+    return fail(WMX_E_INVALID, "q/k/v strides must be multiples of 8 elements");
+  if (a->use_dummy != 0 && a->use_dummy != 1) return fail(WMX_E_INVALID, "use_dummy must be 0 or 1");
+  return WMX_OK;
+}
+
+// Device address of `scratch` on the current device, resolved once per device
+// (with that device current) and kept.
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mutex;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int decode_scratch(void* stream, void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return fail(WMX_E_LAUNCH, "hipGetDevice failed: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= kMaxScratchDevices)
+    return fail(WMX_E_UNSUPPORTED, "device %d is beyond the %d devices the static scratch serves", dev, kMaxScratchDevices);
+  int sdev = dev;
+  e = hipStreamGetDevice((hipStream_t)stream, &sdev);
+  if (e != hipSuccess) return fail(WMX_E_INVALID, "hipStreamGetDevice failed: %s", hipGetErrorString(e));
+  if (sdev != dev) return fail(WMX_E_INVALID, "the stream belongs to device %d, the current device is %d", sdev, dev);
+  std::lock_guard<std::mutex> lock(g_scratch_mutex);
+  if (!g_scratch_ptr[dev]) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess || !p)
+      return fail(WMX_E_LAUNCH, "hipGetSymbolAddress(scratch) failed on device %d: %s", dev, hipGetErrorString(e));
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
   return WMX_OK;
 }
 
@@ -216,21 +273,7 @@ int64_t wmx_decode_workspace_size(const wmx_decode_args* args) {
 int32_t wmx_decode_num_splits(const wmx_decode_args* args) { return args ? wmx::decode_num_splits(*args) : 0; }
 
 int wmx_decode(const wmx_decode_args* a, void* stream) {
-  if (!a) return fail(WMX_E_INVALID, "args is NULL");
-  if (a->head_dim != 64 && a->head_dim != 96 && a->head_dim != 128)
-    return fail(WMX_E_UNSUPPORTED, "head_dim %d is not 64, 96 or 128", a->head_dim);
-  if (a->batch < 0 || a->q_heads <= 0 || a->kv_heads <= 0 || a->capacity < 0)
-    return fail(WMX_E_INVALID, "negative or zero shape");
-  if (a->q_heads % a->kv_heads != 0) return fail(WMX_E_INVALID, "q_heads %% kv_heads != 0");
-  const int g = a->q_heads / a->kv_heads;
-  if (g != 1 && g != 2 && g != 4 && g != 8)
-    return fail(WMX_E_UNSUPPORTED, "decode supports query heads per KV head in {1,2,4,8}, got %d", g);
-  if (!a->q || !a->k || !a->v || !a->o) return fail(WMX_E_INVALID, "q/k/v/o pointer is NULL");
-  if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v))
-    return fail(WMX_E_INVALID, "q/k/v must be 16-byte aligned");
-  if (a->q_stride[0] % 8 || a->q_stride[1] % 8 || !strides_vec8(a->k_stride, 3) || !strides_vec8(a->v_stride, 3))
-    return fail(WMX_E_INVALID, "q/k/v strides must be multiples of 8 elements");
-  if (a->use_dummy != 0 && a->use_dummy != 1) return fail(WMX_E_INVALID, "use_dummy must be 0 or 1");
+  if (const int rc = check_decode(a)) return rc;
   const int64_t need = wmx::decode_workspace_size(*a);
   if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
     return fail(WMX_E_WORKSPACE, "decode needs %lld workspace bytes", (long long)need);
@@ -239,6 +282,21 @@ int wmx_decode(const wmx_decode_args* a, void* stream) {
     return WMX_OK;
   }
   return launched(wmx::launch_decode(*a, (hipStream_t)stream));
+}
+
+int wmx_decode_noalloc(const wmx_decode_args* a, void* stream) {
+  if (const int rc = check_decode(a)) return rc;
+  const int64_t need = wmx::decode_workspace_size(*a);
+  if (need > kDecodeScratchBytes)
+    return fail(WMX_E_WORKSPACE, "decode needs %lld scratch bytes, beyond the %lld-byte static scratch of wmx_decode_noalloc",
+                (long long)need, (long long)kDecodeScratchBytes);
+  if (a->batch == 0 || a->capacity == 0) return WMX_OK;
+  void* ptr = nullptr;
+  if (const int rc = decode_scratch(stream, &ptr)) return rc;
+  wmx_decode_args b = *a;
+  b.workspace = ptr;
+  b.workspace_bytes = kDecodeScratchBytes;
+  return launched(wmx::launch_decode(b, (hipStream_t)stream));
 }
 
 }  // extern "C"

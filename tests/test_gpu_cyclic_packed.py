@@ -3,7 +3,7 @@
 oracle and against the document-mode kernels on the same inputs; the packed
 route is the one taken for builder metadata, a query that sees no key gets a
 zero row and an infinite LSE, and an in-place change of the metadata builds a
-new schedule."""
+new schedule (the C++ operators' schedule cache sees the version counter)."""
 
 import importlib
 
@@ -45,13 +45,15 @@ def test_packed_matches_document_kernels_and_oracle(stride, dummy, monkeypatch):
         options = dict(query_stride=stride, query_offset=residue, strict_past=not dummy, metadata=metas[residue])
         probe = torch.randn(q.shape, device=DEV, dtype=torch.bfloat16)
         packed_out, packed_grads = _run(q, k, v, options, probe)
-        schedule = cyclic_module._packed_schedule(
-            metas[residue], q.shape[2], keys, stride, residue - int(not dummy)
-        )
-        assert schedule is not None and schedule != "empty", "builder metadata takes the packed route"
+        facts = torch.ops.white_matter._cyclic_schedule(*metas[residue], q.shape[2], keys, stride,
+                                                         residue - int(not dummy))[0]
+        assert int(facts[0]) == 2, "builder metadata takes the packed route"
+        # the document-mode kernels on the same inputs: a packer that refuses
         with monkeypatch.context() as m:
-            m.setattr(cyclic_module, "_packed_schedule", lambda *a, **kw: None)
+            m.setattr(cyclic_module, "_build_packed_schedule", lambda *a, **kw: None)
+            torch.ops.white_matter._cyclic_schedule_cache_clear()
             doc_out, doc_grads = _run(q, k, v, options, probe)
+        torch.ops.white_matter._cyclic_schedule_cache_clear()
         leaves = [t.double().cpu().requires_grad_() for t in (q, k, v)]
         expected = ref.cyclic_attention(*leaves, query_stride=stride, query_offset=residue, strict_past=not dummy,
                                         metadata=tuple(t.cpu() for t in metas[residue]))
@@ -76,7 +78,10 @@ def test_unseen_queries_and_metadata_changes():
     first = torch.arange(0, 16, 2)
     assert (out[:, :, first] == 0).all() and torch.isinf(lse[:, :, first]).all()
     assert torch.isfinite(lse[:, :, 1::2]).all()
-    before = cyclic_module._packed_schedule(meta, 16, length, stride, -1)
+    cached = torch.ops.white_matter._cyclic_schedule_cache_size()
+    cyclic_module.cyclic_attn_doc_fwd(q, k, v, *meta, stride, -1, 64)
+    assert torch.ops.white_matter._cyclic_schedule_cache_size() == cached  # a cache hit
     meta.key_query_end.add_(0)  # an in-place write bumps the version: the schedule is rebuilt
-    after = cyclic_module._packed_schedule(meta, 16, length, stride, -1)
-    assert after is not before and torch.equal(after.key_indices, before.key_indices)
+    again, _ = cyclic_module.cyclic_attn_doc_fwd(q, k, v, *meta, stride, -1, 64)
+    assert torch.ops.white_matter._cyclic_schedule_cache_size() == min(cached + 1, 256)
+    assert torch.equal(again, out)

@@ -18,6 +18,18 @@ from . import _native
 SUPPORTED_HEAD_DIMS = (64, 96, 128)
 
 
+def guard_capture(what: str) -> None:
+    """Raise before a host synchronisation or a schedule-cache build inside HIP
+    graph capture: such a step would break the capture (or record a copy from
+    host memory that is gone at replay). The call must run once eagerly on the
+    same metadata first, so everything a captured call needs is cached."""
+    if torch.cuda.is_initialized() and torch.cuda.is_current_stream_capturing():
+        raise RuntimeError(
+            f"{what} synchronises with the host, which HIP graph capture forbids; "
+            "run the same call once before capturing so its schedule is cached"
+        )
+
+
 def kernel_head_dim(dim: int) -> int | None:
     """Smallest kernel head_dim that holds ``dim`` (zero padding), or None."""
     for size in SUPPORTED_HEAD_DIMS:

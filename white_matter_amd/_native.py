@@ -17,6 +17,8 @@ from pathlib import Path
 import torch
 
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
+# the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
+OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
 ABI_VERSION = 4
 
 _c_i64_3 = ctypes.c_int64 * 3
@@ -249,6 +251,17 @@ def load() -> ctypes.CDLL:
     if lib.wmx_strict_meta_args_size() != ctypes.sizeof(StrictMetaArgs):
         raise RuntimeError("wmx_strict_meta_args layout differs between the library and the binding")
     return lib
+
+
+@functools.cache
+def load_ops() -> None:
+    """Register the C++ operators (white_matter::cyclic_attn_*) once; raise
+    RuntimeError if their library is absent (there is no other implementation)."""
+    if not OPS_LIBRARY.exists():
+        raise RuntimeError(
+            f"libwmx_torch.so not found at {OPS_LIBRARY}; build it with `python -c \"import __graft_entry__ as g; g.build()\"`"
+        )
+    torch.ops.load_library(str(OPS_LIBRARY))
 
 
 def _check(lib: ctypes.CDLL, rc: int, what: str) -> None:

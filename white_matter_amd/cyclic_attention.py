@@ -25,12 +25,11 @@ kernels, which evaluate the rule per pair.
 
 from __future__ import annotations
 
-import weakref
 from typing import Literal
 
 import torch
 
-from . import _kernels, portable
+from . import _kernels, _native, portable
 from .metadata import CyclicAttentionMetadata
 
 
@@ -94,60 +93,7 @@ def cyclic_attention(
     return cyclic_attn_doc_fwd(query, key, value, *metadata, query_stride, query_offset, 64)[0]
 
 
-# --------------------------------------------------------------- operators ----
-def _check_residue(K_stride: int, residue: int) -> None:
-    # residue -1 is the strict-past shift of residue 0
-    if not -1 <= residue < K_stride:
-        raise ValueError(f"cyclic residue must be in [-1, {K_stride}), got {residue}")
-
-
-def _check_documents(metadata, Q, K) -> None:
-    shapes = ((Q.shape[0], Q.shape[2]), (K.shape[0], K.shape[2])) * 2
-    if any(tuple(t.shape) != shape or t.device != Q.device for t, shape in zip(metadata, shapes)):
-        raise ValueError("document metadata shape/device does not match Q/K/V")
-
-
-def _documents(metadata, Q, K) -> tuple[torch.Tensor, ...] | None:
-    if metadata is None:
-        return None
-    _check_documents(metadata, Q, K)
-    return tuple(t.to(torch.int32).contiguous() for t in metadata)
-
-
-# packed schedules per metadata, keyed on the id of the query-document tensor
-# (checked against a weak reference, dropped when the tensor is freed)
-_PACKED: dict[int, dict] = {}
-
-
-def _packed_schedule(metadata, q_len: int, k_len: int, stride: int, offset: int):
-    """The varlen schedule equivalent to `metadata` at this stride and residue
-    offset (StrictCausalMetadata over Q rows b * Tq + i and K rows
-    b * Tk + slot), or None when the metadata is not run-structured; cached
-    while the four tensors are alive and unmodified."""
-    qseg = metadata[0]
-    entries = _PACKED.get(id(qseg))
-    if entries is None or entries["tensor"]() is not qseg:
-        entries = _PACKED[id(qseg)] = {"tensor": weakref.ref(qseg)}
-        weakref.finalize(qseg, _PACKED.pop, id(qseg), None)
-    key = (q_len, k_len, stride, offset)
-    entry = entries.get(key)
-    if entry is not None:
-        refs, versions, schedule = entry
-        if all(r() is t for r, t in zip(refs, metadata)) and versions == tuple(t._version for t in metadata):
-            return schedule
-    schedule = _build_packed_schedule(*metadata, q_len, k_len, stride, offset)
-    if schedule is not None and schedule != "empty":
-        from .strict_causal_attention import _schedule_facts
-
-        if _schedule_facts(schedule)[2] == 0:
-            # key rows other than the dummy slot repeat: dK/dV would accumulate
-            # every row with atomics; the document-mode kernels keep one key
-            # row per slot (dummy slots alone go through small accumulators)
-            schedule = None
-    entries[key] = (tuple(weakref.ref(t) for t in metadata), tuple(t._version for t in metadata), schedule)
-    return schedule
-
-
+# ------------------------------------------------------- packed schedule ----
 def _build_packed_schedule(qseg, kseg, qstart, kqend, q_len: int, k_len: int, stride: int, offset: int):
     """Segments of (row, document run): the run's valid queries (consecutive
     indices with one document id and start) and keys = the row's dummy slots,
@@ -245,117 +191,51 @@ def _build_packed_schedule(qseg, kseg, qstart, kqend, q_len: int, k_len: int, st
     )
 
 
-def _packed_visibility(schedule, q, k, stride: int, backward: bool) -> _kernels.Visibility:
-    from .strict_causal_attention import _schedule_flags, _varlen, _work_units
+# ------------------------------------------------- registered operators ----
+@torch.library.custom_op("white_matter::_cyclic_schedule", mutates_args=())
+def _cyclic_schedule(
+    qseg: torch.Tensor, kseg: torch.Tensor, qstart: torch.Tensor, kqend: torch.Tensor,
+    q_len: int, k_len: int, stride: int, offset: int,
+) -> list[torch.Tensor]:
+    """The kernel form of one residue call's document metadata, built when the
+    C++ operators (csrc/torch_ops.cpp) miss their schedule cache: a CPU int64
+    facts tensor {status, num_segments, max_queries, max_keys, segment_layout,
+    keys_unique, ds_elements} and, for status 2 (packed segments), the varlen
+    tensors query_indices, key_indices, cu_queries, cu_keys and the work lists
+    q_units, k_units, ds_offsets. Status 1: no query sees a key; status 0: the
+    metadata is not run-structured, or key rows other than the dummy slots
+    repeat (the document-mode kernels evaluate the rule per pair)."""
+    _kernels.guard_capture("packing cyclic document metadata")
+    schedule = _build_packed_schedule(qseg, kseg, qstart, kqend, q_len, k_len, stride, offset)
+
+    def facts(*values: int) -> torch.Tensor:
+        return torch.tensor(values + (0,) * (7 - len(values)), dtype=torch.int64)
+
+    if schedule is None:
+        return [facts(0)]
+    if schedule == "empty":
+        return [facts(1)]
+    from .strict_causal_attention import _keys_unique_code, _schedule_flags, _work_units
 
     max_q, max_k, flags = _schedule_flags(schedule)
-    units = _work_units(schedule, stride)
-    varlen = _varlen(
-        q, k, schedule.query_indices, schedule.key_indices, schedule.cu_queries, schedule.cu_keys, max_q, max_k, flags,
-        units[0], units[1], *(units[2:] if backward else (None, 0)),
-    )
-    return _kernels.Visibility(query_stride=stride, varlen=varlen)
+    unique = _keys_unique_code(flags)
+    if unique == 0:
+        # key rows other than the dummy slots repeat: dK/dV would accumulate
+        # every row with atomics; the document-mode kernels keep one key row
+        # per slot (dummy slots alone go through small accumulators)
+        return [facts(0)]
+    q_units, k_units, ds_offsets, ds_elements = _work_units(schedule, stride)
+    return [
+        facts(2, schedule.cu_queries.numel() - 1, max_q, max_k, flags & 15, unique, ds_elements),
+        schedule.query_indices, schedule.key_indices, schedule.cu_queries, schedule.cu_keys,
+        q_units, k_units, ds_offsets,
+    ]
 
 
-def _packed_forward(q, k, v, schedule, stride: int):
-    """Forward over the packed schedule: O (B, H, Tq, D) view of (B, Tq, H, D)
-    storage and LSE (+inf for queries outside every segment)."""
-    from .strict_causal_attention import _schedule_gaps
-
-    batch, heads, length, dim = q.shape
-    out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
-    lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
-    if schedule == "empty":
-        return out.zero_().transpose(1, 2), lse.fill_(float("inf"))
-    out_gaps, _, _ = _schedule_gaps(schedule, batch, length, heads, k.shape[2], k.shape[1])
-    if out_gaps.numel():
-        out.view(batch * length, heads * dim).index_fill_(0, out_gaps, 0)
-        # the same query rows of every head: (B*T) row r is query r % T of batch row r // T
-        unscheduled = torch.zeros(batch * length, device=q.device, dtype=torch.bool).index_fill_(0, out_gaps, True)
-        lse.masked_fill_(unscheduled.view(batch, 1, length), float("inf"))
-    _kernels.forward(q, k, v, out.transpose(1, 2), lse, dim**-0.5, _packed_visibility(schedule, q, k, stride, False))
-    return out.transpose(1, 2), lse
-
-
-def _packed_backward(q, k, v, o, lse, g, schedule, stride: int):
-    from .strict_causal_attention import _schedule_gaps
-
-    dim = q.shape[3]
-    dq = torch.empty(q.shape, device=q.device, dtype=torch.bfloat16)
-    dk = torch.empty(k.shape, device=q.device, dtype=torch.bfloat16)
-    dv = torch.empty(v.shape, device=q.device, dtype=torch.bfloat16)
-    if schedule == "empty":
-        return dq.zero_(), dk.zero_(), dv.zero_()
-    _, dq_gaps, dkv_gaps = _schedule_gaps(schedule, q.shape[0], q.shape[2], q.shape[1], k.shape[2], k.shape[1])
-    if dq_gaps.numel():
-        dq.view(-1, dim).index_fill_(0, dq_gaps, 0)
-    if dkv_gaps.numel():
-        dk.view(-1, dim).index_fill_(0, dkv_gaps, 0)
-        dv.view(-1, dim).index_fill_(0, dkv_gaps, 0)
-    _kernels.backward(q, k, v, o, lse, g, dq, dk, dv, dim**-0.5, _packed_visibility(schedule, q, k, stride, True))
-    return dq, dk, dv
-
-
-def _check_shapes(Q, K, V) -> None:
-    if Q.ndim != 4 or K.ndim != 4 or K.shape != V.shape or Q.shape[0] != K.shape[0] or Q.shape[3] != K.shape[3]:
-        raise ValueError("Q/K/V require matching batch/head_dim and K/V shapes")
-    if Q.shape[1] % K.shape[1]:
-        raise ValueError("Q/K/V require divisible query/KV heads")
-
-
-def _forward_impl(Q, K, V, metadata, K_stride, residue):
-    _check_residue(K_stride, residue)
-    _check_shapes(Q, K, V)
-    q = _kernels.operand(Q)
-    k, v = _kernels.operand(K), _kernels.operand(V)
-    batch, heads, length, dim = Q.shape
-    schedule = None
-    if metadata is not None:
-        _check_documents(metadata, Q, K)
-        schedule = _packed_schedule(metadata, length, K.shape[2], K_stride, residue)
-    if schedule is not None:
-        out, lse = _packed_forward(q, k, v, schedule, K_stride)
-    else:
-        out = torch.empty(batch, length, heads, dim, device=Q.device, dtype=torch.bfloat16).transpose(1, 2)
-        lse = torch.empty(batch, heads, length, device=Q.device, dtype=torch.float32)
-        vis = _kernels.Visibility(query_stride=K_stride, query_offset=residue, documents=_documents(metadata, Q, K))
-        _kernels.forward(q, k, v, out, lse, dim**-0.5, vis)
-    return out.to(Q.dtype) if Q.dtype != torch.bfloat16 else out, lse
-
-
-def _backward_impl(Q, K, V, metadata, Out, Lse, dOut, K_stride, residue):
-    _check_residue(K_stride, residue)
-    _check_shapes(Q, K, V)
-    if Out.shape != Q.shape or dOut.shape != Q.shape or Lse.shape != Q.shape[:3]:
-        raise ValueError("Out/dOut/Lse do not match Q")
-    q, k, v = _kernels.operand(Q), _kernels.operand(K), _kernels.operand(V)
-    o, g = _kernels.operand(Out), _kernels.operand(dOut)
-    schedule = None
-    if metadata is not None:
-        _check_documents(metadata, Q, K)
-        schedule = _packed_schedule(metadata, Q.shape[2], K.shape[2], K_stride, residue)
-    if schedule is not None:
-        grads = _packed_backward(q, k, v, o, Lse.contiguous(), g, schedule, K_stride)
-    else:
-        grads = tuple(torch.empty(t.shape, device=Q.device, dtype=torch.bfloat16) for t in (Q, K, V))
-        vis = _kernels.Visibility(query_stride=K_stride, query_offset=residue, documents=_documents(metadata, Q, K))
-        _kernels.backward(q, k, v, o, Lse.contiguous(), g, *grads, Q.shape[-1] ** -0.5, vis)
-    return tuple(t.to(Q.dtype) if Q.dtype != torch.bfloat16 else t for t in grads)
-
-
-@torch.library.custom_op("white_matter::cyclic_attn_fwd", mutates_args=())
-def cyclic_attn_fwd(
-    Q: torch.Tensor,
-    K: torch.Tensor,
-    V: torch.Tensor,
-    K_stride: int,
-    residue: int,
-    block_M: int,
-) -> tuple[torch.Tensor, torch.Tensor]:
-    """(O, LSE) of cyclic attention; O is a (B, H, Tq, D) view of (B, Tq, H, D)
-    storage, LSE the fp32 natural-log row normaliser (+inf for empty rows).
-    ``block_M`` is accepted for schema compatibility; tiles are fixed per D."""
-    return _forward_impl(Q, K, V, None, K_stride, residue)
+# The four cyclic operators are registered from C++ (libwmx_torch.so,
+# csrc/torch_ops.cpp): same names, argument names and output layouts as the
+# reference's torch.library registrations; their fakes are registered here.
+_native.load_ops()
 
 
 def _fake_fwd(Q: torch.Tensor, *_: object, **__: object) -> tuple[torch.Tensor, torch.Tensor]:
@@ -363,25 +243,6 @@ def _fake_fwd(Q: torch.Tensor, *_: object, **__: object) -> tuple[torch.Tensor, 
     out = torch.empty((batch, length, heads, dim), dtype=Q.dtype, device=Q.device).transpose(1, 2)
     lse = torch.empty((batch, heads, length), dtype=torch.float32, device=Q.device)
     return out, lse
-
-
-cyclic_attn_fwd.register_fake(_fake_fwd)
-
-
-@torch.library.custom_op("white_matter::cyclic_attn_bwd", mutates_args=())
-def cyclic_attn_bwd(
-    Q: torch.Tensor,
-    K: torch.Tensor,
-    V: torch.Tensor,
-    Out: torch.Tensor,
-    Lse: torch.Tensor,
-    dOut: torch.Tensor,
-    K_stride: int,
-    residue: int,
-    block_M: int,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """(dQ, dK, dV), contiguous in Q's dtype."""
-    return _backward_impl(Q, K, V, None, Out, Lse, dOut, K_stride, residue)
 
 
 def _fake_bwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, *_: object, **__: object):
@@ -393,68 +254,15 @@ def _fake_bwd(Q: torch.Tensor, K: torch.Tensor, V: torch.Tensor, *_: object, **_
     )
 
 
-cyclic_attn_bwd.register_fake(_fake_bwd)
+for _name, _fake in (
+    ("cyclic_attn_fwd", _fake_fwd),
+    ("cyclic_attn_bwd", _fake_bwd),
+    ("cyclic_attn_doc_fwd", _fake_fwd),
+    ("cyclic_attn_doc_bwd", _fake_bwd),
+):
+    torch.library.register_fake(f"white_matter::{_name}", _fake)
 
-
-@torch.library.custom_op("white_matter::cyclic_attn_doc_fwd", mutates_args=())
-def cyclic_attn_doc_fwd(
-    Q: torch.Tensor,
-    K: torch.Tensor,
-    V: torch.Tensor,
-    QSeg: torch.Tensor,
-    KSeg: torch.Tensor,
-    QStart: torch.Tensor,
-    KQEnd: torch.Tensor,
-    K_stride: int,
-    residue: int,
-    block_M: int,
-) -> tuple[torch.Tensor, torch.Tensor]:
-    """cyclic_attn_fwd with the document rule of CyclicAttentionMetadata."""
-    return _forward_impl(Q, K, V, (QSeg, KSeg, QStart, KQEnd), K_stride, residue)
-
-
-cyclic_attn_doc_fwd.register_fake(_fake_fwd)
-
-
-@torch.library.custom_op("white_matter::cyclic_attn_doc_bwd", mutates_args=())
-def cyclic_attn_doc_bwd(
-    Q: torch.Tensor,
-    K: torch.Tensor,
-    V: torch.Tensor,
-    QSeg: torch.Tensor,
-    KSeg: torch.Tensor,
-    QStart: torch.Tensor,
-    KQEnd: torch.Tensor,
-    Out: torch.Tensor,
-    Lse: torch.Tensor,
-    dOut: torch.Tensor,
-    K_stride: int,
-    residue: int,
-    block_M: int,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    return _backward_impl(Q, K, V, (QSeg, KSeg, QStart, KQEnd), Out, Lse, dOut, K_stride, residue)
-
-
-cyclic_attn_doc_bwd.register_fake(_fake_bwd)
-
-
-def _setup_ctx(ctx, inputs, output):
-    *tensors, ctx.K_stride, ctx.residue, ctx.block_M = inputs
-    ctx.save_for_backward(*tensors, *output)
-    ctx.set_materialize_grads(False)  # Lse has no gradient: no zero fill for it
-
-
-def _backward(ctx, dOut, dLse):
-    tensors = ctx.saved_tensors
-    if dOut is None:
-        dOut = torch.zeros_like(tensors[-2])
-    # Q/K/V, optionally four document tensors, then O and LSE
-    if len(tensors) == 9:
-        grads = cyclic_attn_doc_bwd(*tensors, dOut, ctx.K_stride, ctx.residue, ctx.block_M)
-    else:
-        grads = cyclic_attn_bwd(*tensors, dOut, ctx.K_stride, ctx.residue, ctx.block_M)
-    return (*grads, *((None,) * (len(tensors) - 2)))
-
-
-cyclic_attn_fwd.register_autograd(_backward, setup_context=_setup_ctx)
-cyclic_attn_doc_fwd.register_autograd(_backward, setup_context=_setup_ctx)
+cyclic_attn_fwd = torch.ops.white_matter.cyclic_attn_fwd
+cyclic_attn_bwd = torch.ops.white_matter.cyclic_attn_bwd
+cyclic_attn_doc_fwd = torch.ops.white_matter.cyclic_attn_doc_fwd
+cyclic_attn_doc_bwd = torch.ops.white_matter.cyclic_attn_doc_bwd

@@ -112,6 +112,7 @@ def prepare_strict_causal_metadata(
     (wmx_strict_meta_count / _fill): one host synchronisation, to size the
     outputs. Elsewhere the same steps run as torch operations.
     """
+    _kernels.guard_capture("prepare_strict_causal_metadata")
     if document_ids.is_cuda and not document_ids.is_floating_point() and document_ids.dtype != torch.bool:
         return _device_schedule(document_ids, query_length, query_start, kv_lengths, use_dummy_token)
     return _torch_schedule(document_ids, query_length, query_start, kv_lengths, use_dummy_token)
@@ -285,6 +286,7 @@ def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, int, int,
     whether query rows repeat."""
     facts = getattr(metadata, "_facts", None)
     if facts is None:
+        _kernels.guard_capture("deriving the facts of a packed-document schedule")
         segments = metadata.segments
         max_q = max((qe - qs for qs, qe, _, _ in segments), default=0)
         max_k = max((ke - ks for _, _, ks, ke in segments), default=0)
@@ -459,6 +461,7 @@ def _schedule_gaps(
     key = (batch, length, heads, key_extent, kv_heads)
     gaps = cache.get(key)
     if gaps is None:
+        _kernels.guard_capture("finding the rows a packed-document schedule leaves out")
         facts = _schedule_facts(metadata)
         unique_k, unique_q = facts[2], facts[6]
         device = metadata.query_indices.device
@@ -510,6 +513,7 @@ def _covering_schedule(metadata: StrictCausalMetadata, batch: int, length: int, 
     shape = (batch, length, key_extent)
     cover = cache.get(shape)
     if cover is None:
+        _kernels.guard_capture("covering a packed-document schedule")
         device = metadata.query_indices.device
         seen_q = torch.zeros(batch * length, dtype=torch.bool, device=device)
         seen_q[metadata.query_indices] = True
@@ -552,6 +556,7 @@ def _work_units(
     by_stride = metadata.__dict__.setdefault("_units", {})
     units = by_stride.get(stride)
     if units is None:
+        _kernels.guard_capture("building the work lists of a packed-document schedule")
         q_units, k_units, ds_blocks = [], [], []
         for s, (qs, qe, ks, ke) in enumerate(metadata.segments):
             nq, nk = qe - qs, ke - ks

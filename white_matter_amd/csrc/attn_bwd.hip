@@ -642,13 +642,35 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     rrd.refresh();
 #pragma unroll
     for (int mb = 0; mb < BMQ / 32; ++mb) tacc[mb] = f32x16{};
-    // k-step major: the two halves' operand reads interleave
+    // k-step major, each operand read PF k-steps ahead of its product (the
+    // scheduling barriers keep the compiler from sinking the reads next to
+    // their uses, where every product would wait out the LDS latency)
+    constexpr int PF = KS < 4 ? KS : 4;
+    bf16x8 op[KS][BMQ / 32];
+#pragma unroll
+    for (int s = 0; s < PF; ++s) {
+#pragma unroll
+      for (int mb = 0; mb < BMQ / 32; ++mb) op[s][mb] = rrd.get(rows, s, mb);
+    }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + PF < KS) {
 #pragma unroll
-      for (int mb = 0; mb < BMQ / 32; ++mb) tacc[mb] = mfma32(rrd.get(rows, s, mb), kvf[s], tacc[mb]);
+        for (int mb = 0; mb < BMQ / 32; ++mb) op[s + PF][mb] = rrd.get(rows, s + PF, mb);
+      }
+#pragma unroll
+      for (int mb = 0; mb < BMQ / 32; ++mb) tacc[mb] = mfma32(op[s][mb], kvf[s], tacc[mb]);
     }
+    __builtin_amdgcn_sched_barrier(0);
     if constexpr (DP) return;
+    // the rows' lse, read while the products drain
+    f32x4 l4s[BMQ / 32][4];
+#pragma unroll
+    for (int mb = 0; mb < BMQ / 32; ++mb) {
+#pragma unroll
+      for (int g = 0; g < 4; ++g) l4s[mb][g] = *reinterpret_cast<const f32x4*>(&stat_lds[B][0][mb * 32 + 8 * g + 4 * half]);
+    }
     // every pair of the tile is visible to this pair's keys: no per-element mask
     const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= pair_m_begin &&
                       m0 + BMQ <= nq && pb.bound.lim(m0) >= pair_key0 + 31;
@@ -682,8 +704,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       }
 #pragma unroll
       for (int g = 0; g < 4; ++g) {
-        const int ml = mb * 32 + 8 * g + 4 * half;
-        const f32x4 l4 = *reinterpret_cast<const f32x4*>(&stat_lds[B][0][ml]);
+        const f32x4 l4 = l4s[mb][g];
         f32x4 p4;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
@@ -699,24 +720,41 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     constexpr int B = decltype(bufc)::value;
     constexpr bool DP = decltype(sidec)::value;
     trd.refresh();
-    if constexpr (DP) {
-#pragma unroll
-      for (int mb = 0; mb < BMQ / 32; ++mb) {
-#pragma unroll
-        for (int g = 0; g < 4; ++g) {
-          const int ml = mb * 32 + 8 * g + 4 * half;
-          const f32x4 d4 = *reinterpret_cast<const f32x4*>(&stat_lds[B][1][ml]);
-          const f32x4 p4 = p_lds[pair][mb][g][lane];
-#pragma unroll
-          for (int e = 0; e < 4; ++e) tacc[mb][4 * g + e] = p4[e] * (tacc[mb][4 * g + e] - d4[e]);
-        }
-      }
-    }
     const bf16* tr = DP ? (B ? q_lds1 : q_lds0) : (B ? g_lds1 : g_lds0);  // Q^T for dK, dO^T for dV
+    // transposed operands one k-step ahead of their products
+    bf16x8 top[BMQ / 16][DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) top[0][d] = trd.get(tr, d, 0);
+    // dP side: dS = P (dP - delta) per k-step (its two register quads), P and
+    // delta read one k-step ahead
+    f32x4 d4s[BMQ / 16][2], p4s[BMQ / 16][2];
+    auto read_pd = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int g = 2 * (s & 1) + q, mb = s >> 1;
+        d4s[s][q] = *reinterpret_cast<const f32x4*>(&stat_lds[B][1][mb * 32 + 8 * g + 4 * half]);
+        p4s[s][q] = p_lds[pair][mb][g][lane];
+      }
+    };
+    if constexpr (DP) read_pd(0);
     bf16* ds_row = nullptr;
     if constexpr (DP && DS) ds_row = ds_key + hq * ds_head + m0;
 #pragma unroll
     for (int s = 0; s < BMQ / 16; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < BMQ / 16) {
+        if constexpr (DP) read_pd(s + 1);
+#pragma unroll
+        for (int d = 0; d < DB; ++d) top[s + 1][d] = trd.get(tr, d, s + 1);
+      }
+      if constexpr (DP) {
+#pragma unroll
+        for (int q = 0; q < 2; ++q) {
+          const int g = 2 * (s & 1) + q, mb = s >> 1;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) tacc[mb][4 * g + e] = p4s[s][q][e] * (tacc[mb][4 * g + e] - d4s[s][q][e]);
+        }
+      }
       const bf16x8 op = acc_kperm_operand(tacc[s >> 1], s);
       if constexpr (DP && DS) {
         // operand element e is query m0 + 16 s + 8 (e / 4) + 4 half + e % 4;
@@ -728,8 +766,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
         if (valid_k) *reinterpret_cast<u32x4*>(ds_row + 16 * s) = u32x4{lo[0], hi[0], lo[1], hi[1]};
       }
 #pragma unroll
-      for (int d = 0; d < DB; ++d) acc[d] = mfma32(trd.get(tr, d, s), op, acc[d]);
+      for (int d = 0; d < DB; ++d) acc[d] = mfma32(top[s][d], op, acc[d]);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // iteration `it` works on buffer B and prefetches iteration it + 1
@@ -741,8 +780,9 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       ++hq;
     }
   };
-  auto iteration = [&](auto bufc, int it) __attribute__((always_inline)) {
+  auto iteration = [&](auto bufc, auto sidec, int it) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
+    constexpr bool DP = decltype(sidec)::value;
     const int m0 = m_cur;
     int hn = hq_cur, mn = m0;
     advance(hn, mn);
@@ -750,7 +790,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     // every dP-side wave has taken the previous P. A dP-side wave that stored
     // dS in the previous step issued its 4 stores after this tile's loads:
     // those may still be in flight.
-    if (DS && dp_side && pair_live && it > 0) {
+    if (DS && DP && pair_live && it > 0) {
       lds_sync<4>();
     } else {
       lds_sync<0>();
@@ -761,26 +801,14 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       issue_meta(std::integral_constant<int, B ^ 1>{}, hn, mn);
     }
     const bool active = pair_live && m0 + BMQ > pair_m_begin;  // uniform over the pair
-    using S_side = std::integral_constant<bool, false>;
-    using DP_side = std::integral_constant<bool, true>;
-    if (active) {
-      if (dp_side) {
-        first_half(bufc, DP_side{}, m0);
-      } else {
-        first_half(bufc, S_side{}, m0);
-      }
-    }
+    if (active) first_half(bufc, sidec, m0);
     lds_barrier();  // P of this tile is in LDS
     if (active) {
-      if (dp_side) {
-        second_half(bufc, DP_side{}, hq_cur, m0);
-      } else {
-        second_half(bufc, S_side{}, hq_cur, m0);
-      }
-    } else if constexpr (DS) {
+      second_half(bufc, sidec, hq_cur, m0);
+    } else if constexpr (DS && DP) {
       // the dQ kernel reads every key row of a visited tile: zeros for a
       // pair that sees none of its rows
-      if (dp_side && valid_k) {
+      if (valid_k) {
         bf16* row = ds_key + hq_cur * ds_head + m0;
 #pragma unroll
         for (int s = 0; s < BMQ / 16; ++s) *reinterpret_cast<u32x4*>(row + 16 * s) = u32x4{0u, 0u, 0u, 0u};
@@ -794,9 +822,18 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     qrows.issue(a, pb, dma, hq_cur, m_cur, q_lds0, g_lds0);
     issue_meta(std::integral_constant<int, 0>{}, hq_cur, m_cur);
   }
-  for (int it = 0; it < total; it += 2) {
-    iteration(std::integral_constant<int, 0>{}, it);
-    if (it + 1 < total) iteration(std::integral_constant<int, 1>{}, it + 1);
+  // one copy of the tile loop per role, so that no role branch sits inside it
+  // (a branch there makes the compiler copy the accumulators at every merge)
+  auto run = [&](auto sidec) __attribute__((always_inline)) {
+    for (int it = 0; it < total; it += 2) {
+      iteration(std::integral_constant<int, 0>{}, sidec, it);
+      if (it + 1 < total) iteration(std::integral_constant<int, 1>{}, sidec, it + 1);
+    }
+  };
+  if (dp_side) {
+    run(std::integral_constant<bool, true>{});
+  } else {
+    run(std::integral_constant<bool, false>{});
   }
 
   if (!valid_k) return;

@@ -387,9 +387,20 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
   auto tile_step = [&](int n0, int buf, const bf16* kt, const bf16* st) __attribute__((always_inline)) {
     trd.refresh();
     srd.refresh();
+    // operands one k-step ahead of their products
+    bf16x8 sop[BN / 16], kop[BN / 16][DB];
+    sop[0] = srd.get(st, 0, 0);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) kop[0][d] = trd.get(kt, d, 0);
 #pragma unroll
     for (int s = 0; s < BN / 16; ++s) {
-      bf16x8 op = srd.get(st, 0, s);
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < BN / 16) {
+        sop[s + 1] = srd.get(st, 0, s + 1);
+#pragma unroll
+        for (int d = 0; d < DB; ++d) kop[s + 1][d] = trd.get(kt, d, s + 1);
+      }
+      bf16x8 op = sop[s];
       if constexpr (MODE == kDoc) {
         // element e is key n0 + 16 s + 8 (e / 4) + 4 half + e % 4
         u32x4 w = __builtin_bit_cast(u32x4, op);
@@ -406,8 +417,9 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
         op = as_bf16x8(w);
       }
 #pragma unroll
-      for (int d = 0; d < DB; ++d) dqacc[d] = mfma32(trd.get(kt, d, s), op, dqacc[d]);
+      for (int d = 0; d < DB; ++d) dqacc[d] = mfma32(kop[s][d], op, dqacc[d]);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   auto iteration = [&](auto bufc, int it) __attribute__((always_inline)) {

@@ -182,13 +182,27 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void attn_fwd_kernel(cons
     f32x16 sacc[BN / 32];
 #pragma unroll
     for (int nb = 0; nb < BN / 32; ++nb) sacc[nb] = f32x16{};
-    // k-step major: the two blocks' operand reads interleave, so each read
-    // has the other block's product to hide behind
+    // k-step major, each operand read PF k-steps ahead of its product (the
+    // scheduling barriers keep the compiler from sinking the reads next to
+    // their uses, where every product would wait out the LDS latency)
+    constexpr int PF = KS < 4 ? KS : 4;
+    bf16x8 kop[KS][BN / 32];
+#pragma unroll
+    for (int s = 0; s < PF; ++s) {
+#pragma unroll
+      for (int nb = 0; nb < BN / 32; ++nb) kop[s][nb] = krd.get(kt, s, nb);
+    }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + PF < KS) {
 #pragma unroll
-      for (int nb = 0; nb < BN / 32; ++nb) sacc[nb] = mfma32(krd.get(kt, s, nb), qf[s], sacc[nb]);
+        for (int nb = 0; nb < BN / 32; ++nb) kop[s + PF][nb] = krd.get(kt, s + PF, nb);
+      }
+#pragma unroll
+      for (int nb = 0; nb < BN / 32; ++nb) sacc[nb] = mfma32(kop[s][nb], qf[s], sacc[nb]);
     }
+    __builtin_amdgcn_sched_barrier(0);
 
     if (masked) {
       // keeps this block a real (wave-uniform) branch instead of selects
@@ -247,12 +261,22 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void attn_fwd_kernel(cons
       for (int d = 0; d < DB; ++d) oacc[d] *= alpha;
     }
 
+    // V^T operands one k-step ahead of their products
+    bf16x8 vop[BN / 16][DB];
+#pragma unroll
+    for (int d = 0; d < DB; ++d) vop[0][d] = vrd.get(vt, d, 0);
 #pragma unroll
     for (int s = 0; s < BN / 16; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < BN / 16) {
+#pragma unroll
+        for (int d = 0; d < DB; ++d) vop[s + 1][d] = vrd.get(vt, d, s + 1);
+      }
       const bf16x8 pb = acc_kperm_operand(sacc[s >> 1], s);
 #pragma unroll
-      for (int d = 0; d < DB; ++d) oacc[d] = mfma32(vrd.get(vt, d, s), pb, oacc[d]);
+      for (int d = 0; d < DB; ++d) oacc[d] = mfma32(vop[s][d], pb, oacc[d]);
     }
+    __builtin_amdgcn_sched_barrier(0);
   };
 
   // One iteration of the tile loop on buffer B (tile `it` resident there),

@@ -656,7 +656,7 @@ def metadata_line(device, batch=8, length=2048, reps=20):
     (returns with the host segment list), through the HIP builder, through the
     reference's torch sequence on the same GPU, and that sequence on the host
     CPU (the reference's CPU path)."""
-    from white_matter_amd import prepare_strict_causal_metadata
+    from white_matter_amd import prepare_feedback_metadata, prepare_strict_causal_metadata
     from white_matter_amd.strict_causal_attention import _torch_schedule
 
     docs = geometric_documents(batch, length, 0)
@@ -674,12 +674,23 @@ def metadata_line(device, batch=8, length=2048, reps=20):
     hip_ms = wall(lambda: prepare_strict_causal_metadata(on_gpu, length), reps)
     torch_ms = wall(lambda: _torch_schedule(on_gpu, length, 0, None, False), reps)
     cpu_ms = wall(lambda: _torch_schedule(docs, length, 0, None, False), 5)
+    # the model's per-forward cyclic metadata at the default stride 8, every residue
+    stride = 8
+    slots_cpu = [torch.arange(r, length, stride) for r in range(stride)]
+    slots_gpu = [p.to(device) for p in slots_cpu]
+    feedback_hip = wall(lambda: prepare_feedback_metadata(on_gpu, slots_gpu, length + 1), reps)
+    feedback_cpu = wall(lambda: prepare_feedback_metadata(docs, slots_cpu, length + 1), 5)
     return {
         "workload": f"prepare_strict_causal_metadata, C2 documents B={batch} T={length}, host segment list included",
         "hip_ms": round(hip_ms, 4),
         "torch_on_gpu_ms": round(torch_ms, 4),
         "torch_on_cpu_ms": round(cpu_ms, 4),
         "cpu_threads": torch.get_num_threads(),
+        "feedback": {
+            "workload": f"prepare_feedback_metadata, same documents, stride {stride} (all residues), dummy slot",
+            "hip_ms": round(feedback_hip, 4),
+            "cpu_ms": round(feedback_cpu, 4),
+        },
     }
 
 

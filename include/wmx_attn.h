@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 4
+#define WMX_ABI_VERSION 5
 
 enum {
   WMX_OK = 0,
@@ -277,12 +277,52 @@ typedef struct wmx_strict_meta_args {
   int32_t use_dummy;          /* 0 or 1 */
 } wmx_strict_meta_args;
 
+/*
+ * Per-residue cyclic metadata of packed documents on the device: replaces the
+ * reference's prepare_feedback_metadata (blocks/_execution/metadata.py:11-55),
+ * its torch sequence (cummax / flipped cummin run bounds, index_select, div)
+ * issued once per residue. One kernel, one workgroup per batch row, no host
+ * synchronisation. For the groups r = group_base .. group_base + group_count - 1
+ * of G = groups (the model's query tokens r, r + G, ...; any slots here), with
+ * d = use_dummy and runs = maximal sequences of equal ids in a row:
+ *   key_ids[b, j]                -1 for j < d, else id(token j - d), negative as -2
+ *   key_query_end[g, b, j]       count_g for j < d, else
+ *                                min(ceil(max(run_end(j - d) - r, 0) / G), count_g)
+ *   query_ids[B*o_g + b*count_g + i]        id(slots[o_g + i]), negative as -2
+ *   query_key_start[B*o_g + b*count_g + i]  run_start(slots[o_g + i]) + d
+ * with o_g = group_offsets[g], count_g = o_{g+1} - o_g (group g's outputs are a
+ * contiguous (B, count_g) block). Slots outside [0, length) give -2 and 0.
+ */
+#define WMX_FEEDBACK_MAX_GROUPS 64
+
+typedef struct wmx_feedback_meta_args {
+  const void* document_ids;   /* (B, length) of doc_dtype, rows doc_stride elements apart */
+  const int64_t* slots;       /* the groups' query slots, group g at [group_offsets[g], group_offsets[g+1]) */
+  void* workspace;            /* wmx_feedback_meta_workspace_size bytes (per-token run bounds) */
+  int32_t* key_ids;           /* (B, key_length) */
+  int32_t* key_query_end;     /* (group_count, B, key_length) */
+  int32_t* query_ids;         /* B * group_offsets[group_count] */
+  int32_t* query_key_start;   /* B * group_offsets[group_count] */
+  int64_t doc_stride;
+  int64_t workspace_bytes;
+  int64_t group_offsets[WMX_FEEDBACK_MAX_GROUPS + 1]; /* group_offsets[0] = 0, nondecreasing */
+  int32_t doc_dtype;          /* WMX_DTYPE_I32 or WMX_DTYPE_I64 */
+  int32_t batch;
+  int32_t length;
+  int32_t key_length;         /* <= length + use_dummy */
+  int32_t groups;             /* G >= 1: the cyclic stride */
+  int32_t group_base;         /* residue of this call's first group */
+  int32_t group_count;        /* 1 .. WMX_FEEDBACK_MAX_GROUPS */
+  int32_t use_dummy;          /* 0 or 1 */
+} wmx_feedback_meta_args;
+
 /* Library identity and struct layout checks for FFI bindings. */
 int wmx_abi_version(void);
 size_t wmx_attn_args_size(void);
 size_t wmx_decode_args_size(void);
 size_t wmx_kv_store_args_size(void);
 size_t wmx_strict_meta_args_size(void);
+size_t wmx_feedback_meta_args_size(void);
 const char* wmx_last_error(void);
 
 /* Forward: o and lse. (see replaced interfaces above) */
@@ -352,6 +392,12 @@ int wmx_kv_pool_store(const wmx_kv_store_args* args, void* stream);
 int64_t wmx_strict_meta_workspace_size(const wmx_strict_meta_args* args);
 int wmx_strict_meta_count(const wmx_strict_meta_args* args, void* stream);
 int wmx_strict_meta_fill(const wmx_strict_meta_args* args, void* stream);
+
+/* Per-residue cyclic metadata (see wmx_feedback_meta_args): replaces the torch
+ * sequence of prepare_feedback_metadata (reference
+ * blocks/_execution/metadata.py:11-55). */
+int64_t wmx_feedback_meta_workspace_size(const wmx_feedback_meta_args* args);
+int wmx_feedback_meta(const wmx_feedback_meta_args* args, void* stream);
 
 #ifdef __cplusplus
 }

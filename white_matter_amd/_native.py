@@ -19,7 +19,7 @@ import torch
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
 # the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
 OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -177,6 +177,34 @@ class StrictMetaArgs(ctypes.Structure):
     ]
 
 
+FEEDBACK_MAX_GROUPS = 64
+
+
+class FeedbackMetaArgs(ctypes.Structure):
+    """Mirror of wmx_feedback_meta_args."""
+
+    _fields_ = [
+        ("document_ids", _vp),
+        ("slots", _vp),
+        ("workspace", _vp),
+        ("key_ids", _vp),
+        ("key_query_end", _vp),
+        ("query_ids", _vp),
+        ("query_key_start", _vp),
+        ("doc_stride", ctypes.c_int64),
+        ("workspace_bytes", ctypes.c_int64),
+        ("group_offsets", ctypes.c_int64 * (FEEDBACK_MAX_GROUPS + 1)),
+        ("doc_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("length", ctypes.c_int32),
+        ("key_length", ctypes.c_int32),
+        ("groups", ctypes.c_int32),
+        ("group_base", ctypes.c_int32),
+        ("group_count", ctypes.c_int32),
+        ("use_dummy", ctypes.c_int32),
+    ]
+
+
 EXPORTS = (
     "wmx_abi_version",
     "wmx_attn_args_size",
@@ -199,6 +227,9 @@ EXPORTS = (
     "wmx_strict_meta_workspace_size",
     "wmx_strict_meta_count",
     "wmx_strict_meta_fill",
+    "wmx_feedback_meta_args_size",
+    "wmx_feedback_meta_workspace_size",
+    "wmx_feedback_meta",
 )
 
 
@@ -240,6 +271,11 @@ def load() -> ctypes.CDLL:
     for name in ("wmx_strict_meta_count", "wmx_strict_meta_fill"):
         getattr(lib, name).argtypes = [ctypes.POINTER(StrictMetaArgs), _vp]
         getattr(lib, name).restype = ctypes.c_int
+    lib.wmx_feedback_meta_args_size.restype = ctypes.c_size_t
+    lib.wmx_feedback_meta_workspace_size.argtypes = [ctypes.POINTER(FeedbackMetaArgs)]
+    lib.wmx_feedback_meta_workspace_size.restype = ctypes.c_int64
+    lib.wmx_feedback_meta.argtypes = [ctypes.POINTER(FeedbackMetaArgs), _vp]
+    lib.wmx_feedback_meta.restype = ctypes.c_int
     if lib.wmx_abi_version() != ABI_VERSION:
         raise RuntimeError(f"{path} has ABI {lib.wmx_abi_version()}, expected {ABI_VERSION}")
     if lib.wmx_attn_args_size() != ctypes.sizeof(AttnArgs):
@@ -248,6 +284,8 @@ def load() -> ctypes.CDLL:
         raise RuntimeError("wmx_decode_args layout differs between the library and the binding")
     if lib.wmx_kv_store_args_size() != ctypes.sizeof(KvStoreArgs):
         raise RuntimeError("wmx_kv_store_args layout differs between the library and the binding")
+    if lib.wmx_feedback_meta_args_size() != ctypes.sizeof(FeedbackMetaArgs):
+        raise RuntimeError("wmx_feedback_meta_args layout differs between the library and the binding")
     if lib.wmx_strict_meta_args_size() != ctypes.sizeof(StrictMetaArgs):
         raise RuntimeError("wmx_strict_meta_args layout differs between the library and the binding")
     return lib
@@ -352,3 +390,12 @@ def strict_meta_count(args: StrictMetaArgs, device: torch.device) -> None:
 def strict_meta_fill(args: StrictMetaArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_strict_meta_fill(ctypes.byref(args), _stream(device)), "wmx_strict_meta_fill")
+
+
+def feedback_meta_workspace_size(args: FeedbackMetaArgs) -> int:
+    return int(load().wmx_feedback_meta_workspace_size(ctypes.byref(args)))
+
+
+def feedback_meta(args: FeedbackMetaArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_feedback_meta(ctypes.byref(args), _stream(device)), "wmx_feedback_meta")

@@ -168,6 +168,36 @@ int check_strict_meta(const wmx_strict_meta_args* a, bool fill) {
   return WMX_OK;
 }
 
+int check_feedback_meta(const wmx_feedback_meta_args* a) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->batch < 0 || a->length < 0 || a->key_length < 0) return fail(WMX_E_INVALID, "negative shape");
+  if (a->use_dummy != 0 && a->use_dummy != 1) return fail(WMX_E_INVALID, "use_dummy must be 0 or 1");
+  if (a->doc_dtype != WMX_DTYPE_I32 && a->doc_dtype != WMX_DTYPE_I64)
+    return fail(WMX_E_INVALID, "document_ids must be WMX_DTYPE_I32 or WMX_DTYPE_I64");
+  if ((int64_t)a->key_length > (int64_t)a->length + a->use_dummy)
+    return fail(WMX_E_INVALID, "key_length %d exceeds the dummy-shifted extent %d", a->key_length,
+                a->length + a->use_dummy);
+  if (a->groups < 1) return fail(WMX_E_INVALID, "groups must be >= 1");
+  if (a->group_count < 1 || a->group_count > WMX_FEEDBACK_MAX_GROUPS)
+    return fail(WMX_E_INVALID, "group_count must be in [1, %d]", WMX_FEEDBACK_MAX_GROUPS);
+  if (a->group_base < 0 || (int64_t)a->group_base + a->group_count > a->groups)
+    return fail(WMX_E_INVALID, "groups [group_base, group_base + group_count) must lie in [0, groups)");
+  if (a->group_offsets[0] != 0) return fail(WMX_E_INVALID, "group_offsets[0] must be 0");
+  for (int g = 0; g < a->group_count; ++g)
+    if (a->group_offsets[g + 1] < a->group_offsets[g]) return fail(WMX_E_INVALID, "group_offsets must be nondecreasing");
+  if (a->batch == 0) return WMX_OK;
+  if (a->length > 0 && (!a->document_ids || a->doc_stride < a->length))
+    return fail(WMX_E_INVALID, "document_ids is NULL or doc_stride is smaller than length");
+  if (a->key_length > 0 && (!a->key_ids || !a->key_query_end))
+    return fail(WMX_E_INVALID, "key_ids/key_query_end pointer is NULL");
+  if (a->group_offsets[a->group_count] > 0 && (!a->slots || !a->query_ids || !a->query_key_start))
+    return fail(WMX_E_INVALID, "slots/query_ids/query_key_start pointer is NULL");
+  const int64_t need = wmx::feedback_meta_workspace_size(*a);
+  if (need > 0 && (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace)))
+    return fail(WMX_E_WORKSPACE, "feedback metadata needs %lld workspace bytes", (long long)need);
+  return WMX_OK;
+}
+
 }  // namespace
 
 extern "C" {
@@ -264,6 +294,17 @@ int wmx_strict_meta_count(const wmx_strict_meta_args* a, void* stream) {
 int wmx_strict_meta_fill(const wmx_strict_meta_args* a, void* stream) {
   if (const int rc = check_strict_meta(a, true)) return rc;
   return launched(wmx::launch_strict_meta(*a, true, (hipStream_t)stream));
+}
+
+size_t wmx_feedback_meta_args_size(void) { return sizeof(wmx_feedback_meta_args); }
+
+int64_t wmx_feedback_meta_workspace_size(const wmx_feedback_meta_args* args) {
+  return args ? wmx::feedback_meta_workspace_size(*args) : 0;
+}
+
+int wmx_feedback_meta(const wmx_feedback_meta_args* a, void* stream) {
+  if (const int rc = check_feedback_meta(a)) return rc;
+  return launched(wmx::launch_feedback_meta(*a, (hipStream_t)stream));
 }
 
 int64_t wmx_decode_workspace_size(const wmx_decode_args* args) {

@@ -46,5 +46,7 @@ int launch_decode(const wmx_decode_args& a, hipStream_t stream);
 int launch_kv_store(const wmx_kv_store_args& a, hipStream_t stream);
 int64_t strict_meta_workspace_size(const wmx_strict_meta_args& a);
 int launch_strict_meta(const wmx_strict_meta_args& a, bool fill, hipStream_t stream);
+int64_t feedback_meta_workspace_size(const wmx_feedback_meta_args& a);
+int launch_feedback_meta(const wmx_feedback_meta_args& a, hipStream_t stream);
 
 }  // namespace wmx

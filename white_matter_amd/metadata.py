@@ -77,25 +77,29 @@ def prepare_cyclic_attention_metadata(
     return CyclicAttentionMetadata(queries, keys, query_key_start, key_query_end)
 
 
-def document_start_mask(document_ids: torch.Tensor) -> torch.Tensor:
-    """True at each row's first token and wherever the id changes
-    (reference src/white_matter/modules/documents.py:24-27)."""
-    starts = torch.ones_like(document_ids, dtype=torch.bool)
-    starts[:, 1:] = document_ids[:, 1:] != document_ids[:, :-1]
-    return starts
-
-
 def _run_bounds(document_ids: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-    """First token and exclusive end token of the equal-id run of every token."""
+    """First token and exclusive end token of the run of equal ids holding
+    every token: a run is numbered by counting the id changes before it, and
+    its bounds are the positions of its own start and of the next run's start
+    (rows are laid end to end, each row's first token opening a run)."""
     batch, length = document_ids.shape
-    token = torch.arange(length, device=document_ids.device).expand(batch, length)
-    starts = document_start_mask(document_ids)
-    run_first = torch.where(starts, token, 0).cummax(dim=1).values
-    # a run ends where the next one starts (or at the row end)
-    next_start = torch.full_like(token, length)
-    next_start[:, :-1] = torch.where(starts[:, 1:], token[:, 1:], length)
-    run_end = next_start.flip(1).cummin(dim=1).values.flip(1)
+    change = torch.ones(batch, length, dtype=torch.bool, device=document_ids.device)
+    change[:, 1:] = document_ids[:, 1:] != document_ids[:, :-1]
+    flat = change.reshape(-1)
+    run = flat.cumsum(0) - 1  # run number of every token, over all rows
+    starts = flat.nonzero().reshape(-1)  # flat position of every run's first token
+    ends = torch.cat((starts[1:], starts.new_full((1,), flat.numel())))
+    row_base = (torch.arange(batch, device=document_ids.device) * length)[:, None]
+    run_first = starts[run].reshape(batch, length) - row_base
+    run_end = ends[run].reshape(batch, length) - row_base
     return run_first, run_end
+
+
+def _slots(position: torch.Tensor, device: torch.device) -> torch.Tensor:
+    slots = torch.as_tensor(position, device=device)
+    if slots.ndim != 1 or slots.dtype not in (torch.int32, torch.int64):
+        raise ValueError("cyclic query positions must be 1-D integer index tensors")
+    return slots.long()
 
 
 def prepare_feedback_metadata(
@@ -108,9 +112,12 @@ def prepare_feedback_metadata(
     """Per-residue cyclic metadata for packed documents (reference
     blocks/_execution/metadata.py:11-55).
 
-    Group r holds query token slots ``query_positions[r]`` = r, r+s, r+2s, ...
-    (s = number of groups). Keys are token slots shifted by the optional
-    dummy. Negative document ids (padding) become -2 and form their own runs.
+    Group r holds query token slots ``query_positions[r]`` (r, r+s, r+2s, ...
+    in the model's schedule, s = number of groups). Keys are token slots
+    shifted by the optional dummy. Negative document ids (padding) become -2
+    and form their own runs. On a GPU one HIP kernel builds every group's
+    metadata without synchronising with the host; on the CPU the same values
+    come from run numbering and gathers.
     """
     offset = int(use_dummy_token)
     groups = len(query_positions)
@@ -119,17 +126,76 @@ def prepare_feedback_metadata(
     batch, length = document_ids.shape
     if key_length > length + offset:
         raise ValueError(f"key_length={key_length} exceeds dummy-shifted token extent {length + offset}")
+    slots = [_slots(p, document_ids.device) for p in query_positions]
+    if document_ids.is_cuda:
+        return _device_feedback(document_ids, slots, key_length, offset)
     run_first, run_end = _run_bounds(document_ids)
     ids = document_ids.to(torch.int32).masked_fill(document_ids < 0, -2)
     key_ids = torch.cat((ids.new_full((batch, offset), -1), ids), dim=1)[:, :key_length].contiguous()
     result = []
-    for residue, slots in enumerate(query_positions):
-        count = slots.numel()
-        query_ids = ids.index_select(1, slots).contiguous()
-        query_key_start = (run_first.index_select(1, slots) + offset).to(torch.int32).contiguous()
+    for residue, slot in enumerate(slots):
+        count = slot.numel()
+        query_ids = ids.index_select(1, slot).contiguous()
+        query_key_start = (run_first.index_select(1, slot) + offset).to(torch.int32).contiguous()
         # queries r + s*i (i < count) that precede a token's run end
-        visible_until = torch.div((run_end - residue).clamp_min(0) + groups - 1, groups, rounding_mode="floor")
-        visible_until = visible_until.clamp_max(count).to(torch.int32)
+        behind = (run_end - residue).clamp_min(0)
+        visible_until = torch.div(behind + groups - 1, groups, rounding_mode="floor").clamp_max(count).to(torch.int32)
         key_query_end = torch.cat((ids.new_full((batch, offset), count), visible_until), dim=1)[:, :key_length]
         result.append(CyclicAttentionMetadata(query_ids, key_ids, query_key_start, key_query_end.contiguous()))
+    return tuple(result)
+
+
+def _device_feedback(
+    document_ids: torch.Tensor, slots: list[torch.Tensor], key_length: int, offset: int
+) -> tuple[CyclicAttentionMetadata, ...]:
+    """prepare_feedback_metadata through the HIP kernel (wmx_feedback_meta):
+    every group's outputs in one launch per 64 groups, no host synchronisation."""
+    from . import _native
+
+    batch, length = document_ids.shape
+    device = document_ids.device
+    groups = len(slots)
+    ids = document_ids if document_ids.dtype in (torch.int32, torch.int64) else document_ids.long()
+    if ids.stride(-1) != 1 or (batch > 1 and ids.stride(0) < length):
+        ids = ids.contiguous()
+    counts = [s.numel() for s in slots]
+    starts = [0]
+    for c in counts:
+        starts.append(starts[-1] + c)
+    flat_slots = torch.cat(slots).contiguous()
+    key_ids = torch.empty(batch, key_length, device=device, dtype=torch.int32)
+    key_query_end = torch.empty(groups, batch, key_length, device=device, dtype=torch.int32)
+    query_ids = torch.empty(batch * starts[-1], device=device, dtype=torch.int32)
+    query_key_start = torch.empty_like(query_ids)
+    a = _native.FeedbackMetaArgs()
+    a.document_ids = ids.data_ptr()
+    a.doc_stride = ids.stride(0) if batch > 1 else length
+    a.doc_dtype = _native.DTYPE_I32 if ids.dtype == torch.int32 else _native.DTYPE_I64
+    a.batch, a.length, a.key_length, a.groups, a.use_dummy = batch, length, key_length, groups, offset
+    need = _native.feedback_meta_workspace_size(a)
+    workspace = torch.empty(max(need, 16), device=device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), need
+    a.key_ids = key_ids.data_ptr()
+    for base in range(0, groups, _native.FEEDBACK_MAX_GROUPS):
+        count = min(_native.FEEDBACK_MAX_GROUPS, groups - base)
+        o0 = starts[base]
+        a.group_base, a.group_count = base, count
+        for g in range(count + 1):
+            a.group_offsets[g] = starts[base + g] - o0
+        a.slots = flat_slots.data_ptr() + 8 * o0
+        a.query_ids = query_ids.data_ptr() + 4 * batch * o0
+        a.query_key_start = query_key_start.data_ptr() + 4 * batch * o0
+        a.key_query_end = key_query_end.data_ptr() + 4 * base * batch * key_length
+        _native.feedback_meta(a, device)
+    result = []
+    for r, count in enumerate(counts):
+        span = slice(batch * starts[r], batch * starts[r + 1])
+        result.append(
+            CyclicAttentionMetadata(
+                query_ids[span].view(batch, count),
+                key_ids,
+                query_key_start[span].view(batch, count),
+                key_query_end[r],
+            )
+        )
     return tuple(result)

@@ -1,0 +1,136 @@
+"""The torch.compile contract of the HIP path, as the reference's tests state
+it for its accelerated backends:
+
+  - tests/unit/test_strict_causal_attention.py:247-275: strict prefill and
+    Jacobi (dense and packed documents, a cached prefix, a padded head_dim)
+    compiled with fullgraph=True, outputs and gradients against the oracle;
+  - tests/unit/test_strict_causal_attention.py:278-331: single-query decode
+    over per-row device lengths compiled with fullgraph=True, captured in a
+    HIP graph, replayed after the lengths and the cache change, with
+    recompilation forbidden (the lengths are data, not guards);
+  - tests/unit/test_ops.py:89-103 and blocks/_execution/cyclic.py:445: the
+    cyclic operators traced whole (fullgraph) with documents, forward and
+    backward.
+
+Tolerances are the reference's own for these tests (0.03 outputs, 0.04
+gradients, bf16 against the float64 oracle)."""
+
+import pytest
+import torch
+
+from oracle import attention as ref
+from white_matter_amd import (
+    cyclic_attention,
+    prepare_cyclic_attention_metadata,
+    prepare_strict_causal_metadata,
+    strict_causal_attention,
+)
+
+pytestmark = pytest.mark.gpu
+DEV = "cuda"
+
+
+@pytest.mark.parametrize("packed", [False, True])
+@pytest.mark.parametrize("prefix", [0, 5])
+@pytest.mark.parametrize("dim", [63, 64])
+def test_fullgraph_prefill(packed, prefix, dim):
+    torch._dynamo.reset()
+    torch.manual_seed(7 + prefix + dim)
+    q = torch.randn(2, 4, 12, dim, device=DEV, dtype=torch.bfloat16, requires_grad=True)
+    k = torch.randn(2, 2, prefix + 13, dim, device=DEV, dtype=q.dtype, requires_grad=True)
+    v = torch.randn_like(k, requires_grad=True)
+    docs = (torch.arange(prefix + 12, device=DEV) // 7).expand(2, -1)
+    metadata = prepare_strict_causal_metadata(docs, 12, query_start=prefix, use_dummy_token=True) if packed else None
+
+    def run(q, k, v):
+        return strict_causal_attention(
+            q, k, v, query_start=prefix, use_dummy_token=True, metadata=metadata, backend="torch_flash"
+        )
+
+    actual = torch.compile(run, fullgraph=True)(q, k, v)
+    leaves = [t.detach().cpu().double().requires_grad_() for t in (q, k, v)]
+    expected = ref.per_query_strict(*leaves, torch.full((2,), prefix), True, docs.cpu() if packed else None)
+    torch.testing.assert_close(actual.double().cpu(), expected, atol=0.03, rtol=0.03)
+    probe = torch.randn_like(actual)
+    ga = torch.autograd.grad(actual, (q, k, v), probe)
+    ge = torch.autograd.grad(expected, leaves, probe.double().cpu())
+    for a, e in zip(ga, ge, strict=True):
+        torch.testing.assert_close(a.double().cpu(), e, atol=0.04, rtol=0.04)
+
+
+@pytest.mark.parametrize("dummy", [False, True])
+@pytest.mark.parametrize("strided", [False, True])
+@pytest.mark.parametrize("batch", [1, 3])
+@torch.no_grad()
+def test_fullgraph_decode_graph_replay(dummy, strided, batch):
+    torch._dynamo.reset()
+    torch.manual_seed(11 + batch)
+    q = torch.randn(batch, 4, 1, 64, device=DEV, dtype=torch.bfloat16)
+    k = torch.randn(batch, 4 if strided else 2, 33 + int(dummy), 64, device=DEV, dtype=q.dtype)
+    v = torch.randn_like(k)
+    if strided:  # a pool view: the batch stride spans heads this call does not read
+        k, v = k[:, :2], v[:, :2]
+    lengths = torch.tensor([0, 7, 16][:batch], device=DEV, dtype=torch.int32)
+
+    def run(q, k, v, lengths):
+        return strict_causal_attention(
+            q, k, v, query_start=lengths, use_dummy_token=dummy, backend="torch_flash", static_cache=True
+        )
+
+    compiled = torch.compile(run, fullgraph=True)
+    compiled(q, k, v, lengths)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        captured = compiled(q, k, v, lengths)
+    for values in ([0, 7, 16][:batch], [3, 12, 32][:batch]):
+        lengths.copy_(torch.tensor(values, device=DEV, dtype=torch.int32))
+        for row, count in enumerate(values):
+            k[row, :, : count + int(dummy)].normal_()
+            v[row, :, : count + int(dummy)].normal_()
+            k[row, :, count + int(dummy) :] = float("nan")
+            v[row, :, count + int(dummy) :] = float("nan")
+        with torch.compiler.set_stance("fail_on_recompile"):
+            actual = compiled(q, k, v, lengths)
+        graph.replay()
+        torch.cuda.synchronize()
+        expected = ref.per_query_strict(q.cpu(), k.cpu(), v.cpu(), lengths.cpu(), dummy)
+        torch.testing.assert_close(actual.double().cpu(), expected, atol=0.03, rtol=0.03)
+        torch.testing.assert_close(captured.double().cpu(), expected, atol=0.03, rtol=0.03)
+
+
+@pytest.mark.parametrize("dummy", [False, True])
+def test_fullgraph_cyclic_with_documents(dummy):
+    """A residue call of the cyclic pass traced whole: the registered cyclic
+    operators (forward and backward) and the document metadata."""
+    torch._dynamo.reset()
+    torch.manual_seed(19 + int(dummy))
+    stride, length = 4, 96
+    docs = torch.cat([torch.full((n,), d) for d, n in enumerate((30, 41, 25))])[None].expand(2, -1).to(DEV)
+    residue = 1
+    qseg = docs[:, residue::stride].contiguous()
+    kseg = torch.cat((docs.new_full((2, 1), -1), docs[:, :-1]), 1) if dummy else docs
+    meta = prepare_cyclic_attention_metadata(qseg, kseg, use_dummy_token=dummy)
+    keys = kseg.shape[1]
+    q = (torch.randn(2, 4, qseg.shape[1], 64) * 0.125).to(DEV, torch.bfloat16).requires_grad_()
+    k = (torch.randn(2, 2, keys, 64) * 0.125).to(DEV, torch.bfloat16).requires_grad_()
+    v = (torch.randn(2, 2, keys, 64) * 0.125).to(DEV, torch.bfloat16).requires_grad_()
+
+    def run(q, k, v):
+        return cyclic_attention(
+            q, k, v, query_stride=stride, query_offset=residue, metadata=meta, strict_past=not dummy, backend="tilelang"
+        )
+
+    actual = torch.compile(run, fullgraph=True)(q, k, v)
+    eager = run(q, k, v)
+    torch.testing.assert_close(actual, eager, atol=0, rtol=0)
+    probe = torch.randn_like(actual)
+    ga = torch.autograd.grad(actual, (q, k, v), probe)
+    ge = torch.autograd.grad(eager, (q, k, v), probe)
+    for a, e in zip(ga, ge, strict=True):
+        torch.testing.assert_close(a, e, atol=0, rtol=0)
+    expected = ref.cyclic_attention(
+        q.detach().cpu(), k.detach().cpu(), v.detach().cpu(), query_stride=stride, query_offset=residue,
+        strict_past=not dummy, metadata=tuple(t.cpu() for t in meta),
+    )
+    torch.testing.assert_close(actual.double().cpu(), expected, atol=0.03, rtol=0.03)

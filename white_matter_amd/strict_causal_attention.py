@@ -18,6 +18,7 @@ PyTorch math path.
 
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 from typing import Literal
 
@@ -633,6 +634,16 @@ def strict_varlen_fwd(
     (see _schedule_gaps) are kept for the backward; `q_units`, `k_units`,
     `ds_offsets` and `ds_elements` are the kernels' work lists and the
     backward's dS layout (see _work_units)."""
+    return _varlen_forward(
+        query, key, value, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags,
+        scale, out_gaps, q_units, k_units,
+    )
+
+
+def _varlen_forward(
+    query, key, value, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, schedule_flags, scale,
+    out_gaps, q_units, k_units,
+):
     q, k, v = (_kernels.operand(t) for t in (query, key, value))
     batch, heads, length, dim = q.shape
     out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
@@ -683,6 +694,16 @@ def strict_varlen_bwd(
     """Gradients of strict_varlen_fwd; the rows no segment writes (`dq_gaps`
     of the (B*H*T, D) view of dQ, `dkv_gaps` of the (B*Hkv*N, D) views of dK
     and dV) are zero."""
+    return _varlen_backward_kernels(
+        query, key, value, out, lse, dout, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys,
+        schedule_flags, scale, dq_gaps, dkv_gaps, q_units, k_units, ds_offsets, ds_elements,
+    )
+
+
+def _varlen_backward_kernels(
+    query, key, value, out, lse, dout, query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys,
+    schedule_flags, scale, dq_gaps, dkv_gaps, q_units, k_units, ds_offsets, ds_elements,
+):
     q, k, v = (_kernels.operand(t) for t in (query, key, value))
     o = _kernels.operand(out.transpose(1, 2))
     g = _kernels.operand(dout.transpose(1, 2))
@@ -734,6 +755,149 @@ def _varlen_backward(ctx, dout, dlse):
 
 
 strict_varlen_fwd.register_autograd(_varlen_backward, setup_context=_varlen_setup)
+
+
+# ------------------------------------------------- packed-document plans ----
+class _PackedPlan:
+    """What the kernels need beyond a schedule's own tensors, derived on the
+    host once per schedule and call shape: the covering schedule (None when
+    it is the schedule itself), its flags, the rows no segment writes and the
+    work lists. It keeps only weak references to the schedule's tensors, so a
+    plan lives exactly as long as its schedule."""
+
+    __slots__ = ("others", "cover", "max_q", "max_k", "flags", "gaps", "units")
+
+    def schedule(self, qi, ki, cq, ck):
+        c = self.cover
+        return (qi, ki, cq, ck) if c is None else (c.query_indices, c.key_indices, c.cu_queries, c.cu_keys)
+
+
+# plans by id of the schedule's query_indices tensor: (weak reference to it,
+# plans by call shape); an entry is dropped when that tensor is freed
+_PLANS: dict[int, tuple[weakref.ref, dict]] = {}
+
+
+def _packed_plan(qi, ki, cq, ck, max_queries, max_keys, batch, length, key_slots, heads, kv_heads) -> _PackedPlan:
+    """The plan of a packed-document schedule given as its tensors (as the
+    packed operators receive it, also from a compiled graph), built on a miss
+    and kept until the schedule's tensors are freed or changed in place."""
+    shape = (max_queries, max_keys, batch, length, key_slots, heads, kv_heads)
+    entry = _PLANS.get(id(qi))
+    if entry is None or entry[0]() is not qi:
+        entry = _PLANS[id(qi)] = (weakref.ref(qi), {})
+        weakref.finalize(qi, _PLANS.pop, id(qi), None)
+    by_shape = entry[1]
+    plan = by_shape.get(shape)
+    versions = (qi._version, ki._version, cq._version, ck._version)
+    if plan is not None and plan.others[1] == versions and all(r() is t for r, t in zip(plan.others[0], (ki, cq, ck))):
+        return plan
+    _kernels.guard_capture("planning a packed-document schedule")
+    metadata = StrictCausalMetadata(qi, ki, cq, ck, max_queries, max_keys, key_slots)
+    top_q, top_k = _schedule_facts(metadata)[3:5]
+    if max_queries != length or top_q >= batch * length or top_k >= batch * key_slots:
+        raise ValueError("metadata was prepared for other query/key shapes")
+    cover = _covering_schedule(metadata, batch, length, key_slots)
+    plan = _PackedPlan()
+    plan.others = (tuple(weakref.ref(t) for t in (ki, cq, ck)), versions)
+    plan.cover = None if cover is metadata else cover
+    plan.max_q, plan.max_k, plan.flags = _schedule_flags(cover)
+    plan.gaps = _schedule_gaps(cover, batch, length, heads, key_slots, kv_heads)
+    plan.units = _work_units(cover)
+    by_shape[shape] = plan
+    return plan
+
+
+@torch.library.custom_op("white_matter::strict_packed_fwd", mutates_args=())
+def strict_packed_fwd(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    query_indices: torch.Tensor,
+    key_indices: torch.Tensor,
+    cu_queries: torch.Tensor,
+    cu_keys: torch.Tensor,
+    max_queries: int,
+    max_keys: int,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """Attention over a packed-document schedule given as its own tensors
+    (StrictCausalMetadata's fields): the host work the kernels need is planned
+    inside the operator, so a compiled graph holds this call and nothing
+    data-dependent. Output (B, T, H, D) bf16 and LSE (B, H, T) fp32."""
+    batch, heads, length, _ = query.shape
+    plan = _packed_plan(
+        query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, batch, length, key.shape[2], heads,
+        key.shape[1],
+    )
+    qi, ki, cq, ck = plan.schedule(query_indices, key_indices, cu_queries, cu_keys)
+    return _varlen_forward(
+        query, key, value, qi, ki, cq, ck, plan.max_q, plan.max_k, plan.flags, scale, plan.gaps[0], *plan.units[:2]
+    )
+
+
+@strict_packed_fwd.register_fake
+def _(query, key, value, *args):
+    batch, heads, length, dim = query.shape
+    return (
+        query.new_empty(batch, length, heads, dim, dtype=torch.bfloat16),
+        query.new_empty(batch, heads, length, dtype=torch.float32),
+    )
+
+
+@torch.library.custom_op("white_matter::strict_packed_bwd", mutates_args=())
+def strict_packed_bwd(
+    query: torch.Tensor,
+    key: torch.Tensor,
+    value: torch.Tensor,
+    out: torch.Tensor,
+    lse: torch.Tensor,
+    dout: torch.Tensor,
+    query_indices: torch.Tensor,
+    key_indices: torch.Tensor,
+    cu_queries: torch.Tensor,
+    cu_keys: torch.Tensor,
+    max_queries: int,
+    max_keys: int,
+    scale: float,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Gradients of strict_packed_fwd (the same plan)."""
+    batch, heads, length, _ = query.shape
+    plan = _packed_plan(
+        query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, batch, length, key.shape[2], heads,
+        key.shape[1],
+    )
+    qi, ki, cq, ck = plan.schedule(query_indices, key_indices, cu_queries, cu_keys)
+    return _varlen_backward_kernels(
+        query, key, value, out, lse, dout, qi, ki, cq, ck, plan.max_q, plan.max_k, plan.flags, scale, *plan.gaps[1:],
+        *plan.units,
+    )
+
+
+@strict_packed_bwd.register_fake
+def _(query, key, value, *args):
+    return (
+        query.new_empty(query.shape, dtype=torch.bfloat16),
+        key.new_empty(key.shape, dtype=torch.bfloat16),
+        value.new_empty(value.shape, dtype=torch.bfloat16),
+    )
+
+
+def _packed_setup(ctx, inputs, output):
+    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.scale = inputs
+    ctx.dtypes = (query.dtype, key.dtype, value.dtype)
+    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck)
+    ctx.set_materialize_grads(False)  # the LSE output has no gradient: no zero fill for it
+
+
+def _packed_backward(ctx, dout, dlse):
+    query, key, value, out, lse, qi, ki, cq, ck = ctx.saved_tensors
+    if dout is None:
+        dout = torch.zeros_like(out)
+    dq, dk, dv = strict_packed_bwd(query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.scale)
+    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 7
+
+
+strict_packed_fwd.register_autograd(_packed_backward, setup_context=_packed_setup)
 
 
 @torch.library.custom_op("white_matter::strict_decode", mutates_args=())
@@ -804,16 +968,11 @@ def _hip_attention(query, key, value, query_start, kv_lengths, use_dummy_token, 
     elif metadata is not None:
         if metadata.query_indices.numel() == 0:
             return _zeros_linked(query, key, value, batch, length, heads, dim)
-        top_q, top_k = _schedule_facts(metadata)[3:5]
-        max_q, max_k, flags = _schedule_flags(metadata)
-        if metadata.max_queries != length or top_q >= batch * length or top_k >= batch * key.shape[2]:
+        if metadata.max_queries != length:
             raise ValueError("metadata was prepared for other query/key shapes")
-        cover = _covering_schedule(metadata, batch, length, key.shape[2])
-        max_q, max_k, flags = _schedule_flags(cover)
-        gaps = _schedule_gaps(cover, batch, length, heads, key.shape[2], key.shape[1])
-        out, _ = strict_varlen_fwd(
-            q, k, v, cover.query_indices, cover.key_indices, cover.cu_queries, cover.cu_keys,
-            max_q, max_k, flags, scale, *gaps, *_work_units(cover),
+        out, _ = strict_packed_fwd(
+            q, k, v, metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
+            metadata.max_queries, metadata.max_keys, scale,
         )
     else:
         row_offset = row_limit = None

@@ -47,6 +47,8 @@ KERNEL_NAMES = {  # rocprof kernel name prefix -> bench kernel key
     "wmx::attn_bwd_dq_kernel": "bwd_dq",
     "wmx::attn_bwd_dq_ds_kernel": "bwd_dq",
     "wmx::attn_bwd_dkv_kernel": "bwd_dkv",
+    "wmx::decode_split_kernel<128, 1>": "decode_split_g1",  # C4 decode, 16 KV heads
+    "wmx::decode_split_kernel<128, 2>": "decode_split_g2",  # C4 decode, 8 KV heads
     "wmx::decode_split_kernel": "decode_split",
     "wmx::decode_combine_kernel": "decode_combine",
 }
@@ -318,6 +320,13 @@ def main(argv=None) -> int:
     from white_matter_amd import strict_causal_attention
 
     device = torch.device("cuda:0")
+    if args.copy_calibration:
+        # one elementwise kernel that reads and writes exactly CALIBRATION_BYTES
+        src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=device)
+        dst = torch.empty_like(src)
+        torch.neg(src, out=dst)
+        torch.cuda.synchronize()
+        del src, dst
     if args.only:
         lines = {
             "decode": decode_line,
@@ -331,13 +340,6 @@ def main(argv=None) -> int:
         }
         print(json.dumps({args.only: lines[args.only](device)}), flush=True)
         return 0
-    if args.copy_calibration:
-        # one elementwise kernel that reads and writes exactly CALIBRATION_BYTES
-        src = torch.ones(CALIBRATION_BYTES // 4, dtype=torch.float32, device=device)
-        dst = torch.empty_like(src)
-        torch.neg(src, out=dst)
-        torch.cuda.synchronize()
-        del src, dst
     q, k, v, docs, metadata, meta_ms = strict_jacobi_setup(device)
     batch, heads, length, dim = q.shape
     pairs = visible_pairs(metadata)
@@ -437,26 +439,30 @@ def main(argv=None) -> int:
 
 
 def decode_line(device):
-    """C4 decode: B=32, H=Hkv=16, D=128, kv lengths ~ U{512..8192}, one token per row."""
+    """C4 decode: B=32, H=16, D=128, kv lengths ~ U{512..8192}, one token per
+    row, over 16 KV heads (MHA, the primary line) and over 8 (GQA 2)."""
     from white_matter_amd import strict_causal_attention
 
-    q, k, v, lengths = decode_setup(device)
-    batch, kv_heads, capacity, dim = k.shape
-    with torch.no_grad():
-        fn = lambda: strict_causal_attention(q, k, v, query_start=lengths)  # noqa: E731
-        for _ in range(3):
-            fn()
-        ms = Timer()(fn, 50)
-    kv_bytes = int(lengths.sum()) * 2 * kv_heads * dim * 2
-    other = q.numel() * 2 * 2 + batch * 8
-    gbps = (kv_bytes + other) / (ms * 1e-3) / 1e9
-    return {
-        "workload": "C4 decode B=32 H=Hkv=16 D=128 kv_len~U[512,8192]",
-        "ms": round(ms, 4),
-        "gbps": round(gbps, 1),
-        "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
-        "bytes": kv_bytes + other,
-    }
+    lines = {}
+    for kv_heads in (16, 8):
+        q, k, v, lengths = decode_setup(device, kv_heads=kv_heads)
+        batch, _, capacity, dim = k.shape
+        with torch.no_grad():
+            fn = lambda: strict_causal_attention(q, k, v, query_start=lengths)  # noqa: E731
+            for _ in range(3):
+                fn()
+            ms = Timer()(fn, 100)
+        kv_bytes = int(lengths.sum()) * 2 * kv_heads * dim * 2
+        other = q.numel() * 2 * 2 + batch * 8
+        gbps = (kv_bytes + other) / (ms * 1e-3) / 1e9
+        lines[kv_heads] = {
+            "workload": f"C4 decode B=32 H=16 Hkv={kv_heads} D=128 kv_len~U[512,8192]",
+            "ms": round(ms, 4),
+            "gbps": round(gbps, 1),
+            "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
+            "bytes": kv_bytes + other,
+        }
+    return {**lines[16], "kv_heads_8": lines[8]}
 
 
 def dummy_jacobi_line(device, steps=30):

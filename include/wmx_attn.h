@@ -328,6 +328,17 @@ const char* wmx_last_error(void);
 /* Forward: o and lse. (see replaced interfaces above) */
 int wmx_attn_fwd(const wmx_attn_args* args, void* stream);
 
+/* Work list of a dense problem (no varlen schedule, no documents) for
+ * args->q_units: the (batch row, query tile) pairs, tiles of query_tile rows
+ * (128 when 0), ordered by how many 64-key tiles their rows reach under
+ * query_offset / row_offset / row_limit / query_stride, largest first,
+ * written as int32 pairs to units[0 .. 2 * batch * ceil(q_len / tile)).
+ * One kernel on the stream, no host synchronisation; the order of units with
+ * equal loads is unspecified. Replaces the host-side ordering a ragged
+ * prefill would need (the reference's FlashAttention varlen call orders its
+ * own work: ops/strict_causal_attention.py:443-458). */
+int wmx_dense_units(const wmx_attn_args* args, int32_t* units, void* stream);
+
 /* delta[b,h,i] = sum_d dout[b,h,i,d] * o[b,h,i,d] in fp32. */
 int wmx_attn_bwd_preprocess(const wmx_attn_args* args, void* stream);
 

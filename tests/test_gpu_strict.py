@@ -323,3 +323,28 @@ def test_prefill_wide_query_tile(ragged):
     vis = _kernels.Visibility(query_offset=999, row_offset=row_offset, row_limit=row_limit)
     _kernels.forward(q, k, v, o128.transpose(1, 2), lse, 64**-0.5, vis)
     assert_bf16_close(out.double(), o128.double(), max_abs=2e-3, rel_l2=1e-3, what="256 vs 128 rows")
+
+
+@pytest.mark.parametrize("tile", [128, 256])
+def test_dense_work_list_orders_tiles_by_steps(tile):
+    """wmx_dense_units (the ragged prefill's work list, one HIP kernel): every
+    (row, query tile) pair exactly once, ordered by the number of 64-key tiles
+    its bound reaches (brute force over the rows of the tile), largest first."""
+    from white_matter_amd import _kernels
+
+    gen = torch.Generator().manual_seed(5 + tile)
+    for batch, q_len, kv_len in ((3, 300, 1000), (5, 128, 64), (2, 1, 9000), (32, 256, 8448), (700, 5, 300000)):
+        offset = torch.randint(-5, kv_len, (batch,), generator=gen, dtype=torch.int32)
+        limit = torch.randint(0, kv_len + 3, (batch,), generator=gen, dtype=torch.int32)
+        units = _kernels.dense_units(batch, q_len, kv_len, 0, offset.to(DEV), limit.to(DEV), torch.device(DEV), tile)
+        tiles = -(-q_len // tile)
+        assert units.dtype == torch.int32 and units.shape == (batch * tiles, 2)
+        assert sorted(map(tuple, units.tolist())) == [(b, t) for b in range(batch) for t in range(tiles)]
+
+        def steps(b, t):
+            rows = range(t * tile, min(q_len, t * tile + tile))
+            reach = max(min(int(offset[b]) + i, int(limit[b]), kv_len - 1) for i in rows)
+            return min((max(reach, -1) + 1 + 63) // 64, 4095)  # loads past 4095 key tiles share one bin
+
+        costs = [steps(b, t) for b, t in units.tolist()]
+        assert costs == sorted(costs, reverse=True)

@@ -298,28 +298,6 @@ assert callable(cyclic_attention) and callable(strict_causal_attention)
     subprocess.run([sys.executable, "-c", code], check=True, cwd=str(__import__("pathlib").Path(__file__).parents[1]))
 
 
-def test_dense_work_list_orders_tiles_by_steps():
-    """dense_units: every (row, 128-row tile) pair once, ordered by the number
-    of 64-key tiles its bound reaches (brute force over the rows of the tile)."""
-    from white_matter_amd import _kernels
-
-    gen = torch.Generator().manual_seed(5)
-    for batch, q_len, kv_len in ((3, 300, 1000), (5, 128, 64), (2, 1, 9000)):
-        offset = torch.randint(-5, kv_len, (batch,), generator=gen)
-        limit = torch.randint(0, kv_len + 3, (batch,), generator=gen)
-        units = _kernels.dense_units(batch, q_len, kv_len, 0, offset, limit, torch.device("cpu"))
-        tiles = -(-q_len // 128)
-        assert sorted(map(tuple, units.tolist())) == [(b, t) for b in range(batch) for t in range(tiles)]
-
-        def steps(b, t):
-            rows = range(t * 128, min(q_len, t * 128 + 128))
-            reach = max(min(int(offset[b]) + i, int(limit[b]), kv_len - 1) for i in rows)
-            return (max(reach, -1) + 1 + 63) // 64
-
-        costs = [steps(b, t) for b, t in units.tolist()]
-        assert costs == sorted(costs, reverse=True)
-
-
 @pytest.mark.parametrize("dummy", [False, True])
 def test_covering_schedule_adds_rows_not_pairs(dummy):
     """The schedule the kernels run covers every query and key row (idle query

@@ -149,17 +149,18 @@ def dense_units(
 ) -> torch.Tensor:
     """Work list of a dense problem with per-row bounds: the (batch row,
     `tile`-row query tile) pairs ordered by the number of 64-key tiles they
-    visit, largest first, computed on the device (no host synchronisation).
-    Query i of row b sees key slots j <= min(offset_b + i, limit_b)."""
+    visit, largest first, as an int32 (n, 2) tensor built by one HIP kernel
+    (wmx_dense_units; no host synchronisation). Query i of row b sees key
+    slots j <= min(offset_b + i, limit_b)."""
     tiles = -(-q_len // tile)
-    last = torch.clamp(torch.arange(tiles, device=device) * tile + tile - 1, max=q_len - 1)
-    off = row_offset.to(torch.int64)[:, None] if row_offset is not None else torch.full((batch, 1), query_offset, device=device)
-    bound = off + last[None, :]
-    if row_limit is not None:
-        bound = torch.minimum(bound, row_limit.to(torch.int64)[:, None])
-    steps = (bound.clamp(-1, kv_len - 1) + KEY_STEP) // KEY_STEP
-    order = torch.argsort(steps.flatten(), descending=True, stable=True)
-    return torch.stack((order // tiles, order % tiles), 1).to(torch.int32)
+    units = torch.empty(batch * tiles, 2, device=device, dtype=torch.int32)
+    args = _native.AttnArgs()
+    args.batch, args.q_len, args.kv_len = batch, q_len, kv_len
+    args.query_stride, args.query_offset = 1, query_offset
+    args.row_offset, args.row_limit = _native.ptr(row_offset), _native.ptr(row_limit)
+    args.query_tile = tile if tile == 256 else 0
+    _native.dense_units(args, units, device)
+    return units
 
 
 def _base_args(q, k, v, o, lse, scale: float, vis: Visibility, q_len: int) -> _native.AttnArgs:

@@ -227,6 +227,7 @@ EXPORTS = (
     "wmx_strict_meta_workspace_size",
     "wmx_strict_meta_count",
     "wmx_strict_meta_fill",
+    "wmx_dense_units",
     "wmx_feedback_meta_args_size",
     "wmx_feedback_meta_workspace_size",
     "wmx_feedback_meta",
@@ -271,6 +272,8 @@ def load() -> ctypes.CDLL:
     for name in ("wmx_strict_meta_count", "wmx_strict_meta_fill"):
         getattr(lib, name).argtypes = [ctypes.POINTER(StrictMetaArgs), _vp]
         getattr(lib, name).restype = ctypes.c_int
+    lib.wmx_dense_units.argtypes = [ctypes.POINTER(AttnArgs), _vp, _vp]
+    lib.wmx_dense_units.restype = ctypes.c_int
     lib.wmx_feedback_meta_args_size.restype = ctypes.c_size_t
     lib.wmx_feedback_meta_workspace_size.argtypes = [ctypes.POINTER(FeedbackMetaArgs)]
     lib.wmx_feedback_meta_workspace_size.restype = ctypes.c_int64
@@ -399,3 +402,8 @@ def feedback_meta_workspace_size(args: FeedbackMetaArgs) -> int:
 def feedback_meta(args: FeedbackMetaArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_feedback_meta(ctypes.byref(args), _stream(device)), "wmx_feedback_meta")
+
+
+def dense_units(args: AttnArgs, units: torch.Tensor, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_dense_units(ctypes.byref(args), units.data_ptr(), _stream(device)), "wmx_dense_units")

@@ -296,6 +296,20 @@ int wmx_strict_meta_fill(const wmx_strict_meta_args* a, void* stream) {
   return launched(wmx::launch_strict_meta(*a, true, (hipStream_t)stream));
 }
 
+int wmx_dense_units(const wmx_attn_args* a, int32_t* units, void* stream) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->batch < 0 || a->q_len < 0 || a->kv_len < 0) return fail(WMX_E_INVALID, "negative shape");
+  if (a->query_indices || a->q_seg) return fail(WMX_E_INVALID, "work lists of dense problems only");
+  if (a->query_stride < 1) return fail(WMX_E_INVALID, "query_stride must be >= 1");
+  if (a->query_tile != 0 && a->query_tile != 128 && a->query_tile != 256)
+    return fail(WMX_E_INVALID, "query_tile must be 0, 128 or 256");
+  const int64_t tile = a->query_tile == 256 ? 256 : 128;
+  const int64_t n = (int64_t)a->batch * ((a->q_len + tile - 1) / tile);
+  if (n > INT32_MAX / 2) return fail(WMX_E_UNSUPPORTED, "work list of %lld units is too long", (long long)n);
+  if (n > 0 && !units) return fail(WMX_E_INVALID, "units pointer is NULL");
+  return launched(wmx::launch_dense_units(*a, units, (hipStream_t)stream));
+}
+
 size_t wmx_feedback_meta_args_size(void) { return sizeof(wmx_feedback_meta_args); }
 
 int64_t wmx_feedback_meta_workspace_size(const wmx_feedback_meta_args* args) {

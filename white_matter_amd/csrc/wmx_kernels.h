@@ -34,6 +34,7 @@ int64_t bwd_ds_bytes(const wmx_attn_args& a);  // 0 when the layout has no dS bu
 bool bwd_uses_ds(const wmx_attn_args& a);      // the workspace holds the dS buffer
 
 int launch_fwd(const wmx_attn_args& a, hipStream_t stream);
+int launch_dense_units(const wmx_attn_args& a, int32_t* units, hipStream_t stream);
 int launch_bwd_preprocess(const wmx_attn_args& a, hipStream_t stream);
 int64_t bwd_workspace_size(const wmx_attn_args& a);
 int64_t bwd_min_workspace_size(const wmx_attn_args& a);

@@ -51,9 +51,13 @@ def test_argument_checks_return_errors_without_launching():
     assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -1
     assert b"aligned" in lib.wmx_last_error()
     dec = _native.DecodeArgs()
-    dec.head_dim, dec.batch, dec.q_heads, dec.kv_heads = 128, 1, 6, 2
+    dec.head_dim, dec.batch, dec.q_heads, dec.kv_heads = 128, 1, 6, 4
+    assert lib.wmx_decode(ctypes.byref(dec), None) == -1
+    assert b"kv_heads" in lib.wmx_last_error()
+    dec.head_dim = 80
     assert lib.wmx_decode(ctypes.byref(dec), None) == -2
-    assert b"{1,2,4,8}" in lib.wmx_last_error()
+    assert b"head_dim" in lib.wmx_last_error()
+    dec.head_dim, dec.kv_heads = 128, 2
     # the allocation-free decode refuses partials beyond its static scratch
     # before it touches a device
     dec.q_heads, dec.capacity, dec.num_splits, dec.softmax_scale = 2, 4096, 20000, 0.1

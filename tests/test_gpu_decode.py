@@ -1,4 +1,4 @@
-"""Decode over the KV pool at every supported GQA ratio and at the C4 shape,
+"""Decode over the KV pool at GQA ratios 1-8, 12 and 16 and at the C4 shape,
 and the reference's FlashAttention-layout entry points, against the float64
 oracle (bf16 vs float64: max-abs <= 1e-2 * max(1, max|ref|), rel-L2 <= 5e-3).
 
@@ -46,6 +46,28 @@ def test_decode_group_sizes(group, num_splits):
     expected = ref.strict_attention(q.cpu(), k.cpu(), v.cpu(), query_start=lengths, kv_lengths=lengths)
     assert_bf16_close(out, expected, what=f"decode G={group} splits={num_splits}")
     assert out[0].count_nonzero() == 0
+
+
+@pytest.mark.parametrize("num_splits", [1, 0])
+@pytest.mark.parametrize("group", [3, 5, 6, 7, 12, 16])
+@torch.no_grad()
+def test_decode_any_group_size(group, num_splits):
+    """GQA ratios beyond powers of two (one workgroup serves up to 8 query
+    heads of a KV head; 12 and 16 heads take two launches over the same rows),
+    with head_dim 64 and 96 as well."""
+    gen = torch.Generator().manual_seed(200 + group)
+    for dim in (128, 64, 96):
+        batch, kv_heads, capacity = 3, 2, 700
+        q = _normal((batch, kv_heads * group, 1, dim), gen)
+        k = _normal((batch, kv_heads, capacity, dim), gen)
+        v = _normal((batch, kv_heads, capacity, dim), gen)
+        lengths = torch.tensor([5, 700, 333])
+        for b in range(batch):
+            k[b, :, int(lengths[b]) :] = float("nan")
+            v[b, :, int(lengths[b]) :] = float("nan")
+        out = strict_causal_attention(q, k, v, query_start=lengths.to(DEV), num_splits=num_splits)
+        expected = ref.strict_attention(q.cpu(), k.cpu(), v.cpu(), query_start=lengths)
+        assert_bf16_close(out, expected, what=f"decode G={group} D={dim} splits={num_splits}")
 
 
 @pytest.mark.parametrize("kv_heads", [16, 8])

@@ -111,9 +111,6 @@ int check_decode(const wmx_decode_args* a) {
   if (a->batch < 0 || a->q_heads <= 0 || a->kv_heads <= 0 || a->capacity < 0)
     return fail(WMX_E_INVALID, "negative or zero shape");
   if (a->q_heads % a->kv_heads != 0) return fail(WMX_E_INVALID, "q_heads %% kv_heads != 0");
-  const int g = a->q_heads / a->kv_heads;
-  if (g != 1 && g != 2 && g != 4 && g != 8)
-    return fail(WMX_E_UNSUPPORTED, "decode supports query heads per KV head in {1,2,4,8}, got %d", g);
   if (!a->q || !a->k || !a->v || !a->o) return fail(WMX_E_INVALID, "q/k/v/o pointer is NULL");
   if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v))
     return fail(WMX_E_INVALID, "q/k/v must be 16-byte aligned");

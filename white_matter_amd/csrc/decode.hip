@@ -48,8 +48,10 @@ __device__ __forceinline__ DecodeLen decode_len(const wmx_decode_args& a, int b)
   return r;
 }
 
+// G query heads of one KV head per workgroup, from head head_offset of the
+// KV head's group on (groups of more than 8 heads run in several launches)
 template <int D, int G>
-__global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args a, int chunk) {
+__global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args a, int chunk, int head_offset) {
   constexpr int LPR = D <= 64 ? 8 : 16;   // lanes per key row
   constexpr int RPW = 64 / LPR;           // rows per wave load
   constexpr int ROWS_ITER = 4 * RPW * kDecodeUnroll;
@@ -68,7 +70,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
   const int b = pair / a.kv_heads, hk = pair - b * a.kv_heads;
   const int nsplit = gridDim.x / pairs;
   const int group = a.q_heads / a.kv_heads;
-  const int h0 = hk * group;  // first query head of this KV head (G == group)
+  const int h0 = hk * group + head_offset;  // first query head of this workgroup
 
   const DecodeLen dl = decode_len(a, b);
   const int64_t j_begin = (int64_t)split * chunk;
@@ -273,20 +275,29 @@ int64_t decode_workspace_size(const wmx_decode_args& a) {
 }
 
 template <int D, int G>
-static void launch_decode_t(const wmx_decode_args& a, int nsplit, int chunk, hipStream_t stream) {
+static void launch_decode_t(const wmx_decode_args& a, int nsplit, int chunk, int head_offset, hipStream_t stream) {
   const int64_t blocks = (int64_t)nsplit * a.batch * a.kv_heads;  // <= INT32_MAX (checked by the caller)
-  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3((unsigned)blocks), dim3(256), 0, stream, a, chunk);
+  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3((unsigned)blocks), dim3(256), 0, stream, a, chunk, head_offset);
 }
 
+// Any group size: up to 8 query heads share one read of each K/V row; larger
+// groups take one launch per 8 heads (and the remainder).
 template <int D>
 static int launch_decode_d(const wmx_decode_args& a, int nsplit, int chunk, hipStream_t stream) {
-  switch (a.q_heads / a.kv_heads) {
-    case 1: launch_decode_t<D, 1>(a, nsplit, chunk, stream); return WMX_OK;
-    case 2: launch_decode_t<D, 2>(a, nsplit, chunk, stream); return WMX_OK;
-    case 4: launch_decode_t<D, 4>(a, nsplit, chunk, stream); return WMX_OK;
-    case 8: launch_decode_t<D, 8>(a, nsplit, chunk, stream); return WMX_OK;
-    default: return WMX_E_UNSUPPORTED;
+  const int group = a.q_heads / a.kv_heads;
+  for (int off = 0; off < group; off += 8) {
+    switch (group - off < 8 ? group - off : 8) {
+      case 1: launch_decode_t<D, 1>(a, nsplit, chunk, off, stream); break;
+      case 2: launch_decode_t<D, 2>(a, nsplit, chunk, off, stream); break;
+      case 3: launch_decode_t<D, 3>(a, nsplit, chunk, off, stream); break;
+      case 4: launch_decode_t<D, 4>(a, nsplit, chunk, off, stream); break;
+      case 5: launch_decode_t<D, 5>(a, nsplit, chunk, off, stream); break;
+      case 6: launch_decode_t<D, 6>(a, nsplit, chunk, off, stream); break;
+      case 7: launch_decode_t<D, 7>(a, nsplit, chunk, off, stream); break;
+      default: launch_decode_t<D, 8>(a, nsplit, chunk, off, stream); break;
+    }
   }
+  return WMX_OK;
 }
 
 int launch_decode(const wmx_decode_args& a, hipStream_t stream) {

@@ -259,6 +259,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
     keys.issue(a, pb, dma, n0, k_lds0, v_lds0);
     store_meta(0, load_meta(n0));
   }
+  lgkm_settle();  // no scalar load of the prologue stays pending into the tile loop
   for (int it = 0; it < ntiles; it += 2) {
     iteration(std::integral_constant<int, 0>{}, it);
     if (it + 1 < ntiles) iteration(std::integral_constant<int, 1>{}, it + 1);
@@ -448,6 +449,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
     issue_ds(n0, s_lds0);
     store_meta(0, load_meta(n0));
   }
+  lgkm_settle();  // no scalar load of the prologue stays pending into the tile loop
   for (int it = 0; it < ntiles; it += 2) {
     iteration(std::integral_constant<int, 0>{}, it);
     if (it + 1 < ntiles) iteration(std::integral_constant<int, 1>{}, it + 1);
@@ -628,6 +630,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
         const void* zero = (const void*)kZeroChunk;
         __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.lse + idx) : zero, (lds_void*)&stat_lds[B][0][0], 4, 0, 0);
         __builtin_amdgcn_global_load_lds(ok ? (const void*)(a.delta + idx) : zero, (lds_void*)&stat_lds[B][1][0], 4, 0, 0);
+        lgkm_settle();
       }
     }
   };
@@ -834,6 +837,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     qrows.issue(a, pb, dma, hq_cur, m_cur, q_lds0, g_lds0);
     issue_meta(std::integral_constant<int, 0>{}, hq_cur, m_cur);
   }
+  lgkm_settle();  // no scalar load of the prologue stays pending into the tile loop
   // one copy of the tile loop per role, so that no role branch sits inside it
   // (a branch there makes the compiler copy the accumulators at every merge)
   auto run = [&](auto sidec) __attribute__((always_inline)) {
@@ -975,6 +979,11 @@ static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
   return WMX_OK;
 }
 
+template <int D, int MODE, bool ATOMIC, bool DS>
+static void launch_dkv_kernel(const wmx_attn_args& a, dim3 grid, hipStream_t stream) {
+  hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, ATOMIC, DS>), grid, dim3(512), 0, stream, a);
+}
+
 template <int D, int MODE>
 static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + 127) / 128;
@@ -991,19 +1000,19 @@ static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
                        (float*)a.workspace, n);
     // every row through atomics, or (keys_unique 2) slot 0 only: the direct-store kernel
     if (a.keys_unique == 2) {
-      if (ds) hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false, true>), grid, dim3(512), 0, stream, a);
-      else hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false, false>), grid, dim3(512), 0, stream, a);
+      if (ds) launch_dkv_kernel<D, MODE, false, true>(a, grid, stream);
+      else launch_dkv_kernel<D, MODE, false, false>(a, grid, stream);
     } else if (ds) {
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true, true>), grid, dim3(512), 0, stream, a);
+      launch_dkv_kernel<D, MODE, true, true>(a, grid, stream);
     } else {
-      hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, true, false>), grid, dim3(512), 0, stream, a);
+      launch_dkv_kernel<D, MODE, true, false>(a, grid, stream);
     }
     const int64_t total = n / 2;
     hipLaunchKernelGGL(acc_to_bf16_kernel, dim3((unsigned)((total + 255) / 256)), dim3(256), 0, stream, a);
   } else if (ds) {
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false, true>), grid, dim3(512), 0, stream, a);
+    launch_dkv_kernel<D, MODE, false, true>(a, grid, stream);
   } else {
-    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, false, false>), grid, dim3(512), 0, stream, a);
+    launch_dkv_kernel<D, MODE, false, false>(a, grid, stream);
   }
   return WMX_OK;
 }

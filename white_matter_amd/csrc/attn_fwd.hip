@@ -323,6 +323,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void attn_fwd_kernel(cons
     keys.issue(a, pb, dma, n0, k_lds0, v_lds0);
     store_meta(0, load_meta(n0));
   }
+  lgkm_settle();  // no scalar load of the prologue stays pending into the tile loop
   for (int it = 0; it < ntiles; it += 2) {
     iteration(std::integral_constant<int, 0>{}, it);
     if (it + 1 < ntiles) iteration(std::integral_constant<int, 1>{}, it + 1);

@@ -134,6 +134,19 @@ __device__ __forceinline__ rsrc_t make_rsrc(const void* base, int bytes) {
 // Source of the zero rows of gathered tiles.
 static __device__ __attribute__((aligned(16))) const uint32_t kZeroChunk[4] = {0u, 0u, 0u, 0u};
 
+// After global_load_lds: the compiler counts these direct-to-LDS loads (FLAT
+// encoding) as LDS operations whose completion order it cannot track, and
+// from then on waits for every outstanding LDS read (lgkmcnt(0)) wherever any
+// one is needed, on every path that joins this one, so reads issued ahead of
+// their products no longer overlap them. An explicit lgkmcnt(0) here settles
+// that state once, on the path that issued the loads (buffer_load ... lds, the
+// strided form, does not need it).
+__device__ __forceinline__ void lgkm_settle() {
+  __asm__ volatile("" ::: "memory");
+  __builtin_amdgcn_s_waitcnt(0xC07F);  // lgkmcnt(0); vmcnt and expcnt left at their maximum
+  __asm__ volatile("" ::: "memory");
+}
+
 // This thread's 16-byte slots of a 64-row tile filled by NW waves: each wave
 // fills 64 / NW rows with 16 / NW instructions of 4 rows.
 template <int D, int NW = 4>
@@ -202,6 +215,7 @@ struct TileDMA {
       const void* s0 = (ok && c >= 0) ? (const void*)((const char*)p0 + c) : (const void*)kZeroChunk;
       __builtin_amdgcn_global_load_lds(s0, dst(t0, r), 16, 0, 0);
     }
+    lgkm_settle();
   }
   // Two tiles whose rows are located together: rows(tr, ok, p0, p1) returns
   // the addresses of tile row tr and sets ok = false for a row that must read
@@ -220,6 +234,7 @@ struct TileDMA {
       __builtin_amdgcn_global_load_lds(s0, dst(t0, r), 16, 0, 0);
       __builtin_amdgcn_global_load_lds(s1, dst(t1, r), 16, 0, 0);
     }
+    lgkm_settle();
   }
 };
 

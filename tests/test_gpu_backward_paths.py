@@ -12,7 +12,7 @@ import torch
 from oracle import attention as ref
 from tests.numerics import assert_bf16_close
 from white_matter_amd import _kernels, _native, prepare_strict_causal_metadata
-from white_matter_amd.strict_causal_attention import _schedule_flags, _work_units
+from white_matter_amd.strict_causal_attention import _keys_unique_code, _schedule_flags, _work_units
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -52,11 +52,14 @@ def _inputs(batch, heads, kv_heads, length, dim, seed):
     return q, k, v, dout
 
 
-def _compare(q, k, v, dout, vis, keep):
+def _compare(q, k, v, dout, vis, keep, repeats=0):
     scale = q.shape[-1] ** -0.5
     o1, dq1, dk1, dv1 = _run(q, k, v, dout, vis, scale, True)
     o2, dq2, dk2, dv2 = _run(q, k, v, dout, vis, scale, False)
     assert torch.equal(dk1, dk2) and torch.equal(dv1, dv2)
+    for _ in range(repeats):  # the same gradients, bit for bit, on every run
+        _, dq3, dk3, dv3 = _run(q, k, v, dout, vis, scale, True)
+        assert torch.equal(dq3, dq1) and torch.equal(dk3, dk1) and torch.equal(dv3, dv1)
     assert torch.isfinite(dq1.float()).all()
     qr, kr, vr = (t.double().cpu().requires_grad_() for t in (q, k, v))
     expected = ref.masked_attention(qr, kr, vr, keep.cpu(), scale)
@@ -95,3 +98,36 @@ def test_varlen_paths_agree(length):
     }
     keep = ref.schedule_keep(meta, batch, length, length)[:, None]
     _compare(q, k, v, dout, _kernels.Visibility(varlen=varlen), keep)
+
+
+@pytest.mark.parametrize(("length", "kv_heads"), [(300, 2), (1024, 4)])
+def test_dummy_slot_parts(length, kv_heads):
+    """A packed schedule with the leading dummy (only slot 0 repeats across
+    segments, keys_unique 2): every segment stores its part of the dummy's
+    dK/dV and a second kernel adds them in segment order. Both dQ paths
+    against the oracle, the workspace filled with NaN patterns beforehand,
+    and the same gradients bit for bit over repeated runs."""
+    batch, heads, dim = 3, 4, 128
+    gen = torch.Generator().manual_seed(length)
+    q = (torch.randn(batch, heads, length, dim, generator=gen) * dim**-0.5).bfloat16().to(DEV)
+    k = (torch.randn(batch, kv_heads, length + 1, dim, generator=gen) * dim**-0.5).bfloat16().to(DEV)
+    v = torch.randn(batch, kv_heads, length + 1, dim, generator=gen).bfloat16().to(DEV)
+    dout = torch.randn(batch, heads, length, dim, generator=gen).bfloat16().to(DEV)
+    docs = torch.cumsum(torch.rand(batch, length, generator=gen) < 0.01, 1).to(DEV)
+    md = prepare_strict_causal_metadata(docs, length, use_dummy_token=True)
+    max_q, max_k, flags = _schedule_flags(md)
+    assert _keys_unique_code(flags) == 2 and md.cu_queries.numel() - 1 > batch
+    varlen = _kernels.Varlen(
+        md.query_indices, md.key_indices, md.cu_queries, md.cu_keys, md.cu_queries.numel() - 1, max_q, max_k,
+        length, length + 1, 2, flags & 15, *_work_units(md),
+    )
+    meta = {
+        "query_indices": md.query_indices.cpu().numpy(),
+        "key_indices": md.key_indices.cpu().numpy(),
+        "cu_queries": md.cu_queries.cpu().numpy(),
+        "cu_keys": md.cu_keys.cpu().numpy(),
+        "key_extent": md.key_extent,
+    }
+    keep = ref.schedule_keep(meta, batch, length, length + 1)[:, None]
+    assert keep[..., 0].all()
+    _compare(q, k, v, dout, _kernels.Visibility(varlen=varlen), keep, repeats=2)

@@ -20,9 +20,11 @@
 //         dS form streams K and dS^T tiles and runs after dKV; the recompute
 //         form (no dS buffer) evaluates S^T = K Q^T and dP^T = V dO^T itself,
 //         a lane owning one query column so its LSE and delta are scalars.
-// Varlen schedules whose key rows repeat across segments (the shared dummy
-// slot, capped histories) accumulate dK/dV in fp32 workspace rows with
-// atomics and convert once at the end.
+// Varlen schedules whose key rows repeat across segments: where only the
+// dummy slot of each batch row is shared, each segment stores its part of the
+// dummy's dK/dV and a second kernel adds the parts in segment order (the same
+// result on every run); where other rows repeat (capped histories), dK/dV
+// accumulate in fp32 workspace rows with atomics, converted once at the end.
 #include <type_traits>
 
 #include "attn_tiles.h"
@@ -869,17 +871,20 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     }
   } else {
     if (MODE == kVarlen && a.keys_unique == 2 && kslot == 0) {
-      // the shared dummy row: fp32 accumulators [batch row][kv head][D], dK then dV
-      float* dst = (float*)a.workspace + ((int64_t)kb * a.kv_heads + hk) * D +
-                   (dp_side ? 0 : (int64_t)a.batch * a.kv_heads * D);
+      // the dummy slot shared by the segments of a batch row: this segment's
+      // part, [dK, dV][segment][kv head][D], and its mark (the dummy's batch
+      // row + 1); dummy_reduce_kernel adds the parts in segment order
+      float* dst = (float*)((char*)a.workspace + bwd_dummy_mark_bytes(a)) +
+                   (((dp_side ? 0 : (int64_t)a.num_segments) + grp) * a.kv_heads + hk) * D;
 #pragma unroll
       for (int d = 0; d < DB; ++d) {
 #pragma unroll
         for (int r = 0; r < 16; ++r) {
           const int dd = d * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
-          atomicAdd(dst + dd, acc[d][r] * scale);
+          dst[dd] = acc[d][r] * scale;
         }
       }
+      if (!dp_side) ((int32_t*)a.workspace)[grp] = kb + 1;
       return;
     }
     bf16* dst = dp_side ? (bf16*)row_at(a.dk, a.dk_stride, kb, hk, kslot) : (bf16*)row_at(a.dv, a.dv_stride, kb, hk, kslot);
@@ -897,8 +902,51 @@ __global__ void zero_f32_kernel(float* p, int64_t n) {
   }
 }
 
-// Convert the fp32 [B*R][Hkv][D] accumulators (R = bwd_acc_rows: every slot,
-// or slot 0 only) to bf16 dK/dV with their strides.
+// The dummy slot's dK/dV where only it repeats: for every batch row, the sum
+// of the parts of the segments marked with that row, added in segment order,
+// stored as bf16 at slot 0 (zero for a row that no segment marks). Block
+// (b, c) covers elements c * 256 .. of the [dK, dV][kv head][D] rows of b;
+// the segments are taken 256 at a time, the marked ones listed in LDS in
+// order (wave ballots and a prefix over the four waves).
+__global__ __launch_bounds__(256) void dummy_reduce_kernel(const wmx_attn_args a, int cols) {
+  __shared__ int list[256];
+  __shared__ int wave_count[4];
+  const int per_side = a.kv_heads * a.head_dim;
+  const int b = blockIdx.x / cols;
+  const int e = (blockIdx.x - b * cols) * 256 + threadIdx.x;
+  const bool live = e < 2 * per_side;
+  const int side = live ? e / per_side : 0;
+  const int rem = live ? e - side * per_side : 0;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int32_t* marks = (const int32_t*)a.workspace;
+  const float* parts = (const float*)((const char*)a.workspace + bwd_dummy_mark_bytes(a)) +
+                       (int64_t)side * a.num_segments * per_side + rem;
+  float sum = 0.f;
+  for (int c0 = 0; c0 < a.num_segments; c0 += 256) {
+    const int s = c0 + threadIdx.x;
+    const bool mine = s < a.num_segments && marks[s] == b + 1;
+    const uint64_t ballot = __ballot(mine);
+    if (lane == 0) wave_count[w] = __popcll(ballot);
+    __syncthreads();
+    int base = 0;
+    for (int i = 0; i < w; ++i) base += wave_count[i];
+    const int total = wave_count[0] + wave_count[1] + wave_count[2] + wave_count[3];
+    if (mine) list[base + __popcll(ballot & ((1ull << lane) - 1))] = s;
+    __syncthreads();
+    if (live) {
+      for (int i = 0; i < total; ++i) sum += parts[(int64_t)list[i] * per_side];
+    }
+    __syncthreads();  // list and wave_count are rewritten by the next chunk
+  }
+  if (!live) return;
+  const int h = rem / a.head_dim, d = rem - h * a.head_dim;
+  void* out = side == 0 ? a.dk : a.dv;
+  const int64_t* st = side == 0 ? a.dk_stride : a.dv_stride;
+  ((bf16*)out)[(int64_t)b * st[0] + (int64_t)h * st[1] + d] = (__bf16)sum;
+}
+
+// Convert the fp32 [B*R][Hkv][D] accumulators (R = bwd_acc_rows, every key
+// slot) to bf16 dK/dV with their strides.
 __global__ void acc_to_bf16_kernel(const wmx_attn_args a) {
   const int D = a.head_dim;
   const int64_t rows = bwd_acc_rows(a);
@@ -994,15 +1042,22 @@ static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
   if (units > UINT32_MAX) return WMX_E_UNSUPPORTED;
   const dim3 grid((unsigned)units);
   const bool ds = bwd_uses_ds(a);
-  if (MODE == kVarlen && a.keys_unique != 1) {
+  if (MODE == kVarlen && a.keys_unique == 2) {
+    // slot 0 through per-segment parts and an ordered sum, every other row stored directly
+    const int cols = (2 * a.kv_heads * D + 255) / 256;
+    if ((int64_t)a.batch * cols > UINT32_MAX) return WMX_E_UNSUPPORTED;
+    const int64_t marks = bwd_dummy_mark_bytes(a) / (int64_t)sizeof(int32_t);
+    hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((marks / 4 + 256) / 256)), dim3(256), 0, stream,
+                       (float*)a.workspace, marks);
+    if (ds) launch_dkv_kernel<D, MODE, false, true>(a, grid, stream);
+    else launch_dkv_kernel<D, MODE, false, false>(a, grid, stream);
+    hipLaunchKernelGGL(dummy_reduce_kernel, dim3((unsigned)(a.batch * cols)), dim3(256), 0, stream, a, cols);
+  } else if (MODE == kVarlen && a.keys_unique != 1) {
+    // any key row may repeat: every row through fp32 atomics
     const int64_t n = bwd_acc_bytes(a) / (int64_t)sizeof(float);
     hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((n / 4 + 256) / 256)), dim3(256), 0, stream,
                        (float*)a.workspace, n);
-    // every row through atomics, or (keys_unique 2) slot 0 only: the direct-store kernel
-    if (a.keys_unique == 2) {
-      if (ds) launch_dkv_kernel<D, MODE, false, true>(a, grid, stream);
-      else launch_dkv_kernel<D, MODE, false, false>(a, grid, stream);
-    } else if (ds) {
+    if (ds) {
       launch_dkv_kernel<D, MODE, true, true>(a, grid, stream);
     } else {
       launch_dkv_kernel<D, MODE, true, false>(a, grid, stream);

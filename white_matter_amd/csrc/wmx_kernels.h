@@ -14,19 +14,31 @@ enum Mode {
   kVarlen = 2,  // packed segments addressed through flat query/key indices
 };
 
-// Backward workspace: fp32 dK/dV accumulators (varlen schedules whose key
-// rows repeat: all rows, or slot 0 only), then from a 256-byte boundary the bf16 dS buffer: per query
+// Backward workspace: the dK/dV accumulators of varlen schedules whose key
+// rows repeat, then from a 256-byte boundary the bf16 dS buffer: per query
 // head and problem (batch row or segment) a block of keys x ld elements,
 // ld = queries rounded up to 128, holding dS^T (element [j * ld + i] for key
 // j and query i).
-// Rows of the fp32 dK/dV accumulators per batch row: every key slot when any
-// key row may repeat, slot 0 only when only the leading dummy repeats.
+//   keys_unique 0 (any key row may repeat): fp32 rows [2][batch][key slot]
+//     [kv head][D] (dK, then dV), accumulated with atomics;
+//   keys_unique 2 (only the leading dummy of a batch row repeats): per
+//     segment a mark (its dummy's batch row + 1, 0 without one) from offset
+//     0, then from a 256-byte boundary fp32 partials [2][segment][kv head][D]
+//     that a second kernel sums in segment order (no atomics: the dummy's
+//     gradients are the same on every run).
 __host__ __device__ inline int64_t bwd_acc_rows(const wmx_attn_args& a) {
-  if (!a.query_indices || a.keys_unique == 1) return 0;
-  return a.keys_unique == 2 ? 1 : a.key_extent;
+  return a.query_indices && a.keys_unique == 0 ? a.key_extent : 0;
+}
+__host__ __device__ inline bool bwd_dummy_partials(const wmx_attn_args& a) {
+  return a.query_indices && a.keys_unique == 2;
+}
+__host__ __device__ inline int64_t bwd_dummy_mark_bytes(const wmx_attn_args& a) {
+  return ((int64_t)a.num_segments * (int64_t)sizeof(int32_t) + 255) & ~(int64_t)255;
 }
 __host__ __device__ inline int64_t bwd_acc_bytes(const wmx_attn_args& a) {
-  return (int64_t)2 * a.batch * bwd_acc_rows(a) * a.kv_heads * a.head_dim * (int64_t)sizeof(float);
+  const int64_t row = (int64_t)a.kv_heads * a.head_dim * (int64_t)sizeof(float);
+  if (bwd_dummy_partials(a)) return bwd_dummy_mark_bytes(a) + 2 * (int64_t)a.num_segments * row;
+  return 2 * (int64_t)a.batch * bwd_acc_rows(a) * row;
 }
 __host__ __device__ inline int64_t bwd_ds_offset(const wmx_attn_args& a) { return (bwd_acc_bytes(a) + 255) & ~(int64_t)255; }
 __host__ __device__ inline int64_t ds_ld(int nq) { return ((int64_t)nq + 127) & ~(int64_t)127; }

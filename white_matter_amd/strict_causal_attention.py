@@ -299,8 +299,15 @@ def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, int, int,
         # shared by the row's segments) repeats; 0: other rows repeat
         unique = 1 if n == 0 or int(torch.unique(ki).numel()) == n else 0
         if not unique:
-            real = ki[ki % metadata.key_extent != 0]
+            dummy = ki % metadata.key_extent == 0
+            real = ki[~dummy]
             unique = 2 if int(torch.unique(real).numel()) == real.numel() else 0
+            # code 2 keeps one part of the dummy's gradients per segment: a
+            # segment holding two slot-0 keys takes the general path
+            per_segment = torch.cat((dummy.new_zeros(1, dtype=torch.long), dummy.long().cumsum(0)))
+            per_segment = per_segment[metadata.cu_keys.long()].diff()
+            if unique == 2 and per_segment.numel() and int(per_segment.max()) > 1:
+                unique = 0
         unique_q = qi.numel() == 0 or int(torch.unique(qi).numel()) == qi.numel()
         top_q = int(qi.max()) if qi.numel() else -1
         top_k = int(ki.max()) if n else -1

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 5
+#define WMX_ABI_VERSION 6
 
 enum {
   WMX_OK = 0,
@@ -239,6 +239,46 @@ typedef struct wmx_kv_store_args {
 } wmx_kv_store_args;
 
 /*
+ * KV-pool producer, the token-local steps ahead of the per-channel projection
+ * (reference modules/kv_pool.py:97-160 `KVPool._project`, the bf16 inference
+ * form of :108-136; modules/routing.py:77-124 `Router.forward`,
+ * `_RoutedMixer.forward`). For token n = b * T + t with sources
+ * x[s] = sources[b, t, s, :] (S rows of `hidden`) and each side (0 K, 1 V):
+ *   wmx_kv_premix:
+ *     premixed[side][n, s, :] = bf16(x[s] * (1 / sqrt(mean(x[s]^2) + eps)) * pre_mix[side][s, :])
+ *   the router logits alpha[side][n, c * S + s] are the caller's GEMM of the
+ *   premixed row (B*T, S*hidden) by the router weight, plus its bias;
+ *   wmx_kv_mix:
+ *     m = bf16(sum over s ascending of alpha[side][n, c * S + s] * premixed[side][n, s, :])
+ *     mixed[side][c, n, :] = bf16(m * (1 / sqrt(mean(m^2) + mix_eps)) * gain[side][c, :])
+ * with fp32 arithmetic throughout (the sources are read as fp32 whatever their
+ * dtype). mixed[side] is the (C, B*T, hidden) input of the per-channel
+ * projection GEMM.
+ */
+#define WMX_KV_MIX_MAX_SOURCES 512
+#define WMX_KV_MIX_MAX_HIDDEN 4096
+
+typedef struct wmx_kv_mix_args {
+  const void* sources;        /* (B, T, S, hidden), dtype source_dtype, unit stride along hidden */
+  int64_t source_stride[3];   /* element strides [batch, token, source]; 0 repeats one row */
+  const void* pre_mix[2];     /* (S, hidden) contiguous, dtype weight_dtype: K side, V side */
+  void* premixed[2];          /* bf16 (B*T, S*hidden) contiguous */
+  const void* alpha[2];       /* bf16 (B*T, C*S), rows alpha_stride elements apart */
+  int64_t alpha_stride;
+  const void* gain[2];        /* (C, hidden) contiguous, dtype weight_dtype */
+  void* mixed[2];             /* bf16 (C, B*T, hidden) contiguous */
+  int32_t source_dtype;       /* WMX_DTYPE_F32 or WMX_DTYPE_BF16 */
+  int32_t weight_dtype;       /* of pre_mix and gain */
+  int32_t batch;
+  int32_t tokens;
+  int32_t num_sources;        /* S, 1 .. WMX_KV_MIX_MAX_SOURCES */
+  int32_t hidden;             /* a multiple of 8, at most WMX_KV_MIX_MAX_HIDDEN */
+  int32_t channels;           /* C >= 1 */
+  float eps;
+  float mix_eps;
+} wmx_kv_mix_args;
+
+/*
  * Packed-document schedule builder on the device: the reference's
  * prepare_strict_causal_metadata (ops/strict_causal_attention.py:75-155),
  * whose torch sequence synchronises with the host at every data-dependent
@@ -321,6 +361,7 @@ int wmx_abi_version(void);
 size_t wmx_attn_args_size(void);
 size_t wmx_decode_args_size(void);
 size_t wmx_kv_store_args_size(void);
+size_t wmx_kv_mix_args_size(void);
 size_t wmx_strict_meta_args_size(void);
 size_t wmx_feedback_meta_args_size(void);
 const char* wmx_last_error(void);
@@ -396,6 +437,15 @@ int wmx_decode_noalloc(const wmx_decode_args* args, void* stream);
  * rms_norm, weight, RoPE, casts and index_copy_ (modules/kv_pool.py:163-172,
  * 216; blocks/_execution/cyclic.py:448-458). */
 int wmx_kv_pool_store(const wmx_kv_store_args* args, void* stream);
+
+/* KV-pool producer (see wmx_kv_mix_args). wmx_kv_premix replaces the source
+ * RMS norm and the pre-mix products with their bf16 casts (reference
+ * modules/kv_pool.py:15-19 `_premix`, :103-123); wmx_kv_mix replaces the routed
+ * mixture, the mix norm and the gain with its cast and permute (reference
+ * modules/routing.py:117-124 `_RoutedMixer.forward`, modules/kv_pool.py:22-25
+ * `_projection_input`, :129-136). Outputs are fully overwritten. */
+int wmx_kv_premix(const wmx_kv_mix_args* args, void* stream);
+int wmx_kv_mix(const wmx_kv_mix_args* args, void* stream);
 
 /* Packed-document schedule (see wmx_strict_meta_args): replaces the torch
  * sequence of prepare_strict_causal_metadata (reference

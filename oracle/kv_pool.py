@@ -16,6 +16,18 @@ Pinned (tests/test_kv_pool.py) against the same steps written with
 PyTorch's own F.rms_norm and tensor ops on the CPU in the key dtype, and
 against rotation invariants of RoPE (pairwise norm preservation, identity
 and half-turn rotations).
+
+`projection_inputs` follows src/white_matter/modules/kv_pool.py:97-136
+(`KVPool._project` in its bf16 inference form: rms_norm of the sources,
+`_premix` :15-19, the mixer, the mix norm with eps 1e-4, `_projection_input`
+:22-25) and src/white_matter/modules/routing.py:77-124 (`Router.forward` with
+every source in the router's context, `_RoutedMixer.forward`). Sums are
+taken in float64, with a bf16 rounding wherever the reference casts or a
+bf16 operation returns (premixed rows, logits, mixtures, outputs). Pinned
+(tests/test_kv_pool.py) against the reference's formulation with PyTorch's
+F.rms_norm, F.linear and einsum, against the closed form of the routing
+prior (each channel reads one source scaled by 2^-2), at magnitudes where
+both eps values move the result, and by a planted exchange of the two eps.
 """
 
 from __future__ import annotations
@@ -54,3 +66,30 @@ def write_pool(key, value, weight, cos, sin, keys, values, slots, eps):
     if values is not None:
         out_v.index_copy_(3, slots, value.to(values.dtype))
     return out_k, out_v
+
+
+def projection_inputs(stacked, pre_mix, router, gain, eps, mix_eps):
+    """Float64 (2, C, B*T, hidden) holding bf16 values: the K-side and V-side
+    inputs of the per-channel projections for sources stacked (B, T, S,
+    hidden); pre_mix (2, S, hidden); router ((W_K, b_K), (W_V, b_V)) with W
+    (C*S, S*hidden) and b (C*S,) (logit of channel c, source s at c*S + s);
+    gain (2, C, hidden)."""
+    bf16 = torch.bfloat16
+    x = stacked.to(torch.float64)
+    batch, tokens, sources, hidden = x.shape
+    rows = batch * tokens
+    channels = gain[0].shape[0]
+    normed = x / torch.sqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    out = []
+    for side in range(2):
+        premixed = _round(normed * pre_mix[side].to(torch.float64), bf16).reshape(rows, sources, hidden)
+        weight, bias = (t.to(torch.float64) for t in router[side])
+        logits = _round(premixed.reshape(rows, sources * hidden) @ weight.t() + bias, bf16)
+        logits = logits.reshape(rows, channels, sources)
+        mixed = torch.zeros(rows, channels, hidden, dtype=torch.float64)
+        for s in range(sources):  # the routed sum, one source at a time
+            mixed += logits[:, :, s, None] * premixed[:, None, s, :]
+        mixed = _round(mixed, bf16)
+        scale = 1.0 / torch.sqrt(mixed.pow(2).mean(-1, keepdim=True) + mix_eps)
+        out.append(_round(mixed * scale * gain[side].to(torch.float64)[None], bf16).permute(1, 0, 2))
+    return torch.stack(out)

@@ -30,6 +30,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.wmx_abi_version() == _native.ABI_VERSION
     assert lib.wmx_attn_args_size() == ctypes.sizeof(_native.AttnArgs)
     assert lib.wmx_decode_args_size() == ctypes.sizeof(_native.DecodeArgs)
+    assert lib.wmx_kv_mix_args_size() == ctypes.sizeof(_native.KvMixArgs)
 
 
 def test_argument_checks_return_errors_without_launching():
@@ -65,6 +66,25 @@ def test_argument_checks_return_errors_without_launching():
     assert lib.wmx_decode_workspace_size(ctypes.byref(dec)) > _native.DECODE_NOALLOC_MAX_BYTES
     assert lib.wmx_decode_noalloc(ctypes.byref(dec), None) == -3
     assert b"static scratch" in lib.wmx_last_error()
+    mix = _native.KvMixArgs()
+    mix.batch, mix.tokens, mix.num_sources, mix.hidden, mix.channels = 1, 1, 25, 1028, 8
+    assert lib.wmx_kv_premix(ctypes.byref(mix), None) == -2
+    assert b"hidden" in lib.wmx_last_error()
+    mix.hidden, mix.num_sources = 1024, _native.KV_MIX_MAX_SOURCES + 1
+    assert lib.wmx_kv_mix(ctypes.byref(mix), None) == -2
+    assert b"num_sources" in lib.wmx_last_error()
+    mix.num_sources = 25
+    assert lib.wmx_kv_mix(ctypes.byref(mix), None) == -1
+    assert b"NULL" in lib.wmx_last_error()
+    for side in range(2):
+        mix.premixed[side] = mix.alpha[side] = mix.gain[side] = mix.mixed[side] = 0x1000
+    mix.alpha_stride = 8 * 25 - 1
+    assert lib.wmx_kv_mix(ctypes.byref(mix), None) == -1
+    assert b"alpha_stride" in lib.wmx_last_error()
+    mix.pre_mix[0] = mix.pre_mix[1] = 0x1000
+    mix.sources, mix.source_stride = 0x1000, (25 * 1024, 1024, 1028)
+    assert lib.wmx_kv_premix(ctypes.byref(mix), None) == -1
+    assert b"strides" in lib.wmx_last_error()
 
 
 def test_workspace_sizes():

@@ -4,7 +4,14 @@ PyTorch steps on the GPU. Keys: the bf16 bar (max-abs <= 1e-2 * max(1,
 max|ref|), relative L2 <= 5e-3) and >= 99% bit-exact: the rms mean is
 summed in another order, so a rare rounding step lands one ulp apart (and
 RoPE's sum can cancel, which magnifies that ulp relative to the result);
-values: exact."""
+values: exact.
+
+The producer kernels (wmx_kv_premix, wmx_kv_mix around the router GEMM)
+against the float64 oracle of kv_pool.py:103-136 / routing.py:108-124 and
+against the torch formulation of the harness on the GPU: the bf16 bar and
+>= 97% of the outputs bit-exact (a premixed row or a mixture summed in
+another order can round one ulp apart, and a logit that moves by one ulp
+moves its whole channel's mixture slightly)."""
 
 import pytest
 import torch
@@ -13,6 +20,7 @@ import torch.nn.functional as F
 from oracle import kv_pool as ref
 from tests.numerics import assert_bf16_close
 from white_matter_amd import kv_pool
+from white_matter_amd.cyclic_pass import FeedbackConfig, FeedbackModel, HipKernels
 
 pytestmark = pytest.mark.gpu
 DEV = "cuda"
@@ -98,3 +106,94 @@ def test_matches_reference_eager_sequence_on_gpu():
     assert torch.equal(values, ev)
     assert_bf16_close(keys.double().cpu(), ek.double().cpu(), what="kv store vs eager")
     assert (keys[:, :, :, slots] == ek[:, :, :, slots]).float().mean() > 0.95
+
+
+def _producer_inputs(batch, tokens, sources, hidden, channels, seed, src_dtype, weight_dtype, scale=1.0):
+    gen = torch.Generator().manual_seed(seed)
+    stacked = (torch.randn(batch, tokens, sources, hidden, generator=gen) * scale).to(src_dtype)
+    pre_mix = (1 + 0.2 * torch.randn(2, sources, hidden, generator=gen)).to(weight_dtype)
+    router = tuple(
+        (
+            (torch.randn(channels * sources, sources * hidden, generator=gen) * 0.5 / (sources * hidden) ** 0.5).bfloat16(),
+            (torch.randn(channels * sources, generator=gen) * 0.25).bfloat16(),
+        )
+        for _ in range(2)
+    )
+    gain = (1 + 0.2 * torch.randn(2, channels, hidden, generator=gen)).to(weight_dtype)
+    return stacked, pre_mix, router, gain
+
+
+def _hip_inputs(stacked, pre_mix, router, gain):
+    with torch.no_grad():
+        return kv_pool.projection_inputs(
+            stacked.to(DEV), tuple(pre_mix.to(DEV)), tuple((w.to(DEV), b.to(DEV)) for w, b in router),
+            tuple(gain.to(DEV)), eps=1e-6, mix_eps=1e-4,
+        )
+
+
+def _producer_close(actual, expected, what):
+    actual, expected = actual.double().cpu(), expected.double().cpu()
+    assert_bf16_close(actual, expected, what=what)
+    assert (actual == expected).double().mean() >= 0.97, what
+
+
+@pytest.mark.parametrize(
+    ("batch", "tokens", "sources", "hidden", "channels"),
+    [(2, 3, 5, 64, 3), (1, 9, 25, 1024, 8), (2, 2, 3, 2056, 11), (1, 1, 1, 8, 1), (3, 2, 40, 520, 17)],
+)
+@pytest.mark.parametrize(
+    ("src_dtype", "weight_dtype"), [(torch.float32, torch.bfloat16), (torch.bfloat16, torch.float32)]
+)
+def test_producer_matches_oracle(batch, tokens, sources, hidden, channels, src_dtype, weight_dtype):
+    inputs = _producer_inputs(batch, tokens, sources, hidden, channels, hidden + sources, src_dtype, weight_dtype)
+    hk, hv = _hip_inputs(*inputs)
+    assert hk.shape == hv.shape == (channels, batch * tokens, hidden) and hk.dtype == torch.bfloat16
+    expected = ref.projection_inputs(*inputs, 1e-6, 1e-4)
+    _producer_close(hk, expected[0], "h_K")
+    _producer_close(hv, expected[1], "h_V")
+
+
+def test_producer_repeated_source_view_and_small_magnitudes():
+    """Sources given as one row per token repeated along S (stride 0: the
+    pool's initial write of the embeddings), at magnitudes where both eps
+    values move the result."""
+    stacked, pre_mix, router, gain = _producer_inputs(2, 5, 7, 256, 4, 1, torch.float32, torch.bfloat16, scale=1e-3)
+    router = tuple((w * 0.05, b * 0.02) for w, b in router)  # mixtures ~1e-2: mean(m^2) ~ mix_eps
+    row = stacked[:, :, :1]
+    hk, hv = _hip_inputs(row.expand(-1, -1, 7, -1), pre_mix, router, gain)
+    expected = ref.projection_inputs(row.expand(-1, -1, 7, -1).contiguous(), pre_mix, router, gain, 1e-6, 1e-4)
+    _producer_close(hk, expected[0], "h_K")
+    _producer_close(hv, expected[1], "h_V")
+
+
+@torch.no_grad()
+def test_producer_matches_torch_formulation_at_c5_width():
+    """The harness's C5 producer (25 sources of 1024, 8 channels) on 8 x 64
+    tokens: the HIP kernels against the same steps as torch operations on
+    the GPU (F.rms_norm, F.linear, matmul), both ending in the projection."""
+    config = FeedbackConfig()
+    model = FeedbackModel(config, device=DEV, seed=2)
+    gen = torch.Generator(device=DEV).manual_seed(5)
+    for side in "kv":  # a router with content weights, not only the prior
+        weight, bias = model.router[side]
+        weight.copy_((torch.randn(weight.shape, generator=gen, device=DEV) * 0.003).bfloat16())
+    stacked = torch.randn(8, 64, config.num_sources, config.hidden_size, generator=gen, device=DEV)
+    eager = model.projection_inputs(stacked)
+    fused = HipKernels.mix(model, stacked)
+    for side, a, e in zip("KV", fused, eager, strict=True):
+        _producer_close(a, e, f"h_{side}")
+    k_fused, v_fused = model.project(stacked, HipKernels)
+    k_eager, v_eager = model.project(stacked)
+    assert_bf16_close(k_fused.double().cpu(), k_eager.double().cpu(), what="projected keys")
+    assert_bf16_close(v_fused.double().cpu(), v_eager.double().cpu(), what="projected values")
+
+
+def test_producer_rejects_autograd_and_bad_shapes():
+    stacked, pre_mix, router, gain = _producer_inputs(1, 2, 3, 64, 2, 0, torch.float32, torch.float32)
+    args = (tuple(pre_mix.to(DEV)), tuple((w.to(DEV), b.to(DEV)) for w, b in router), tuple(gain.to(DEV)))
+    with pytest.raises(RuntimeError, match="forward-only"):
+        kv_pool.projection_inputs(stacked.to(DEV).requires_grad_(), *args)
+    with torch.no_grad(), pytest.raises(ValueError, match="multiples of 8"):
+        kv_pool.projection_inputs(stacked[..., :60].to(DEV), tuple(p[:, :60] for p in args[0]), args[1], args[2])
+    with torch.no_grad(), pytest.raises(ValueError, match="pre_mix"):
+        kv_pool.projection_inputs(stacked[:, :, :2].to(DEV), *args)

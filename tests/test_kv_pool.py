@@ -1,8 +1,13 @@
-"""KV-pool store oracle pinning (CPU) and the fused HIP kernel's argument
-checks. The oracle is checked against the reference's own steps written
-with PyTorch's F.rms_norm and tensor ops in the key dtype
+"""KV-pool oracle pinning (CPU) and the fused HIP kernels' argument checks.
+
+The store oracle is checked against the reference's own steps written with
+PyTorch's F.rms_norm and tensor ops in the key dtype
 (src/white_matter/modules/kv_pool.py:163-172, rotary.py:30-34), and against
-RoPE's rotation invariants."""
+RoPE's rotation invariants. The producer oracle (`projection_inputs`) is
+checked against the reference's formulation of kv_pool.py:103-136 and
+routing.py:108-124 with F.rms_norm, F.linear and einsum, against the closed
+form of the routing prior, and by planted mistakes at magnitudes where both
+eps values matter."""
 
 import math
 
@@ -101,3 +106,94 @@ def test_write_pool_rejects_autograd_and_bad_shapes():
     with torch.no_grad(), pytest.raises(ValueError, match="head_dim"):
         kv_pool.write_pool(torch.randn(1, 1, 1, 2, 32), None, torch.ones(1, 32), torch.ones(1, 2, 32),
                            torch.ones(1, 2, 32), torch.zeros(1, 1, 1, 4, 32, dtype=torch.bfloat16), None, torch.tensor([0, 1]))
+
+
+# ------------------------------------------------------------ producer ----
+def _producer_inputs(seed, batch=2, tokens=3, sources=5, hidden=64, channels=3, scale=1.0, logit_scale=0.25):
+    gen = torch.Generator().manual_seed(seed)
+    stacked = torch.randn(batch, tokens, sources, hidden, generator=gen) * scale
+    pre_mix = (1 + 0.2 * torch.randn(2, sources, hidden, generator=gen)).bfloat16()
+    router = tuple(
+        (
+            (torch.randn(channels * sources, sources * hidden, generator=gen) * 0.02).bfloat16(),
+            (torch.randn(channels * sources, generator=gen) * logit_scale).bfloat16(),
+        )
+        for _ in range(2)
+    )
+    gain = (1 + 0.2 * torch.randn(2, channels, hidden, generator=gen)).bfloat16()
+    return stacked, pre_mix, router, gain
+
+
+def _reference_formulation(stacked, pre_mix, router, gain, eps, mix_eps):
+    """kv_pool.py:103-136 (fused bf16 inference form) with routing.py:108-124,
+    as eager PyTorch evaluates it on the CPU."""
+    batch, tokens, sources, hidden = stacked.shape
+    channels = gain.shape[1]
+    normed = F.rms_norm(stacked.float(), (hidden,), None, eps)
+    out = []
+    for side in range(2):
+        premixed = (normed * pre_mix[side].float()).bfloat16()  # _premix
+        weight, bias = router[side]
+        logits = F.linear(premixed.reshape(batch, tokens, sources * hidden), weight, bias)
+        logits = logits.view(batch, tokens, channels, sources)
+        mixed = torch.einsum("btld,btkl->btkd", premixed, logits)
+        mixed = F.rms_norm(mixed.float(), (hidden,), None, mix_eps)
+        h = (mixed * gain[side].float()).bfloat16()  # _projection_input
+        out.append(h.permute(2, 0, 1, 3).flatten(1, 2))
+    return torch.stack(out).double()
+
+
+def _close_in_bf16(actual, expected, share=0.97):
+    """Equal but for rare roundings of a bf16 step that land on the other
+    side (sums taken in another order): within 2 bf16 ulps of the result."""
+    ulp = expected.abs().clamp_min(2**-126) * 2**-7
+    return bool(((actual - expected).abs() <= 2 * ulp).all()) and float((actual == expected).double().mean()) > share
+
+
+@pytest.mark.parametrize(
+    ("scale", "logit_scale"),
+    [(1.0, 0.25), (1e-3, 0.25), (1.0, 0.004), (1e-3, 0.004)],  # small magnitudes: both eps values matter
+)
+def test_producer_oracle_matches_reference_formulation(scale, logit_scale):
+    inputs = _producer_inputs(3, scale=scale, logit_scale=logit_scale)
+    expected = _reference_formulation(*inputs, 1e-6, 1e-4)
+    actual = ref.projection_inputs(*inputs, 1e-6, 1e-4)
+    assert actual.shape == (2, 3, 6, 64)
+    assert _close_in_bf16(actual, expected)
+
+
+def test_producer_oracle_routing_prior_closed_form():
+    """The reference's "cyclic" prior with C = S and zero router weights
+    (routing.py:9-25, 77-80): channel c reads source c with logit 2^-2, so
+    the mixture is p_c / 4 exactly and its mix norm p_c / sqrt(mean(p_c^2) +
+    16 mix_eps)."""
+    channels = sources = 4
+    stacked, pre_mix, _, gain = _producer_inputs(9, sources=sources, channels=channels, scale=0.01)
+    bias = torch.zeros(channels, sources)
+    bias[torch.arange(channels), torch.arange(channels)] = 0.25
+    router = tuple((torch.zeros(channels * sources, sources * 64).bfloat16(), bias.reshape(-1).bfloat16()) for _ in range(2))
+    eps, mix_eps = 1e-6, 1e-2  # a large mix eps, so that a mix norm that misses the 1/4 shows
+    actual = ref.projection_inputs(stacked, pre_mix, router, gain, eps, mix_eps)
+    x = stacked.double()
+    normed = x / torch.sqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    for side in range(2):
+        p = (normed * pre_mix[side].double()).bfloat16().double()  # (B, T, S, H)
+        expected = p / torch.sqrt(p.pow(2).mean(-1, keepdim=True) + 16 * mix_eps) * gain[side].double()[None, None]
+        expected = expected.bfloat16().double().permute(2, 0, 1, 3).reshape(channels, -1, 64)
+        assert _close_in_bf16(actual[side], expected, share=0.99)
+
+
+def test_producer_planted_mistakes_are_caught():
+    """The two eps exchanged, or the logits read source-major (c + C*s for
+    c*S + s): each fails the check above."""
+    inputs = _producer_inputs(4, scale=1e-3, logit_scale=0.004)
+    expected = _reference_formulation(*inputs, 1e-6, 1e-4)
+    assert not _close_in_bf16(ref.projection_inputs(*inputs, 1e-4, 1e-6), expected)
+    stacked, pre_mix, router, gain = inputs
+    channels, sources = gain.shape[1], stacked.shape[2]
+    transposed = tuple(
+        (w.view(channels, sources, -1).transpose(0, 1).reshape(channels * sources, -1),
+         b.view(channels, sources).t().reshape(-1))
+        for w, b in router
+    )
+    assert not _close_in_bf16(ref.projection_inputs(stacked, pre_mix, transposed, gain, 1e-6, 1e-4), expected)

@@ -19,7 +19,7 @@ import torch
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
 # the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
 OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -117,6 +117,37 @@ class DecodeArgs(ctypes.Structure):
 
 _c_i64_4 = ctypes.c_int64 * 4
 DTYPE_F32, DTYPE_BF16 = 0, 1
+
+
+_vp2 = _vp * 2
+
+
+class KvMixArgs(ctypes.Structure):
+    """Mirror of wmx_kv_mix_args (index 0 of each pair: the K side, 1: V)."""
+
+    _fields_ = [
+        ("sources", _vp),
+        ("source_stride", _c_i64_3),
+        ("pre_mix", _vp2),
+        ("premixed", _vp2),
+        ("alpha", _vp2),
+        ("alpha_stride", ctypes.c_int64),
+        ("gain", _vp2),
+        ("mixed", _vp2),
+        ("source_dtype", ctypes.c_int32),
+        ("weight_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("tokens", ctypes.c_int32),
+        ("num_sources", ctypes.c_int32),
+        ("hidden", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+        ("mix_eps", ctypes.c_float),
+    ]
+
+
+KV_MIX_MAX_SOURCES = 512
+KV_MIX_MAX_HIDDEN = 4096
 
 
 class KvStoreArgs(ctypes.Structure):
@@ -223,6 +254,9 @@ EXPORTS = (
     "wmx_decode_noalloc",
     "wmx_kv_store_args_size",
     "wmx_kv_pool_store",
+    "wmx_kv_mix_args_size",
+    "wmx_kv_premix",
+    "wmx_kv_mix",
     "wmx_strict_meta_args_size",
     "wmx_strict_meta_workspace_size",
     "wmx_strict_meta_count",
@@ -266,6 +300,10 @@ def load() -> ctypes.CDLL:
     lib.wmx_kv_store_args_size.restype = ctypes.c_size_t
     lib.wmx_kv_pool_store.argtypes = [ctypes.POINTER(KvStoreArgs), _vp]
     lib.wmx_kv_pool_store.restype = ctypes.c_int
+    lib.wmx_kv_mix_args_size.restype = ctypes.c_size_t
+    for name in ("wmx_kv_premix", "wmx_kv_mix"):
+        getattr(lib, name).argtypes = [ctypes.POINTER(KvMixArgs), _vp]
+        getattr(lib, name).restype = ctypes.c_int
     lib.wmx_strict_meta_args_size.restype = ctypes.c_size_t
     lib.wmx_strict_meta_workspace_size.argtypes = [ctypes.POINTER(StrictMetaArgs)]
     lib.wmx_strict_meta_workspace_size.restype = ctypes.c_int64
@@ -287,6 +325,8 @@ def load() -> ctypes.CDLL:
         raise RuntimeError("wmx_decode_args layout differs between the library and the binding")
     if lib.wmx_kv_store_args_size() != ctypes.sizeof(KvStoreArgs):
         raise RuntimeError("wmx_kv_store_args layout differs between the library and the binding")
+    if lib.wmx_kv_mix_args_size() != ctypes.sizeof(KvMixArgs):
+        raise RuntimeError("wmx_kv_mix_args layout differs between the library and the binding")
     if lib.wmx_feedback_meta_args_size() != ctypes.sizeof(FeedbackMetaArgs):
         raise RuntimeError("wmx_feedback_meta_args layout differs between the library and the binding")
     if lib.wmx_strict_meta_args_size() != ctypes.sizeof(StrictMetaArgs):
@@ -379,6 +419,16 @@ def decode_noalloc(args: DecodeArgs, device: torch.device) -> None:
 def kv_pool_store(args: KvStoreArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_kv_pool_store(ctypes.byref(args), _stream(device)), "wmx_kv_pool_store")
+
+
+def kv_premix(args: KvMixArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_kv_premix(ctypes.byref(args), _stream(device)), "wmx_kv_premix")
+
+
+def kv_mix(args: KvMixArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_kv_mix(ctypes.byref(args), _stream(device)), "wmx_kv_mix")
 
 
 def strict_meta_workspace_size(args: StrictMetaArgs) -> int:

@@ -274,7 +274,49 @@ int wmx_kv_pool_store(const wmx_kv_store_args* a, void* stream) {
   return launched(wmx::launch_kv_store(*a, (hipStream_t)stream));
 }
 
+static int check_kv_mix(const wmx_kv_mix_args* a, bool premix) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->batch < 0 || a->tokens < 0) return fail(WMX_E_INVALID, "negative shape");
+  if (a->num_sources < 1 || a->num_sources > WMX_KV_MIX_MAX_SOURCES)
+    return fail(WMX_E_UNSUPPORTED, "kv mix num_sources %d is not in [1, %d]", a->num_sources, WMX_KV_MIX_MAX_SOURCES);
+  if (a->hidden < 8 || a->hidden % 8 || a->hidden > WMX_KV_MIX_MAX_HIDDEN)
+    return fail(WMX_E_UNSUPPORTED, "kv mix hidden %d is not a multiple of 8 in [8, %d]", a->hidden, WMX_KV_MIX_MAX_HIDDEN);
+  if (a->channels < 1) return fail(WMX_E_INVALID, "kv mix channels must be >= 1");
+  for (int dt : {a->source_dtype, a->weight_dtype})
+    if (dt != WMX_DTYPE_F32 && dt != WMX_DTYPE_BF16) return fail(WMX_E_INVALID, "dtype must be WMX_DTYPE_F32 or WMX_DTYPE_BF16");
+  if (!(a->eps >= 0.f) || !(a->mix_eps >= 0.f)) return fail(WMX_E_INVALID, "eps and mix_eps must be >= 0");
+  if ((int64_t)a->batch * a->tokens == 0) return WMX_OK;
+  for (int side = 0; side < 2; ++side) {
+    if (!a->premixed[side]) return fail(WMX_E_INVALID, "kv mix pointer is NULL");
+    if (premix ? !a->pre_mix[side] : (!a->alpha[side] || !a->gain[side] || !a->mixed[side]))
+      return fail(WMX_E_INVALID, "kv mix pointer is NULL");
+    if (!aligned16(a->premixed[side]) || !aligned16(a->pre_mix[side]) || !aligned16(a->gain[side]) ||
+        !aligned16(a->mixed[side]) || ((uintptr_t)a->alpha[side] & 1u))
+      return fail(WMX_E_INVALID, "kv mix operands must be 16-byte aligned (alpha 2-byte)");
+  }
+  return WMX_OK;
+}
+
+int wmx_kv_premix(const wmx_kv_mix_args* a, void* stream) {
+  int rc = check_kv_mix(a, true);
+  if (rc != WMX_OK || (int64_t)a->batch * a->tokens == 0) return rc;
+  if (!a->sources) return fail(WMX_E_INVALID, "kv mix sources is NULL");
+  if (!aligned16(a->sources) || !strides_vec8(a->source_stride, 3))
+    return fail(WMX_E_INVALID, "kv mix sources must be 16-byte aligned with strides of multiples of 8 elements");
+  return launched(wmx::launch_kv_premix(*a, (hipStream_t)stream));
+}
+
+int wmx_kv_mix(const wmx_kv_mix_args* a, void* stream) {
+  int rc = check_kv_mix(a, false);
+  if (rc != WMX_OK || (int64_t)a->batch * a->tokens == 0) return rc;
+  if (a->alpha_stride < (int64_t)a->channels * a->num_sources)
+    return fail(WMX_E_INVALID, "kv mix alpha_stride must cover the C*S logits of a token");
+  return launched(wmx::launch_kv_mix(*a, (hipStream_t)stream));
+}
+
 size_t wmx_kv_store_args_size(void) { return sizeof(wmx_kv_store_args); }
+
+size_t wmx_kv_mix_args_size(void) { return sizeof(wmx_kv_mix_args); }
 
 size_t wmx_strict_meta_args_size(void) { return sizeof(wmx_strict_meta_args); }
 

@@ -1,0 +1,240 @@
+// KV-pool producer for gfx950: the token-local steps ahead of the per-channel
+// projection (reference modules/kv_pool.py:97-160 `_project`,
+// modules/routing.py:77-124 `Router`, `_RoutedMixer`). Between the two
+// kernels the router logits are one plain GEMM of the premixed rows, left to
+// the BLAS library.
+//
+//   premix: every source row of a token is RMS-normalised and scaled by the
+//           K-side and the V-side pre-mix weights, rounded to bf16: the
+//           router's input and the mixture's operand (one wave per row, both
+//           sides from one read of the row);
+//   mix:    per token, side and channel the routed sum over the sources,
+//           rounded to bf16, RMS-normalised with the mix eps, scaled by the
+//           channel gain and rounded to bf16, written in the projection's
+//           input layout (channel, token, hidden) (one workgroup per token,
+//           side and group of 8 channels; the token's premixed rows are read
+//           once for all the group's channels).
+//
+// Both are HBM-bound: per token the sources are read once, the premixed rows
+// written once and read twice (the GEMM and the mixture), the channels
+// written once. The eager sequence materialises the normalised sources, both
+// premixed stacks, the mixtures, their normalisation and the gained copies.
+#include "wmx_kernels.h"
+
+namespace wmx {
+
+namespace {
+
+// Four consecutive elements as fp32 from an fp32 or bf16 array.
+__device__ __forceinline__ void load4(const void* base, int64_t off, bool bf16_src, float (&v)[4]) {
+  if (bf16_src) {
+    const u32x2 w = *reinterpret_cast<const u32x2*>((const bf16*)base + off);
+    v[0] = bf16_lo(w[0]);
+    v[1] = bf16_hi(w[0]);
+    v[2] = bf16_lo(w[1]);
+    v[3] = bf16_hi(w[1]);
+  } else {
+    const f32x4 x = *reinterpret_cast<const f32x4*>((const float*)base + off);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) v[e] = x[e];
+  }
+}
+
+// Eight fp32 values to eight bf16 at base + off (a plain store: the rows are
+// read again soon).
+__device__ __forceinline__ void store8_bf16_cached(void* base, int64_t off, const float (&v)[8]) {
+  const u32x4 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                   pack_bf16x2(v[6], v[7])};
+  *reinterpret_cast<u32x4*>((bf16*)base + off) = w;
+}
+
+constexpr int kMixChannels = 8;  // channels per mix workgroup
+constexpr int kMixBatch = 8;     // source rows whose loads are in flight together
+
+}  // namespace
+
+// One wave per (token, source) row; lane l holds elements 512 c + 8 l + [0, 8)
+// for c < CH (hidden <= 512 CH). Arithmetic in fp32 whatever the source
+// dtype (the pool's fp32 residual policy): y = x * (1 / sqrt(mean(x^2) + eps)),
+// p_side = bf16(y * w_side[s]).
+template <int CH, bool SRC_BF16, bool W_BF16>
+__global__ __launch_bounds__(256) void kv_premix_kernel(const wmx_kv_mix_args a, int64_t rows) {
+#pragma clang fp contract(off)
+  const int64_t r = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (r >= rows) return;  // wave-uniform
+  const int lane = threadIdx.x & 63;
+  const int s = (int)(r % a.num_sources);
+  const int64_t n = r / a.num_sources;
+  const int t = (int)(n % a.tokens), b = (int)(n / a.tokens);
+  const int64_t src = (int64_t)b * a.source_stride[0] + (int64_t)t * a.source_stride[1] + (int64_t)s * a.source_stride[2];
+  float x[CH][8];
+  float ss = 0.f;
+#pragma unroll
+  for (int c = 0; c < CH; ++c) {
+    const int d0 = 512 * c + 8 * lane;
+    if (d0 < a.hidden) {
+      load8(a.sources, src + d0, SRC_BF16, x[c]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) ss = fmaf(x[c][e], x[c][e], ss);
+    }
+  }
+#pragma unroll
+  for (int o = 32; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+  const float inv = 1.f / sqrtf(ss / (float)a.hidden + a.eps);
+  const int64_t out = (n * a.num_sources + s) * a.hidden;
+#pragma unroll
+  for (int side = 0; side < 2; ++side) {
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int d0 = 512 * c + 8 * lane;
+      if (d0 < a.hidden) {
+        float w[8], y[8];
+        load8(a.pre_mix[side], (int64_t)s * a.hidden + d0, W_BF16, w);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = (x[c][e] * inv) * w[e];
+        store8_bf16_cached(a.premixed[side], out + d0, y);
+      }
+    }
+  }
+}
+
+// Workgroup (token n, side, channel group); thread i holds elements
+// 1024 c + 4 i + [0, 4) for c < CH (hidden <= 1024 CH). For each channel j of
+// the group: m = bf16(sum over s ascending of alpha[n, j, s] * p[n, s, :])
+// (fp32 products and sums), then out = bf16((m * (1 / sqrt(mean(m^2) +
+// mix_eps))) * gain[j]).
+template <int CH, bool W_BF16>
+__global__ __launch_bounds__(256) void kv_mix_kernel(const wmx_kv_mix_args a) {
+#pragma clang fp contract(off)
+  __shared__ float alpha_lds[kMixChannels * WMX_KV_MIX_MAX_SOURCES];
+  __shared__ float red[4][kMixChannels];
+  const int64_t n = blockIdx.x;
+  const int side = blockIdx.y;
+  const int c0 = blockIdx.z * kMixChannels;
+  const int nc = min(kMixChannels, a.channels - c0);
+  const int S = a.num_sources, H = a.hidden;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  // this group's logits: channels c0 .. c0 + nc - 1 are contiguous rows of S
+  const bf16* alpha = (const bf16*)a.alpha[side] + n * a.alpha_stride + (int64_t)c0 * S;
+  for (int i = tid; i < nc * S; i += 256) alpha_lds[i] = (float)alpha[i];
+  __syncthreads();
+
+  float acc[kMixChannels][CH][4];
+#pragma unroll
+  for (int j = 0; j < kMixChannels; ++j)
+#pragma unroll
+    for (int c = 0; c < CH; ++c)
+#pragma unroll
+      for (int e = 0; e < 4; ++e) acc[j][c][e] = 0.f;
+  const bf16* p = (const bf16*)a.premixed[side] + n * S * H;
+  for (int s0 = 0; s0 < S; s0 += kMixBatch) {
+    float pv[kMixBatch][CH][4];
+#pragma unroll
+    for (int u = 0; u < kMixBatch; ++u) {
+#pragma unroll
+      for (int c = 0; c < CH; ++c) {
+        const int d0 = 1024 * c + 4 * tid;
+        if (s0 + u < S && d0 < H) {
+          load4(p, (int64_t)(s0 + u) * H + d0, true, pv[u][c]);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pv[u][c][e] = 0.f;
+        }
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kMixBatch; ++u) {
+      if (s0 + u < S) {
+#pragma unroll
+        for (int j = 0; j < kMixChannels; ++j) {
+          if (j < nc) {
+            const float al = alpha_lds[j * S + s0 + u];
+#pragma unroll
+            for (int c = 0; c < CH; ++c)
+#pragma unroll
+              for (int e = 0; e < 4; ++e) acc[j][c][e] = fmaf(al, pv[u][c][e], acc[j][c][e]);
+          }
+        }
+      }
+    }
+  }
+
+  float ss[kMixChannels];
+#pragma unroll
+  for (int j = 0; j < kMixChannels; ++j) {
+    ss[j] = 0.f;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const bool in = 1024 * c + 4 * tid < H;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const float m = in ? round_bf16(acc[j][c][e]) : 0.f;
+        acc[j][c][e] = m;
+        ss[j] = fmaf(m, m, ss[j]);
+      }
+    }
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) ss[j] += __shfl_xor(ss[j], o);
+    if (lane == 0) red[w][j] = ss[j];
+  }
+  __syncthreads();
+  const int64_t tokens_total = (int64_t)a.batch * a.tokens;
+#pragma unroll
+  for (int j = 0; j < kMixChannels; ++j) {
+    if (j >= nc) break;
+    const float total = red[0][j] + red[1][j] + red[2][j] + red[3][j];
+    const float inv = 1.f / sqrtf(total / (float)H + a.mix_eps);
+    const int64_t row = ((int64_t)(c0 + j) * tokens_total + n) * H;
+#pragma unroll
+    for (int c = 0; c < CH; ++c) {
+      const int d0 = 1024 * c + 4 * tid;
+      if (d0 < H) {
+        float g[4];
+        load4(a.gain[side], (int64_t)(c0 + j) * H + d0, W_BF16, g);
+        const u32x2 o = {pack_bf16x2((acc[j][c][0] * inv) * g[0], (acc[j][c][1] * inv) * g[1]),
+                         pack_bf16x2((acc[j][c][2] * inv) * g[2], (acc[j][c][3] * inv) * g[3])};
+        *reinterpret_cast<u32x2*>((bf16*)a.mixed[side] + row + d0) = o;
+      }
+    }
+  }
+}
+
+template <int CH>
+static void launch_premix_ch(const wmx_kv_mix_args& a, int64_t rows, hipStream_t stream) {
+  const dim3 grid((unsigned)((rows + 3) / 4));
+  const bool sb = a.source_dtype == WMX_DTYPE_BF16, wb = a.weight_dtype == WMX_DTYPE_BF16;
+  if (sb && wb) hipLaunchKernelGGL((kv_premix_kernel<CH, true, true>), grid, dim3(256), 0, stream, a, rows);
+  else if (sb) hipLaunchKernelGGL((kv_premix_kernel<CH, true, false>), grid, dim3(256), 0, stream, a, rows);
+  else if (wb) hipLaunchKernelGGL((kv_premix_kernel<CH, false, true>), grid, dim3(256), 0, stream, a, rows);
+  else hipLaunchKernelGGL((kv_premix_kernel<CH, false, false>), grid, dim3(256), 0, stream, a, rows);
+}
+
+int launch_kv_premix(const wmx_kv_mix_args& a, hipStream_t stream) {
+  const int64_t rows = (int64_t)a.batch * a.tokens * a.num_sources;
+  if (rows == 0) return WMX_OK;
+  if ((rows + 3) / 4 > UINT32_MAX) return WMX_E_UNSUPPORTED;
+  if (a.hidden <= 512) launch_premix_ch<1>(a, rows, stream);
+  else if (a.hidden <= 1024) launch_premix_ch<2>(a, rows, stream);
+  else if (a.hidden <= 2048) launch_premix_ch<4>(a, rows, stream);
+  else launch_premix_ch<8>(a, rows, stream);
+  return WMX_OK;
+}
+
+template <int CH>
+static void launch_mix_ch(const wmx_kv_mix_args& a, dim3 grid, hipStream_t stream) {
+  if (a.weight_dtype == WMX_DTYPE_BF16) hipLaunchKernelGGL((kv_mix_kernel<CH, true>), grid, dim3(256), 0, stream, a);
+  else hipLaunchKernelGGL((kv_mix_kernel<CH, false>), grid, dim3(256), 0, stream, a);
+}
+
+int launch_kv_mix(const wmx_kv_mix_args& a, hipStream_t stream) {
+  const int64_t tokens = (int64_t)a.batch * a.tokens;
+  if (tokens == 0) return WMX_OK;
+  if (tokens > UINT32_MAX) return WMX_E_UNSUPPORTED;
+  const dim3 grid((unsigned)tokens, 2, (unsigned)((a.channels + kMixChannels - 1) / kMixChannels));
+  if (a.hidden <= 1024) launch_mix_ch<1>(a, grid, stream);
+  else if (a.hidden <= 2048) launch_mix_ch<2>(a, grid, stream);
+  else launch_mix_ch<4>(a, grid, stream);
+  return WMX_OK;
+}
+
+}  // namespace wmx

@@ -7,45 +7,6 @@
 
 namespace wmx {
 
-namespace {
-
-// Round to bf16 (nearest even) and back: the reference's per-op rounding
-// when the keys are bf16.
-__device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
-
-// Eight consecutive elements as fp32 from an fp32 or bf16 array. STREAM marks
-// data read exactly once (the keys and values): a non-temporal load, which
-// keeps it from displacing the cos/sin rows that every channel re-reads.
-template <bool STREAM = false>
-__device__ __forceinline__ void load8(const void* base, int64_t off, bool bf16_src, float (&v)[8]) {
-  auto ld = [](const auto* p) { return STREAM ? __builtin_nontemporal_load(p) : *p; };
-  if (bf16_src) {
-    const u32x4 w = ld(reinterpret_cast<const u32x4*>((const bf16*)base + off));
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[2 * e] = bf16_lo(w[e]);
-      v[2 * e + 1] = bf16_hi(w[e]);
-    }
-  } else {
-    const f32x4 a = ld(reinterpret_cast<const f32x4*>((const float*)base + off));
-    const f32x4 b = ld(reinterpret_cast<const f32x4*>((const float*)base + off + 4));
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      v[e] = a[e];
-      v[4 + e] = b[e];
-    }
-  }
-}
-
-// Pool rows are written once and not read back by this kernel: non-temporal.
-__device__ __forceinline__ void store8_bf16(void* base, int64_t off, const float (&v)[8]) {
-  const u32x4 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
-                   pack_bf16x2(v[6], v[7])};
-  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>((bf16*)base + off));
-}
-
-}  // namespace
-
 // Value source: none (keys only), fp32 or bf16.
 enum ValueKind { kNoValue = 0, kValueF32 = 1, kValueBF16 = 2 };
 

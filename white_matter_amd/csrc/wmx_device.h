@@ -56,6 +56,43 @@ __device__ __forceinline__ bf16x8 as_bf16x8(const u32x4& v) { return __builtin_b
 __device__ __forceinline__ u32x4 load16(const bf16* p) { return *reinterpret_cast<const u32x4*>(p); }
 __device__ __forceinline__ void store8(bf16* p, const u32x2& v) { *reinterpret_cast<u32x2*>(p) = v; }
 
+// -- row helpers of the HBM-bound kernels (KV-pool producer and store) --
+// Round to bf16 (nearest even) and back: the reference's per-op rounding
+// when the keys are bf16.
+__device__ __forceinline__ float round_bf16(float x) { return (float)(__bf16)x; }
+
+// Eight consecutive elements as fp32 from an fp32 or bf16 array. STREAM marks
+// data read exactly once (the keys and values): a non-temporal load, which
+// keeps it from displacing the cos/sin rows that every channel re-reads.
+template <bool STREAM = false>
+__device__ __forceinline__ void load8(const void* base, int64_t off, bool bf16_src, float (&v)[8]) {
+  auto ld = [](const auto* p) { return STREAM ? __builtin_nontemporal_load(p) : *p; };
+  if (bf16_src) {
+    const u32x4 w = ld(reinterpret_cast<const u32x4*>((const bf16*)base + off));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[2 * e] = bf16_lo(w[e]);
+      v[2 * e + 1] = bf16_hi(w[e]);
+    }
+  } else {
+    const f32x4 a = ld(reinterpret_cast<const f32x4*>((const float*)base + off));
+    const f32x4 b = ld(reinterpret_cast<const f32x4*>((const float*)base + off + 4));
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      v[e] = a[e];
+      v[4 + e] = b[e];
+    }
+  }
+}
+
+// Pool rows are written once and not read back by this kernel: non-temporal.
+__device__ __forceinline__ void store8_bf16(void* base, int64_t off, const float (&v)[8]) {
+  const u32x4 w = {pack_bf16x2(v[0], v[1]), pack_bf16x2(v[2], v[3]), pack_bf16x2(v[4], v[5]),
+                   pack_bf16x2(v[6], v[7])};
+  __builtin_nontemporal_store(w, reinterpret_cast<u32x4*>((bf16*)base + off));
+}
+
+
 // Reductions across the two halves of a wave (lane l with lane l ^ 32),
 // with v_permlane32_swap: the two results hold x[l] and x[l ^ 32] in some order.
 __device__ __forceinline__ float max_halves(float x) {

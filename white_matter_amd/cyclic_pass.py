@@ -18,8 +18,10 @@ Inference restatement of the reference's feedback block:
   * the pool projection (modules/kv_pool.py:97-217 `KVPool._project`,
     `project_sequence`; modules/routing.py:46-124 `Router`, `_RoutedMixer`):
     RMS norm, per-source premix, content routers over all L+1 sources, mix
-    norm, gains and the per-channel projection; the K-norm, RoPE, bf16 cast
-    and pool write run as one HIP kernel (`kv_pool.write_pool`);
+    norm, gains and the per-channel projection: the norms, premix, routed
+    sum and gains run as two HIP kernels around the router GEMM
+    (`kv_pool.projection_inputs`), the K-norm, RoPE, bf16 cast and pool write
+    as one (`kv_pool.write_pool`);
   * cached decoding (models/generation.py:38-100 `DecodeGraph`,
     blocks/white_matter.py:165-186 `_run_token_layers`): one token through
     every layer with the split-K decode kernel over the pool, the token's
@@ -94,6 +96,15 @@ class HipKernels:
     @staticmethod
     def store(key, value, k_norm_weight, cos, sin, keys, values, slots, *, eps):
         kv_pool.write_pool(key, value, k_norm_weight, cos, sin, keys, values, slots, eps=eps)
+
+    @staticmethod
+    def mix(model: "FeedbackModel", stacked):
+        """The projection inputs (k, B T, d) per side on the HIP kernels."""
+        c = model.config
+        return kv_pool.projection_inputs(
+            stacked, (model.pre_mix["k"], model.pre_mix["v"]), (model.router["k"], model.router["v"]),
+            (model.gain["k"], model.gain["v"]), eps=c.rms_norm_eps, mix_eps=c.mix_norm_eps,
+        )
 
 
 def _rotate_half(x: torch.Tensor) -> torch.Tensor:
@@ -204,9 +215,10 @@ class FeedbackModel:
         states.append(x)
         return x, states
 
-    def project(self, stacked: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
-        """KVPool._project (kv_pool.py:97-160): (B, T, S, d) sources -> raw keys
-        and values (B, k, Hkv, T, D) in the activation dtype (views)."""
+    def projection_inputs(self, stacked: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+        """KVPool._project up to the projection (kv_pool.py:97-136, routing.py:
+        108-124) as torch operations: (B, T, S, d) sources -> the K and V
+        projection inputs (k, B T, d) in the activation dtype."""
         c = self.config
         batch, length, sources, d = stacked.shape
         normed = F.rms_norm(stacked.to(self.residual_dtype), (d,), None, c.rms_norm_eps)
@@ -219,8 +231,21 @@ class FeedbackModel:
             mixed = torch.matmul(alpha, premixed)  # (B, T, k, d): sum over sources
             mixed = F.rms_norm(mixed.to(self.residual_dtype), (d,), None, c.mix_norm_eps)
             mixed = (mixed * self.gain[side].to(self.residual_dtype)).to(self.dtype)
-            rows = mixed.permute(2, 0, 1, 3).reshape(c.num_kv_channels, batch * length, d)
-            proj = torch.bmm(rows, self.proj[side])  # (k, B T, Hkv D)
+            out.append(mixed.permute(2, 0, 1, 3).reshape(c.num_kv_channels, batch * length, d))
+        return out[0], out[1]
+
+    def project(self, stacked: torch.Tensor, kernels=None) -> tuple[torch.Tensor, torch.Tensor]:
+        """KVPool._project (kv_pool.py:97-160): (B, T, S, d) sources -> raw keys
+        and values (B, k, Hkv, T, D) in the activation dtype (views). The
+        projection inputs come from `kernels.mix` where the kernel set has one
+        (the HIP producer), else from the torch operations."""
+        c = self.config
+        batch, length = stacked.shape[:2]
+        mix = getattr(kernels, "mix", None)
+        rows = mix(self, stacked) if mix is not None else self.projection_inputs(stacked)
+        out = []
+        for side, r in zip("kv", rows, strict=True):
+            proj = torch.bmm(r, self.proj[side])  # (k, B T, Hkv D)
             out.append(
                 proj.view(c.num_kv_channels, batch, length, c.num_kv_heads, c.head_dim).permute(1, 0, 3, 2, 4)
             )
@@ -245,7 +270,7 @@ def write_sources(model: FeedbackModel, stacked, keys, values, slots, rope, kern
     cos, sin = rope
     for start in range(0, stacked.shape[1], chunk):
         stop = min(start + chunk, stacked.shape[1])
-        key, value = model.project(stacked[:, start:stop])
+        key, value = model.project(stacked[:, start:stop], kernels)
         kernels.store(
             key, value, model.k_norm, cos[:, start:stop], sin[:, start:stop], keys, values, slots[start:stop],
             eps=model.config.rms_norm_eps,
@@ -409,7 +434,7 @@ class GreedyDecoder:
 
         x, states = model.layers_forward(x, attend, rope)
         slot = self.length
-        key, value = model.project(torch.stack(states, dim=2))
+        key, value = model.project(torch.stack(states, dim=2), self.kernels)
         self.kernels.store(key, value, model.k_norm, rope[0], rope[1], self.keys, self.values, slot,
                            eps=c.rms_norm_eps)
         self.key_mask.index_fill_(1, slot, True)

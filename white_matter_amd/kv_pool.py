@@ -1,4 +1,15 @@
-"""Fused KV-pool store: key norm, RoPE, casts and the pool write in one pass.
+"""The KV-pool producer on the HIP kernels: the token-local mixing ahead of the
+per-channel projection, and the fused store (key norm, RoPE, casts and the
+pool write in one pass).
+
+The reference builds the projection's inputs with an eager sequence
+(src/white_matter/modules/kv_pool.py:97-136 `KVPool._project`, its bf16
+inference form; modules/routing.py:77-124 `Router`, `_RoutedMixer`): an RMS
+norm of every source row, the K- and V-side pre-mix products cast to bf16,
+a router linear over the premixed row, the routed sum over the sources, the
+mix norm and the channel gain cast to bf16 and permuted to (channel, token,
+hidden). `projection_inputs` runs that as two HIP kernels (wmx_kv_premix,
+wmx_kv_mix) around the router GEMM, which stays a library GEMM (F.linear).
 
 The reference produces a group's keys with an eager sequence
 (src/white_matter/modules/kv_pool.py:163-172 `_apply_k_norm_rope`, the
@@ -14,6 +25,7 @@ sequence (differentiable) remains the path.
 from __future__ import annotations
 
 import torch
+import torch.nn.functional as F
 
 from . import _native
 
@@ -103,3 +115,92 @@ def k_norm_rope(key: torch.Tensor, k_norm_weight: torch.Tensor, cos: torch.Tenso
     slots = torch.arange(key.shape[3], device=key.device)
     write_pool(key, None, k_norm_weight, cos, sin, out, None, slots, eps=eps)
     return out
+
+
+def _weights(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
+    return t.to(dtype).contiguous()
+
+
+def projection_inputs(
+    stacked: torch.Tensor,
+    pre_mix: tuple[torch.Tensor, torch.Tensor],
+    router: tuple[tuple[torch.Tensor, torch.Tensor], tuple[torch.Tensor, torch.Tensor]],
+    gain: tuple[torch.Tensor, torch.Tensor],
+    *,
+    eps: float = 1e-6,
+    mix_eps: float = 1e-4,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """(h_K, h_V), each (C, B*T, hidden) bf16: the inputs of the per-channel
+    K and V projections (reference kv_pool.py:103-136 with its fused bf16
+    casts, and routing.py:108-124 with the router reading every source).
+
+    stacked (B, T, S, hidden) float32 or bfloat16 (stride 0 along S repeats
+    one row); pre_mix (K, V) weights (S, hidden); router ((W_K, b_K), (W_V,
+    b_V)) with W (C*S, S*hidden) and b (C*S,), the logits of channel c and
+    source s at c*S + s; gain (K, V) (C, hidden). Per side:
+      p = bf16(rms_norm(x, eps) * pre_mix)           (HIP, wmx_kv_premix)
+      alpha = F.linear(p, W, b) in bf16                (library GEMM)
+      m = bf16(sum_s alpha[c, s] * p[s])               (HIP, wmx_kv_mix)
+      h = bf16(rms_norm(m, mix_eps) * gain[c])
+    Forward only (the reference's training form runs under checkpointing).
+    """
+    if torch.is_grad_enabled() and any(
+        t.requires_grad for t in (stacked, *pre_mix, *gain, *router[0], *router[1])
+    ):
+        raise RuntimeError("projection_inputs is forward-only; use the reference's eager sequence under autograd")
+    if stacked.ndim != 4:
+        raise ValueError("stacked must be (B, T, S, hidden)")
+    batch, tokens, sources, hidden = stacked.shape
+    if not stacked.is_cuda:
+        raise RuntimeError("projection_inputs runs on the HIP kernels: stacked must be a GPU tensor")
+    if stacked.dtype not in _DTYPES:
+        raise TypeError(f"stacked must be float32 or bfloat16, got {stacked.dtype}")
+    if sources > _native.KV_MIX_MAX_SOURCES or hidden % 8 or hidden > _native.KV_MIX_MAX_HIDDEN:
+        raise ValueError(
+            f"projection_inputs supports up to {_native.KV_MIX_MAX_SOURCES} sources and hidden sizes that are "
+            f"multiples of 8 up to {_native.KV_MIX_MAX_HIDDEN}"
+        )
+    channels = gain[0].shape[0]
+    for w in pre_mix:
+        if w.shape != (sources, hidden):
+            raise ValueError("pre_mix weights must be (S, hidden)")
+    for g in gain:
+        if g.shape != (channels, hidden):
+            raise ValueError("gains must be (C, hidden), one shape for both sides")
+    for weight, bias in router:
+        if weight.shape != (channels * sources, sources * hidden) or bias.shape != (channels * sources,):
+            raise ValueError("router weights must be (C*S, S*hidden) with a (C*S,) bias")
+    device = stacked.device
+    ok = stacked.stride(-1) == 1 and stacked.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in stacked.stride()[:3])
+    x = stacked if ok else stacked.contiguous()
+    wdtype = torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in (*pre_mix, *gain)) else torch.float32
+    pre = [_weights(w, wdtype) for w in pre_mix]
+    gains = [_weights(g, wdtype) for g in gain]
+    rows = batch * tokens
+    premixed = torch.empty(2, rows, sources * hidden, device=device, dtype=torch.bfloat16)
+    mixed = torch.empty(2, channels, rows, hidden, device=device, dtype=torch.bfloat16)
+    a = _native.KvMixArgs()
+    a.sources, a.source_stride = x.data_ptr(), x.stride()[:3]
+    a.source_dtype, a.weight_dtype = _DTYPES[x.dtype], _DTYPES[wdtype]
+    a.batch, a.tokens, a.num_sources, a.hidden, a.channels = batch, tokens, sources, hidden, channels
+    a.eps, a.mix_eps = float(eps), float(mix_eps)
+    for side in range(2):
+        a.pre_mix[side] = pre[side].data_ptr()
+        a.premixed[side] = premixed[side].data_ptr()
+        a.gain[side] = gains[side].data_ptr()
+        a.mixed[side] = mixed[side].data_ptr()
+    _native.kv_premix(a, device)
+    alphas = [
+        F.linear(premixed[side], weight.to(torch.bfloat16), bias.to(torch.bfloat16))
+        for side, (weight, bias) in enumerate(router)
+    ]
+    for side in range(2):
+        if alphas[side].stride(-1) != 1:
+            alphas[side] = alphas[side].contiguous()
+        a.alpha[side] = alphas[side].data_ptr()
+    if alphas[0].stride(0) != alphas[1].stride(0):
+        alphas = [t.contiguous() for t in alphas]
+        a.alpha[0], a.alpha[1] = alphas[0].data_ptr(), alphas[1].data_ptr()
+    a.alpha_stride = alphas[0].stride(0) if rows > 1 else channels * sources
+    _native.kv_mix(a, device)
+    return mixed[0], mixed[1]

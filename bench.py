@@ -51,6 +51,8 @@ KERNEL_NAMES = {  # rocprof kernel name prefix -> bench kernel key
     "wmx::decode_split_kernel<128, 2>": "decode_split_g2",  # C4 decode, 8 KV heads
     "wmx::decode_split_kernel": "decode_split",
     "wmx::decode_combine_kernel": "decode_combine",
+    "wmx::kv_premix_kernel": "kv_premix",
+    "wmx::kv_mix_kernel": "kv_mix",
 }
 METRIC = "attn fwd+bwd TFLOP/s (bf16, T=2048) and % MFMA peak; decode GB/s"
 
@@ -292,7 +294,7 @@ def main(argv=None) -> int:
     parser.add_argument("--no-secondary", action="store_true", help="skip the secondary lines (decode, cyclic, store, builder, loops, C5)")
     parser.add_argument(
         "--only",
-        choices=("decode", "prefill", "cyclic", "kv_store", "metadata", "decode_loop", "jacobi_dummy", "c5"),
+        choices=("decode", "prefill", "cyclic", "kv_store", "kv_producer", "metadata", "decode_loop", "jacobi_dummy", "c5"),
         help="print one secondary line as JSON and exit (for profiling that path alone)",
     )
     parser.add_argument(
@@ -333,6 +335,7 @@ def main(argv=None) -> int:
             "prefill": prefill_line,
             "cyclic": cyclic_line,
             "kv_store": kv_store_line,
+            "kv_producer": kv_producer_line,
             "metadata": metadata_line,
             "decode_loop": decode_loop_line,
             "jacobi_dummy": dummy_jacobi_line,
@@ -428,6 +431,7 @@ def main(argv=None) -> int:
         line["cyclic"] = cyclic_line(device)
         line["cyclic_variants"] = [cyclic_line(device, 2), cyclic_line(device, 8), cyclic_line(device, 4, dummy=True)]
         line["kv_store"] = kv_store_line(device)
+        line["kv_producer"] = kv_producer_line(device)
         line["metadata"] = metadata_line(device)
         line["decode_loop"] = decode_loop_line(device)
         line["c5"] = c5_line(device)
@@ -750,6 +754,47 @@ def kv_store_line(device, batch=8, channels=8, heads=16, tokens=2048, dim=64, se
         "frac_hbm": round(gbps / PEAK_HBM_GBPS, 4),
         "bytes": moved,
         "eager_reference_ms": round(eager_ms, 4),
+    }
+
+
+def kv_producer_line(device, batch=8, tokens=256, seed=9):
+    """The KV-pool producer ahead of the per-channel projection for one group
+    of the C5 pass (8 rows x 256 tokens, the block input and 24 layer outputs
+    as 25 fp32 sources of 1024, 8 channels): the HIP kernels around the
+    router GEMM (kv_pool.projection_inputs) against the same steps as torch
+    operations on the same GPU (the harness's formulation of the reference's
+    `_project`). Bytes of the HIP kernels: sources read once (fp32), both
+    premixed stacks written (bf16), read again by the mixture, the channels
+    written; the router GEMM reads the premixed stacks once more."""
+    from white_matter_amd.cyclic_pass import FeedbackConfig, FeedbackModel, HipKernels
+
+    config = FeedbackConfig()
+    model = FeedbackModel(config, device=device, seed=seed)
+    gen = torch.Generator(device=device).manual_seed(seed)
+    for side in "kv":  # content weights in the routers, not only the prior
+        weight, _ = model.router[side]
+        weight.copy_((torch.randn(weight.shape, generator=gen, device=device) * 0.003).to(weight.dtype))
+    sources, hidden, channels = config.num_sources, config.hidden_size, config.num_kv_channels
+    stacked = torch.randn(batch, tokens, sources, hidden, generator=gen, device=device)
+    with torch.no_grad():
+        for _ in range(3):
+            HipKernels.mix(model, stacked)
+            model.projection_inputs(stacked)
+        ms = Timer()(lambda: HipKernels.mix(model, stacked), 20)
+        eager_ms = Timer()(lambda: model.projection_inputs(stacked), 10)
+    rows = batch * tokens
+    premix = rows * sources * hidden * (4 + 2 * 2)
+    mix = rows * (2 * sources * hidden * 2 + 2 * channels * sources * 2 + 2 * channels * hidden * 2)
+    gemm = 2 * (rows * sources * hidden * 2 + channels * sources * sources * hidden * 2)
+    moved = premix + mix + gemm
+    return {
+        "workload": f"KV-pool producer, one C5 group: B={batch} T={tokens}, {sources} fp32 sources x {hidden}, "
+        f"{channels} channels (premix, router GEMM, routed sum, mix norm, gain)",
+        "ms": round(ms, 4),
+        "gbps": round(moved / (ms * 1e-3) / 1e9, 1),
+        "frac_hbm": round(moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),
+        "bytes": {"premix": premix, "mix": mix, "router_gemm": gemm},
+        "torch_ops_ms": round(eager_ms, 4),
     }
 
 

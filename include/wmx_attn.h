@@ -239,6 +239,43 @@ typedef struct wmx_kv_store_args {
 } wmx_kv_store_args;
 
 /*
+ * Gradient of the store's key transform k' = rope(rms_norm(key) * w[c]) for
+ * training (the autograd of the reference's `_apply_k_norm_rope` and its cast,
+ * modules/kv_pool.py:163-172, 216). With g = grad_out[b, c, h, t, :] and the
+ * forward's y = x / sqrt(mean(x^2) + eps), u = y * w[c]:
+ *   du = g * cos + rot^T(g * sin),  rot^T(z) = (z[D/2:], -z[:D/2])
+ *   grad_key  = (du * w[c] - y * mean(du * w[c] * y)) / sqrt(mean(x^2) + eps)
+ *   grad_weight[c, :] = sum over b, h, t of du * y
+ * in fp32 (no intermediate rounding). grad_weight is summed through
+ * per-workgroup parts in the workspace in a fixed order: the same bits on
+ * every run.
+ */
+typedef struct wmx_kv_store_bwd_args {
+  const void* key;            /* (B, C, H, T, D) forward input, dtype key_dtype */
+  const void* grad_out;       /* bf16 (B, C, H, T, D): gradient of the bf16 keys */
+  const void* k_norm_weight;  /* (C, D) contiguous, dtype weight_dtype */
+  const void* cos;            /* (B, T, D), dtype rope_dtype */
+  const void* sin;            /* same shape and strides as cos */
+  void* grad_key;             /* (B, C, H, T, D), dtype key_dtype */
+  float* grad_weight;         /* fp32 (C, D) contiguous, overwritten */
+  void* workspace;            /* wmx_kv_store_bwd_workspace_size bytes */
+  int64_t workspace_bytes;
+  int64_t key_stride[4];      /* element strides [batch, channel, head, token] */
+  int64_t grad_out_stride[4];
+  int64_t grad_key_stride[4];
+  int64_t rope_stride[2];     /* [batch, token] */
+  int32_t key_dtype;          /* WMX_DTYPE_F32 or WMX_DTYPE_BF16 */
+  int32_t weight_dtype;
+  int32_t rope_dtype;
+  int32_t batch;
+  int32_t channels;
+  int32_t heads;
+  int32_t tokens;
+  int32_t head_dim;           /* 64, 96 or 128 */
+  float eps;
+} wmx_kv_store_bwd_args;
+
+/*
  * KV-pool producer, the token-local steps ahead of the per-channel projection
  * (reference modules/kv_pool.py:97-160 `KVPool._project`, the bf16 inference
  * form of :108-136; modules/routing.py:77-124 `Router.forward`,
@@ -362,6 +399,7 @@ size_t wmx_attn_args_size(void);
 size_t wmx_decode_args_size(void);
 size_t wmx_kv_store_args_size(void);
 size_t wmx_kv_mix_args_size(void);
+size_t wmx_kv_store_bwd_args_size(void);
 size_t wmx_strict_meta_args_size(void);
 size_t wmx_feedback_meta_args_size(void);
 const char* wmx_last_error(void);
@@ -437,6 +475,12 @@ int wmx_decode_noalloc(const wmx_decode_args* args, void* stream);
  * rms_norm, weight, RoPE, casts and index_copy_ (modules/kv_pool.py:163-172,
  * 216; blocks/_execution/cyclic.py:448-458). */
 int wmx_kv_pool_store(const wmx_kv_store_args* args, void* stream);
+
+/* Backward of the store's key transform (see wmx_kv_store_bwd_args): replaces
+ * the autograd of the reference's eager rms_norm, weight and RoPE steps
+ * (modules/kv_pool.py:163-172) where training projects keys. */
+int64_t wmx_kv_store_bwd_workspace_size(const wmx_kv_store_bwd_args* args);
+int wmx_kv_store_bwd(const wmx_kv_store_bwd_args* args, void* stream);
 
 /* KV-pool producer (see wmx_kv_mix_args). wmx_kv_premix replaces the source
  * RMS norm and the pre-mix products with their bf16 casts (reference

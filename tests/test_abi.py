@@ -31,6 +31,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.wmx_attn_args_size() == ctypes.sizeof(_native.AttnArgs)
     assert lib.wmx_decode_args_size() == ctypes.sizeof(_native.DecodeArgs)
     assert lib.wmx_kv_mix_args_size() == ctypes.sizeof(_native.KvMixArgs)
+    assert lib.wmx_kv_store_bwd_args_size() == ctypes.sizeof(_native.KvStoreBwdArgs)
 
 
 def test_argument_checks_return_errors_without_launching():
@@ -66,6 +67,17 @@ def test_argument_checks_return_errors_without_launching():
     assert lib.wmx_decode_workspace_size(ctypes.byref(dec)) > _native.DECODE_NOALLOC_MAX_BYTES
     assert lib.wmx_decode_noalloc(ctypes.byref(dec), None) == -3
     assert b"static scratch" in lib.wmx_last_error()
+    bwd = _native.KvStoreBwdArgs()
+    bwd.head_dim, bwd.batch, bwd.channels, bwd.heads, bwd.tokens = 80, 1, 1, 1, 1
+    assert lib.wmx_kv_store_bwd(ctypes.byref(bwd), None) == -2
+    assert b"head_dim" in lib.wmx_last_error()
+    bwd.head_dim, bwd.k_norm_weight, bwd.grad_weight = 64, 0x1000, 0x1000
+    assert lib.wmx_kv_store_bwd_workspace_size(ctypes.byref(bwd)) == 64 * 4
+    assert lib.wmx_kv_store_bwd(ctypes.byref(bwd), None) == -1
+    assert b"NULL" in lib.wmx_last_error()
+    bwd.key = bwd.grad_out = bwd.cos = bwd.sin = bwd.grad_key = bwd.workspace = 0x1000
+    bwd.workspace_bytes = 64
+    assert lib.wmx_kv_store_bwd(ctypes.byref(bwd), None) == -3
     mix = _native.KvMixArgs()
     mix.batch, mix.tokens, mix.num_sources, mix.hidden, mix.channels = 1, 1, 25, 1028, 8
     assert lib.wmx_kv_premix(ctypes.byref(mix), None) == -2

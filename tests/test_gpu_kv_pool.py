@@ -197,3 +197,61 @@ def test_producer_rejects_autograd_and_bad_shapes():
         kv_pool.projection_inputs(stacked[..., :60].to(DEV), tuple(p[:, :60] for p in args[0]), args[1], args[2])
     with torch.no_grad(), pytest.raises(ValueError, match="pre_mix"):
         kv_pool.projection_inputs(stacked[:, :, :2].to(DEV), *args)
+
+
+@pytest.mark.parametrize("dim", [64, 96, 128])
+@pytest.mark.parametrize("key_dtype", [torch.float32, torch.bfloat16])
+def test_k_norm_rope_backward_matches_oracle(dim, key_dtype):
+    """white_matter::k_norm_rope's backward (wmx_kv_store_bwd) against float64
+    autograd of the oracle's transform (no rounding), on rows that do not
+    fill the last workgroup (37 tokens); grad_weight sums 2 x 2 x 37 rows
+    per channel through the fixed-order parts, so repeats are bit-identical."""
+    key, _, weight, cos, sin = _inputs(key_dtype, torch.bfloat16, torch.float32, torch.float32, dim, seed=dim)
+    k = key.to(DEV).requires_grad_()
+    w = weight.to(DEV).requires_grad_()
+    out = kv_pool.k_norm_rope(k, w, cos.to(DEV), sin.to(DEV))
+    assert out.dtype == torch.bfloat16
+    probe = torch.randn(out.shape, generator=torch.Generator().manual_seed(dim)).bfloat16()
+    gk, gw = torch.autograd.grad(out, (k, w), probe.to(DEV))
+    assert gk.dtype == key_dtype and gw.dtype == weight.dtype
+    kr, wr = key.double().requires_grad_(), weight.double().requires_grad_()
+    expected = ref.k_norm_rope(kr, wr, cos, sin, 1e-6, dtype=torch.float64)
+    ek, ew = torch.autograd.grad(expected, (kr, wr), probe.double())
+    if key_dtype == torch.bfloat16:
+        assert_bf16_close(gk.double().cpu(), ek, what="grad key")
+    else:
+        torch.testing.assert_close(gk.double().cpu(), ek, rtol=2e-4, atol=2e-5 * ek.abs().max().item())
+    torch.testing.assert_close(gw.double().cpu(), ew, rtol=1e-4, atol=1e-5 * ew.abs().max().item())
+    gk2, gw2 = torch.autograd.grad(kv_pool.k_norm_rope(k, w, cos.to(DEV), sin.to(DEV)), (k, w), probe.to(DEV))
+    assert torch.equal(gk, gk2) and torch.equal(gw, gw2)
+
+
+def test_k_norm_rope_backward_in_a_training_step():
+    """The reference's training use (kv_pool.py:213-216, cyclic.py:448-458):
+    projected keys -> k_norm_rope -> index_copy_ into a pool copy -> a loss;
+    gradients reach the projection input and the norm weight as with the
+    eager torch steps (fp32 keys: to the fp32 bar)."""
+    gen = torch.Generator().manual_seed(3)
+    x = torch.randn(2, 16, 64, generator=gen).to(DEV).requires_grad_()
+    proj = (torch.randn(2, 2 * 64, 64, generator=gen) * 0.1).to(DEV)
+    weight = (1 + 0.1 * torch.randn(2, 64, generator=gen)).to(DEV).requires_grad_()
+    angle = torch.rand(1, 16, 32, generator=gen).to(DEV) * 9.0
+    angle = torch.cat((angle, angle), -1)
+    cos, sin = angle.cos(), angle.sin()
+    slots = torch.arange(16, device=DEV) + 1
+    target = torch.randn(1, 2, 2, 17, 64, generator=gen).to(DEV)
+
+    def loss(transform):
+        key = (x @ proj.transpose(1, 2)).view(2, 16, 2, 64).permute(0, 2, 1, 3)[None]  # (1, C=2, H=2, T, D)
+        pool = torch.zeros(1, 2, 2, 17, 64, device=DEV).index_copy(3, slots, transform(key).float())
+        return ((pool - target) ** 2).sum()
+
+    def eager(key):
+        normed = F.rms_norm(key, (64,), None, 1e-6) * weight.view(1, 2, 1, 1, 64)
+        c, s = cos[:, None, None], sin[:, None, None]
+        return (normed * c + torch.cat((-normed[..., 32:], normed[..., :32]), -1) * s).bfloat16()
+
+    gx, gw = torch.autograd.grad(loss(lambda k: kv_pool.k_norm_rope(k, weight, cos, sin)), (x, weight))
+    ex, ew = torch.autograd.grad(loss(eager), (x, weight))
+    torch.testing.assert_close(gx, ex, rtol=1e-3, atol=1e-3 * ex.abs().max().item())
+    torch.testing.assert_close(gw, ew, rtol=1e-3, atol=1e-3 * ew.abs().max().item())

@@ -146,6 +146,35 @@ class KvMixArgs(ctypes.Structure):
     ]
 
 
+class KvStoreBwdArgs(ctypes.Structure):
+    """Mirror of wmx_kv_store_bwd_args."""
+
+    _fields_ = [
+        ("key", _vp),
+        ("grad_out", _vp),
+        ("k_norm_weight", _vp),
+        ("cos", _vp),
+        ("sin", _vp),
+        ("grad_key", _vp),
+        ("grad_weight", _vp),
+        ("workspace", _vp),
+        ("workspace_bytes", ctypes.c_int64),
+        ("key_stride", ctypes.c_int64 * 4),
+        ("grad_out_stride", ctypes.c_int64 * 4),
+        ("grad_key_stride", ctypes.c_int64 * 4),
+        ("rope_stride", _c_i64_2),
+        ("key_dtype", ctypes.c_int32),
+        ("weight_dtype", ctypes.c_int32),
+        ("rope_dtype", ctypes.c_int32),
+        ("batch", ctypes.c_int32),
+        ("channels", ctypes.c_int32),
+        ("heads", ctypes.c_int32),
+        ("tokens", ctypes.c_int32),
+        ("head_dim", ctypes.c_int32),
+        ("eps", ctypes.c_float),
+    ]
+
+
 KV_MIX_MAX_SOURCES = 512
 KV_MIX_MAX_HIDDEN = 4096
 
@@ -255,6 +284,9 @@ EXPORTS = (
     "wmx_kv_store_args_size",
     "wmx_kv_pool_store",
     "wmx_kv_mix_args_size",
+    "wmx_kv_store_bwd_args_size",
+    "wmx_kv_store_bwd_workspace_size",
+    "wmx_kv_store_bwd",
     "wmx_kv_premix",
     "wmx_kv_mix",
     "wmx_strict_meta_args_size",
@@ -301,6 +333,11 @@ def load() -> ctypes.CDLL:
     lib.wmx_kv_pool_store.argtypes = [ctypes.POINTER(KvStoreArgs), _vp]
     lib.wmx_kv_pool_store.restype = ctypes.c_int
     lib.wmx_kv_mix_args_size.restype = ctypes.c_size_t
+    lib.wmx_kv_store_bwd_args_size.restype = ctypes.c_size_t
+    lib.wmx_kv_store_bwd_workspace_size.argtypes = [ctypes.POINTER(KvStoreBwdArgs)]
+    lib.wmx_kv_store_bwd_workspace_size.restype = ctypes.c_int64
+    lib.wmx_kv_store_bwd.argtypes = [ctypes.POINTER(KvStoreBwdArgs), _vp]
+    lib.wmx_kv_store_bwd.restype = ctypes.c_int
     for name in ("wmx_kv_premix", "wmx_kv_mix"):
         getattr(lib, name).argtypes = [ctypes.POINTER(KvMixArgs), _vp]
         getattr(lib, name).restype = ctypes.c_int
@@ -325,6 +362,8 @@ def load() -> ctypes.CDLL:
         raise RuntimeError("wmx_decode_args layout differs between the library and the binding")
     if lib.wmx_kv_store_args_size() != ctypes.sizeof(KvStoreArgs):
         raise RuntimeError("wmx_kv_store_args layout differs between the library and the binding")
+    if lib.wmx_kv_store_bwd_args_size() != ctypes.sizeof(KvStoreBwdArgs):
+        raise RuntimeError("wmx_kv_store_bwd_args layout differs between the library and the binding")
     if lib.wmx_kv_mix_args_size() != ctypes.sizeof(KvMixArgs):
         raise RuntimeError("wmx_kv_mix_args layout differs between the library and the binding")
     if lib.wmx_feedback_meta_args_size() != ctypes.sizeof(FeedbackMetaArgs):
@@ -419,6 +458,15 @@ def decode_noalloc(args: DecodeArgs, device: torch.device) -> None:
 def kv_pool_store(args: KvStoreArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_kv_pool_store(ctypes.byref(args), _stream(device)), "wmx_kv_pool_store")
+
+
+def kv_store_bwd_workspace_size(args: KvStoreBwdArgs) -> int:
+    return int(load().wmx_kv_store_bwd_workspace_size(ctypes.byref(args)))
+
+
+def kv_store_bwd(args: KvStoreBwdArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_kv_store_bwd(ctypes.byref(args), _stream(device)), "wmx_kv_store_bwd")
 
 
 def kv_premix(args: KvMixArgs, device: torch.device) -> None:

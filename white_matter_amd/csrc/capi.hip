@@ -318,6 +318,37 @@ size_t wmx_kv_store_args_size(void) { return sizeof(wmx_kv_store_args); }
 
 size_t wmx_kv_mix_args_size(void) { return sizeof(wmx_kv_mix_args); }
 
+size_t wmx_kv_store_bwd_args_size(void) { return sizeof(wmx_kv_store_bwd_args); }
+
+int64_t wmx_kv_store_bwd_workspace_size(const wmx_kv_store_bwd_args* a) {
+  return a ? wmx::kv_store_bwd_workspace_size(*a) : 0;
+}
+
+int wmx_kv_store_bwd(const wmx_kv_store_bwd_args* a, void* stream) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->head_dim != 64 && a->head_dim != 96 && a->head_dim != 128)
+    return fail(WMX_E_UNSUPPORTED, "kv store head_dim %d is not 64, 96 or 128", a->head_dim);
+  if (a->batch < 0 || a->channels < 0 || a->heads < 0 || a->tokens < 0) return fail(WMX_E_INVALID, "negative shape");
+  for (int dt : {a->key_dtype, a->weight_dtype, a->rope_dtype})
+    if (dt != WMX_DTYPE_F32 && dt != WMX_DTYPE_BF16) return fail(WMX_E_INVALID, "dtype must be WMX_DTYPE_F32 or WMX_DTYPE_BF16");
+  if (!(a->eps >= 0.f)) return fail(WMX_E_INVALID, "eps must be >= 0");
+  if (a->channels == 0) return WMX_OK;
+  if (!a->k_norm_weight || !a->grad_weight) return fail(WMX_E_INVALID, "kv store backward pointer is NULL");
+  const int64_t need = wmx::kv_store_bwd_workspace_size(*a);
+  if (need > 0) {
+    if (!a->key || !a->grad_out || !a->cos || !a->sin || !a->grad_key || !a->workspace)
+      return fail(WMX_E_INVALID, "kv store backward pointer is NULL");
+    if (a->workspace_bytes < need) return fail(WMX_E_WORKSPACE, "workspace %lld < %lld bytes", (long long)a->workspace_bytes, (long long)need);
+  }
+  if (!aligned16(a->key) || !aligned16(a->grad_out) || !aligned16(a->k_norm_weight) || !aligned16(a->cos) ||
+      !aligned16(a->sin) || !aligned16(a->grad_key) || !aligned16(a->workspace) || !aligned16(a->grad_weight))
+    return fail(WMX_E_INVALID, "kv store backward operands must be 16-byte aligned");
+  if (!strides_vec8(a->key_stride, 4) || !strides_vec8(a->grad_out_stride, 4) || !strides_vec8(a->grad_key_stride, 4) ||
+      !strides_vec8(a->rope_stride, 2))
+    return fail(WMX_E_INVALID, "kv store backward strides must be multiples of 8 elements");
+  return launched(wmx::launch_kv_store_bwd(*a, (hipStream_t)stream));
+}
+
 size_t wmx_strict_meta_args_size(void) { return sizeof(wmx_strict_meta_args); }
 
 

@@ -134,4 +134,163 @@ int launch_kv_store(const wmx_kv_store_args& a, hipStream_t stream) {
   return WMX_OK;
 }
 
+// ------------------------------------------------------------ backward ----
+// Rows per workgroup of the backward: (256 / L) tokens of one (b, c), each
+// thread walking the heads of its token like the forward.
+template <int D>
+constexpr int bwd_lanes() { return D / 8 <= 8 ? 8 : 16; }
+
+int64_t kv_store_bwd_chunks(const wmx_kv_store_bwd_args& a) {
+  const int rows = 256 / (a.head_dim <= 64 ? 8 : 16);
+  return ((int64_t)a.tokens + rows - 1) / rows;
+}
+
+int64_t kv_store_bwd_workspace_size(const wmx_kv_store_bwd_args& a) {
+  return (int64_t)a.batch * a.channels * kv_store_bwd_chunks(a) * a.head_dim * (int64_t)sizeof(float);
+}
+
+// Workgroup (b, c, token chunk). Per row: y = x * inv, du = g cos +
+// rot^T(g sin), dx = inv (du w - y mean(du w y)); the workgroup's part of
+// grad_weight[c] (sum of du y over its rows and heads) goes to the workspace.
+template <int D, bool KEY_BF16>
+__global__ __launch_bounds__(256) void kv_store_bwd_kernel(const wmx_kv_store_bwd_args a, int chunks) {
+  constexpr int LD = D / 8;
+  constexpr int L = bwd_lanes<D>();
+  constexpr int RB = 256 / L;
+  __shared__ float red[4][D];
+  const int bc = blockIdx.x / chunks, chunk = blockIdx.x - bc * chunks;
+  const int b = bc / a.channels, c = bc - b * a.channels;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int l = tid % L;
+  const int t = chunk * RB + tid / L;
+  const bool row_ok = t < a.tokens;
+  const int d0 = 8 * l;
+  const bool data = l < LD;
+  const bool live = row_ok && data;
+  const int dl = data ? d0 : 0;
+  const int tl = row_ok ? t : 0;
+  const bool low = d0 < D / 2;
+  const int partner = data ? lane + (low ? LD / 2 : -(LD / 2)) : lane;
+
+  float wt[8], cs[8], sn[8];
+  load8(a.k_norm_weight, (int64_t)c * D + dl, a.weight_dtype == WMX_DTYPE_BF16, wt);
+  const int64_t ro = (int64_t)b * a.rope_stride[0] + (int64_t)tl * a.rope_stride[1] + dl;
+  load8(a.cos, ro, a.rope_dtype == WMX_DTYPE_BF16, cs);
+  load8(a.sin, ro, a.rope_dtype == WMX_DTYPE_BF16, sn);
+  const int64_t key_row = (int64_t)b * a.key_stride[0] + (int64_t)c * a.key_stride[1] + (int64_t)tl * a.key_stride[3] + dl;
+  const int64_t g_row =
+      (int64_t)b * a.grad_out_stride[0] + (int64_t)c * a.grad_out_stride[1] + (int64_t)tl * a.grad_out_stride[3] + dl;
+  const int64_t dk_row =
+      (int64_t)b * a.grad_key_stride[0] + (int64_t)c * a.grad_key_stride[1] + (int64_t)tl * a.grad_key_stride[3] + dl;
+  float dw[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dw[e] = 0.f;
+
+  for (int h = 0; h < a.heads; ++h) {
+    float x[8], g[8];
+    load8(a.key, key_row + (int64_t)h * a.key_stride[2], KEY_BF16, x);
+    load8(a.grad_out, g_row + (int64_t)h * a.grad_out_stride[2], true, g);
+    if (!live) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[e] = g[e] = 0.f;
+    }
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss = fmaf(x[e], x[e], ss);
+#pragma unroll
+    for (int o = L / 2; o > 0; o >>= 1) ss += __shfl_xor(ss, o);
+    const float inv = 1.f / sqrtf(ss / (float)D + a.eps);
+    float y[8], du[8], dot = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      y[e] = x[e] * inv;
+      const float other = __shfl(g[e] * sn[e], partner);
+      du[e] = g[e] * cs[e] + (low ? other : -other);
+      dw[e] = fmaf(du[e], y[e], dw[e]);
+      du[e] *= wt[e];
+      dot = fmaf(du[e], y[e], dot);
+    }
+#pragma unroll
+    for (int o = L / 2; o > 0; o >>= 1) dot += __shfl_xor(dot, o);
+    const float mean = dot / (float)D;
+    float dx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dx[e] = inv * (du[e] - y[e] * mean);
+    if (live) {
+      const int64_t off = dk_row + (int64_t)h * a.grad_key_stride[2];
+      if constexpr (KEY_BF16) {
+        store8_bf16(a.grad_key, off, dx);
+      } else {
+        float* dst = (float*)a.grad_key + off;
+        *reinterpret_cast<f32x4*>(dst) = f32x4{dx[0], dx[1], dx[2], dx[3]};
+        *reinterpret_cast<f32x4*>(dst + 4) = f32x4{dx[4], dx[5], dx[6], dx[7]};
+      }
+    }
+  }
+  // the workgroup's grad_weight part: rows of a wave, then the four waves in order
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+#pragma unroll
+    for (int o = L; o < 64; o <<= 1) dw[e] += __shfl_xor(dw[e], o);
+  }
+  if (lane < L && data) {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) red[w][d0 + e] = dw[e];
+  }
+  __syncthreads();
+  if (tid < D) {
+    float* part = (float*)a.workspace + (int64_t)blockIdx.x * D;
+    part[tid] = ((red[0][tid] + red[1][tid]) + red[2][tid]) + red[3][tid];
+  }
+}
+
+// grad_weight[c, d] = the parts of every (b, chunk) of channel c, added in
+// order (eight interleaved partial sums, combined in a fixed order).
+__global__ __launch_bounds__(128) void kv_store_bwd_reduce_kernel(const wmx_kv_store_bwd_args a, int chunks) {
+  const int c = blockIdx.x, d = threadIdx.x;
+  if (d >= a.head_dim) return;
+  const int D = a.head_dim;
+  float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+  const int64_t per_b = (int64_t)chunks;
+  const int n = a.batch * chunks;
+  int i = 0;
+  for (; i + 8 <= n; i += 8) {
+#pragma unroll
+    for (int u = 0; u < 8; ++u) {
+      const int k = i + u, bb = k / chunks, ch = k - bb * chunks;
+      acc[u] += ((const float*)a.workspace)[(((int64_t)bb * a.channels + c) * per_b + ch) * D + d];
+    }
+  }
+  for (; i < n; ++i) {
+    const int bb = i / chunks, ch = i - bb * chunks;
+    acc[i & 7] += ((const float*)a.workspace)[(((int64_t)bb * a.channels + c) * per_b + ch) * D + d];
+  }
+  a.grad_weight[(int64_t)c * D + d] = ((acc[0] + acc[1]) + (acc[2] + acc[3])) + ((acc[4] + acc[5]) + (acc[6] + acc[7]));
+}
+
+template <int D>
+static void launch_kv_store_bwd_d(const wmx_kv_store_bwd_args& a, unsigned blocks, int chunks, hipStream_t stream) {
+  if (a.key_dtype == WMX_DTYPE_BF16)
+    hipLaunchKernelGGL((kv_store_bwd_kernel<D, true>), dim3(blocks), dim3(256), 0, stream, a, chunks);
+  else
+    hipLaunchKernelGGL((kv_store_bwd_kernel<D, false>), dim3(blocks), dim3(256), 0, stream, a, chunks);
+}
+
+int launch_kv_store_bwd(const wmx_kv_store_bwd_args& a, hipStream_t stream) {
+  const int64_t chunks = kv_store_bwd_chunks(a);
+  const int64_t blocks = (int64_t)a.batch * a.channels * chunks;
+  if (a.channels == 0) return WMX_OK;
+  if (blocks > UINT32_MAX || chunks > INT32_MAX) return WMX_E_UNSUPPORTED;
+  if (blocks > 0) {
+    switch (a.head_dim) {
+      case 64: launch_kv_store_bwd_d<64>(a, (unsigned)blocks, (int)chunks, stream); break;
+      case 96: launch_kv_store_bwd_d<96>(a, (unsigned)blocks, (int)chunks, stream); break;
+      case 128: launch_kv_store_bwd_d<128>(a, (unsigned)blocks, (int)chunks, stream); break;
+      default: return WMX_E_UNSUPPORTED;
+    }
+  }
+  hipLaunchKernelGGL(kv_store_bwd_reduce_kernel, dim3((unsigned)a.channels), dim3(128), 0, stream, a, (int)chunks);
+  return WMX_OK;
+}
+
 }  // namespace wmx

@@ -57,6 +57,8 @@ int64_t decode_workspace_size(const wmx_decode_args& a);
 int decode_num_splits(const wmx_decode_args& a);
 int launch_decode(const wmx_decode_args& a, hipStream_t stream);
 int launch_kv_store(const wmx_kv_store_args& a, hipStream_t stream);
+int launch_kv_store_bwd(const wmx_kv_store_bwd_args& a, hipStream_t stream);
+int64_t kv_store_bwd_workspace_size(const wmx_kv_store_bwd_args& a);
 int launch_kv_premix(const wmx_kv_mix_args& a, hipStream_t stream);
 int launch_kv_mix(const wmx_kv_mix_args& a, hipStream_t stream);
 int64_t strict_meta_workspace_size(const wmx_strict_meta_args& a);

@@ -18,8 +18,10 @@ pool with two `index_copy_` along the token axis
 (src/white_matter/blocks/_execution/cyclic.py:448-458 `_write_pool`). Here the
 whole step is one HIP kernel (wmx_kv_pool_store) that reads each key and value
 once and writes the pool slots, with the reference's rounding after every step
-when the keys are bf16. Forward only: under autograd the reference's eager
-sequence (differentiable) remains the path.
+when the keys are bf16. The in-place pool write is forward-only; training
+projects keys through `k_norm_rope`, an operator (white_matter::k_norm_rope)
+whose backward is one HIP kernel pair (wmx_kv_store_bwd: the key gradient
+and the norm weight's gradient summed in a fixed order).
 """
 
 from __future__ import annotations
@@ -67,7 +69,7 @@ def write_pool(
     slots (T,) int64 distinct pool slots. head_dim 64, 96 or 128.
     """
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (key, value, k_norm_weight, cos, sin)):
-        raise RuntimeError("write_pool is forward-only; use the reference's eager sequence under autograd")
+        raise RuntimeError("write_pool is forward-only; under autograd produce the keys with k_norm_rope")
     if key.ndim != 5 or (value is not None and value.shape != key.shape):
         raise ValueError("key and value must be (B, C, H, T, D) of one shape")
     batch, channels, heads, tokens, dim = key.shape
@@ -107,14 +109,75 @@ def write_pool(
     _native.kv_pool_store(a, key.device)
 
 
+@torch.library.custom_op("white_matter::k_norm_rope", mutates_args=())
+def _k_norm_rope_op(key: torch.Tensor, k_norm_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float) -> torch.Tensor:
+    out = torch.empty(key.shape, device=key.device, dtype=torch.bfloat16)
+    slots = torch.arange(key.shape[3], device=key.device)
+    with torch.no_grad():
+        write_pool(key, None, k_norm_weight, cos, sin, out, None, slots, eps=eps)
+    return out
+
+
+@_k_norm_rope_op.register_fake
+def _(key, k_norm_weight, cos, sin, eps):
+    return key.new_empty(key.shape, dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("white_matter::k_norm_rope_bwd", mutates_args=())
+def _k_norm_rope_bwd_op(
+    grad: torch.Tensor, key: torch.Tensor, k_norm_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, eps: float
+) -> tuple[torch.Tensor, torch.Tensor]:
+    batch, channels, heads, tokens, dim = key.shape
+    key = _rows(key)
+    grad = _rows(grad.to(torch.bfloat16))
+    cos, sin = _rows(cos), _rows(sin)
+    if sin.stride() != cos.stride():
+        cos, sin = cos.contiguous(), sin.contiguous()
+    weight = k_norm_weight.contiguous()
+    grad_key = torch.empty(key.shape, device=key.device, dtype=key.dtype)
+    grad_weight = torch.empty(channels, dim, device=key.device, dtype=torch.float32)
+    a = _native.KvStoreBwdArgs()
+    a.key, a.key_stride, a.key_dtype = key.data_ptr(), key.stride()[:4], _dtype(key, "key")
+    a.grad_out, a.grad_out_stride = grad.data_ptr(), grad.stride()[:4]
+    a.grad_key, a.grad_key_stride = grad_key.data_ptr(), grad_key.stride()[:4]
+    a.k_norm_weight, a.weight_dtype = weight.data_ptr(), _dtype(weight, "k_norm_weight")
+    a.cos, a.sin, a.rope_stride, a.rope_dtype = cos.data_ptr(), sin.data_ptr(), cos.stride()[:2], _dtype(cos, "cos")
+    a.grad_weight = grad_weight.data_ptr()
+    a.batch, a.channels, a.heads, a.tokens, a.head_dim, a.eps = batch, channels, heads, tokens, dim, float(eps)
+    need = _native.kv_store_bwd_workspace_size(a)
+    workspace = torch.empty(max(need, 16), device=key.device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), need
+    _native.kv_store_bwd(a, key.device)
+    return grad_key, grad_weight.to(k_norm_weight.dtype)
+
+
+@_k_norm_rope_bwd_op.register_fake
+def _(grad, key, k_norm_weight, cos, sin, eps):
+    return torch.empty_like(key), torch.empty_like(k_norm_weight)
+
+
+def _k_norm_rope_setup(ctx, inputs, output):
+    key, k_norm_weight, cos, sin, eps = inputs
+    ctx.save_for_backward(key, k_norm_weight, cos, sin)
+    ctx.eps = eps
+
+
+def _k_norm_rope_backward(ctx, grad):
+    key, k_norm_weight, cos, sin = ctx.saved_tensors
+    grad_key, grad_weight = _k_norm_rope_bwd_op(grad, key, k_norm_weight, cos, sin, ctx.eps)
+    return grad_key, grad_weight, None, None, None
+
+
+_k_norm_rope_op.register_autograd(_k_norm_rope_backward, setup_context=_k_norm_rope_setup)
+
+
 def k_norm_rope(key: torch.Tensor, k_norm_weight: torch.Tensor, cos: torch.Tensor, sin: torch.Tensor, *, eps: float = 1e-6) -> torch.Tensor:
     """bf16(rope(rms_norm(key) * k_norm_weight)) as a new (B, C, H, T, D)
     tensor: the reference's `_apply_k_norm_rope(...).to(bfloat16)`
-    (modules/kv_pool.py:163-172, 216)."""
-    out = torch.empty(key.shape, device=key.device, dtype=torch.bfloat16)
-    slots = torch.arange(key.shape[3], device=key.device)
-    write_pool(key, None, k_norm_weight, cos, sin, out, None, slots, eps=eps)
-    return out
+    (modules/kv_pool.py:163-172, 216). Differentiable in key and
+    k_norm_weight (cos and sin are position embeddings and get no gradient):
+    the backward evaluates the exact gradient in fp32 on the HIP kernels."""
+    return _k_norm_rope_op(key, k_norm_weight, cos, sin, float(eps))
 
 
 def _weights(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:

@@ -32,32 +32,45 @@
 namespace wmx {
 
 // ---------------------------------------------------------------- delta ----
-// 16 lanes per row, 8 elements per lane; 16 rows per 256-thread block.
+// 16 lanes per row, 8 elements per lane; a thread takes kDeltaRows rows (16
+// apart) with all their loads issued before any is used, so each thread has
+// kDeltaRows x 32 bytes in flight; 16 kDeltaRows rows per 256-thread block.
+constexpr int kDeltaRows = 4;
 template <int D>
 __global__ __launch_bounds__(256) void bwd_delta_kernel(const wmx_attn_args a, int64_t rows) {
   const int tid = threadIdx.x;
-  const int64_t r = (int64_t)blockIdx.x * 16 + (tid >> 4);
   const int l16 = tid & 15;
-  float acc = 0.f;
-  if (r < rows && 8 * l16 < D) {
-    const int i = (int)(r % a.q_len);
-    const int64_t bh = r / a.q_len;
-    const int h = (int)(bh % a.q_heads);
-    const int b = (int)(bh / a.q_heads);
-    const bf16* o = (const bf16*)a.o + (int64_t)b * a.o_stride[0] + (int64_t)h * a.o_stride[1] +
-                    (int64_t)i * a.o_stride[2] + 8 * l16;
-    const bf16* g = (const bf16*)a.dout + (int64_t)b * a.do_stride[0] + (int64_t)h * a.do_stride[1] +
-                    (int64_t)i * a.do_stride[2] + 8 * l16;
-    const u32x4 ow = load16(o), gw = load16(g);
+  const int r0 = (int)blockIdx.x * 16 * kDeltaRows + (tid >> 4);  // rows < 2^31 (checked on the host)
+  const bool lane_live = 8 * l16 < D;
+  u32x4 ow[kDeltaRows], gw[kDeltaRows];
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      acc = fmaf(bf16_lo(ow[e]), bf16_lo(gw[e]), acc);
-      acc = fmaf(bf16_hi(ow[e]), bf16_hi(gw[e]), acc);
+  for (int k = 0; k < kDeltaRows; ++k) {
+    const int r = r0 + 16 * k;
+    ow[k] = gw[k] = u32x4{0u, 0u, 0u, 0u};
+    if (r < rows && lane_live) {
+      const int i = (int)((unsigned)r % (unsigned)a.q_len);
+      const int bh = (int)((unsigned)r / (unsigned)a.q_len);
+      const int h = (int)((unsigned)bh % (unsigned)a.q_heads);
+      const int b = (int)((unsigned)bh / (unsigned)a.q_heads);
+      ow[k] = load16((const bf16*)a.o + (int64_t)b * a.o_stride[0] + (int64_t)h * a.o_stride[1] +
+                     (int64_t)i * a.o_stride[2] + 8 * l16);
+      gw[k] = load16((const bf16*)a.dout + (int64_t)b * a.do_stride[0] + (int64_t)h * a.do_stride[1] +
+                     (int64_t)i * a.do_stride[2] + 8 * l16);
     }
   }
 #pragma unroll
-  for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
-  if (r < rows && l16 == 0) a.delta[r] = acc;
+  for (int k = 0; k < kDeltaRows; ++k) {
+    float acc = 0.f;
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      acc = fmaf(bf16_lo(ow[k][e]), bf16_lo(gw[k][e]), acc);
+      acc = fmaf(bf16_hi(ow[k][e]), bf16_hi(gw[k][e]), acc);
+    }
+#pragma unroll
+    for (int o = 8; o > 0; o >>= 1) acc += __shfl_xor(acc, o);
+    const int r = r0 + 16 * k;
+    if (r < rows && l16 == 0) a.delta[r] = acc;
+  }
 }
 
 // ------------------------------------------------------------------- dQ ----
@@ -971,7 +984,9 @@ __global__ void acc_to_bf16_kernel(const wmx_attn_args a) {
 int launch_bwd_preprocess(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t rows = (int64_t)a.batch * a.q_heads * a.q_len;
   if (rows == 0) return WMX_OK;
-  const dim3 grid((unsigned)((rows + 15) / 16));
+  if (rows + 16 * kDeltaRows > INT32_MAX) return WMX_E_UNSUPPORTED;
+  const int64_t blocks = (rows + 16 * kDeltaRows - 1) / (16 * kDeltaRows);
+  const dim3 grid((unsigned)blocks);
   switch (a.head_dim) {
     case 64: hipLaunchKernelGGL(bwd_delta_kernel<64>, grid, dim3(256), 0, stream, a, rows); break;
     case 96: hipLaunchKernelGGL(bwd_delta_kernel<96>, grid, dim3(256), 0, stream, a, rows); break;

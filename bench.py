@@ -130,7 +130,7 @@ def kernel_times(q, k, v, metadata, reps):
     varlen = _kernels.Varlen(
         metadata.query_indices, metadata.key_indices, metadata.cu_queries, metadata.cu_keys,
         metadata.cu_queries.numel() - 1, max_q, max_k, length, k.shape[2], _keys_unique_code(flags), flags & 15,
-        *_work_units(metadata),
+        *_work_units(metadata, query_extent=length),
     )
     vis = _kernels.Visibility(varlen=varlen)
     out = torch.zeros(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 6
+#define WMX_ABI_VERSION 7
 
 enum {
   WMX_OK = 0,
@@ -152,7 +152,33 @@ typedef struct wmx_attn_args {
    * key ranges such as a chunk after a cached prefix). q_units tiles count in
    * these rows. The backward kernels are unaffected. */
   int32_t query_tile;
+  /* Ints per entry of q_units and k_units: 0 or 2 for (segment or batch row,
+   * tile) pairs; WMX_UNIT_FIELDS (varlen schedules only) for entries that
+   * also carry their segment's bounds, so a workgroup reads one entry instead
+   * of cu_queries, cu_keys and the index arrays one after another (fields
+   * below; the row and slots are those of the segment's index elements 0 and
+   * 1, slot 1 being slot 0 + 1 for a one-element side; the dS offset is
+   * ds_offsets[segment] as two int32 halves). */
+  int32_t unit_fields;
 } wmx_attn_args;
+
+enum {
+  WMX_UNIT_SEGMENT = 0,
+  WMX_UNIT_TILE = 1,
+  WMX_UNIT_QUERY_START = 2, /* cu_queries[segment] */
+  WMX_UNIT_QUERIES = 3,
+  WMX_UNIT_KEY_START = 4,   /* cu_keys[segment] */
+  WMX_UNIT_KEYS = 5,
+  WMX_UNIT_QUERY_ROW = 6,   /* query_indices[start] / query_extent */
+  WMX_UNIT_QUERY_SLOT0 = 7,
+  WMX_UNIT_QUERY_SLOT1 = 8,
+  WMX_UNIT_KEY_ROW = 9,     /* key_indices[start] / key_extent */
+  WMX_UNIT_KEY_SLOT0 = 10,
+  WMX_UNIT_KEY_SLOT1 = 11,
+  WMX_UNIT_DS_LO = 12,      /* ds_offsets[segment], low and high 32 bits */
+  WMX_UNIT_DS_HI = 13,
+  WMX_UNIT_FIELDS = 16
+};
 
 /*
  * Single-query decode over a KV pool (no gradient).

@@ -131,3 +131,31 @@ def test_dummy_slot_parts(length, kv_heads):
     keep = ref.schedule_keep(meta, batch, length, length + 1)[:, None]
     assert keep[..., 0].all()
     _compare(q, k, v, dout, _kernels.Visibility(varlen=varlen), keep, repeats=2)
+
+
+def test_work_list_entries_with_segment_fields_match_pairs():
+    """The same packed schedule through work lists of (segment, tile) pairs
+    and of entries that carry the segment's bounds (unit_fields 16): the
+    kernels take the same values from the entry instead of reading cu_* and
+    the index arrays, so every output and gradient is bit-identical."""
+    batch, heads, dim, length = 2, 4, 128, 700
+    q, k, v, dout = _inputs(batch, heads, 2, length, dim, seed=23)
+    docs = torch.cumsum(torch.rand(batch, length, generator=torch.Generator().manual_seed(2)) < 0.01, 1).to(DEV)
+    md = prepare_strict_causal_metadata(docs, length)
+    max_q, max_k, flags = _schedule_flags(md)
+    results = []
+    for extent in (None, length):
+        units = _work_units(md, query_extent=extent)
+        assert units[0].shape[1] == (2 if extent is None else 16)
+        varlen = _kernels.Varlen(
+            md.query_indices, md.key_indices, md.cu_queries, md.cu_keys, md.cu_queries.numel() - 1, max_q, max_k,
+            length, length, bool(flags & 16), flags & 15, *units,
+        )
+        results.append(_run(q, k, v, dout, _kernels.Visibility(varlen=varlen), dim**-0.5, True))
+    # O rows of queries outside every segment are not written by the kernel
+    # (the operators zero them): compare the rows the schedule holds
+    rows = md.query_indices.long()
+    written = [o.transpose(1, 2).reshape(batch * length, heads * dim).index_select(0, rows) for o, *_ in results]
+    assert torch.equal(written[0], written[1])
+    for a, b in zip(results[0][1:], results[1][1:]):
+        assert torch.equal(a, b)

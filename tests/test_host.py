@@ -316,3 +316,37 @@ def test_covering_schedule_adds_rows_not_pairs(dummy):
     assert sorted(_np(cover.query_indices).tolist()) == list(range(2 * length))
     assert set(_np(cover.key_indices).tolist()) == set(range(2 * extent))
     assert _covering_schedule(schedule, 2, length, extent) is cover  # cached per call shape
+
+
+@pytest.mark.parametrize("dummy", [False, True])
+def test_work_list_entries_carry_segment_fields(dummy):
+    """The work-list entries with segment fields (wmx_attn_args unit_fields
+    16): each entry's segment and tile match the pair form's, and its fields
+    equal what the kernels would read from cu_queries, cu_keys, the index
+    arrays and ds_offsets (rows and slots of index elements 0 and 1)."""
+    from white_matter_amd import prepare_strict_causal_metadata
+    from white_matter_amd.strict_causal_attention import _work_units
+
+    gen = torch.Generator().manual_seed(17 + dummy)
+    length = 700
+    docs = torch.cumsum(torch.rand(3, length, generator=gen) < 0.01, 1)
+    md = prepare_strict_causal_metadata(docs, length, use_dummy_token=dummy)
+    pairs = _work_units(md)
+    full = _work_units(md, query_extent=length)
+    assert full[0].shape[1] == full[1].shape[1] == 16
+    for p, f in zip(pairs[:2], full[:2]):
+        assert torch.equal(p, f[:, :2])
+    assert torch.equal(pairs[2], full[2]) and pairs[3] == full[3]
+    cq, ck = md.cu_queries.tolist(), md.cu_keys.tolist()
+    qi, ki = md.query_indices.tolist(), md.key_indices.tolist()
+    offsets = full[2].tolist()
+    for entry in torch.cat(full[:2]).tolist():
+        s = entry[0]
+        qs, nq, ks, nk = cq[s], cq[s + 1] - cq[s], ck[s], ck[s + 1] - ck[s]
+        assert entry[2:6] == [qs, nq, ks, nk]
+        for base, start, n, index, extent in ((6, qs, nq, qi, length), (9, ks, nk, ki, md.key_extent)):
+            if n:
+                row, slot0 = divmod(index[start], extent)
+                slot1 = index[start + 1] - row * extent if n > 1 else slot0 + 1
+                assert entry[base : base + 3] == [row, slot0, slot1]
+        assert (entry[12] & 0xFFFFFFFF) | (entry[13] << 32) == offsets[s]

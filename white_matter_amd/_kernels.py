@@ -83,8 +83,10 @@ class Varlen:
     key_extent: int
     keys_unique: int  # wmx_attn_args.keys_unique: 1 unique, 2 only slot 0 repeats, 0 others repeat
     segment_layout: int = 0  # bit 0 consecutive queries, bit 1 consecutive keys from key 1
-    q_units: torch.Tensor | None = None  # int32 (n, 2) (segment, query tile), heaviest first
-    k_units: torch.Tensor | None = None  # int32 (n, 2) (segment, key tile), heaviest first
+    # work lists, heaviest first: int32 (n, 2) (segment, tile) or (n, UNIT_FIELDS)
+    # entries that also carry the segment's bounds (see _native.UNIT_FIELDS)
+    q_units: torch.Tensor | None = None  # query tiles
+    k_units: torch.Tensor | None = None  # key tiles
     ds_offsets: torch.Tensor | None = None  # int64 (num_segments + 1) dS block offsets (see wmx_attn.h)
     ds_elements: int = 0  # ds_offsets[-1]
 
@@ -135,6 +137,10 @@ class Visibility:
                 args.q_units, args.num_q_units = s.q_units.data_ptr(), s.q_units.shape[0]
             if s.k_units is not None:
                 args.k_units, args.num_k_units = s.k_units.data_ptr(), s.k_units.shape[0]
+            widths = {t.shape[1] for t in (s.q_units, s.k_units) if t is not None}
+            if len(widths) > 1:
+                raise ValueError("q_units and k_units must have entries of one width")
+            args.unit_fields = widths.pop() if widths else 0
             if s.ds_offsets is not None:
                 args.ds_offsets, args.ds_elements = s.ds_offsets.data_ptr(), s.ds_elements
 

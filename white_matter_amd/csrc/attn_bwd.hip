@@ -31,6 +31,12 @@
 
 namespace wmx {
 
+// Segment grp's dS block offset: from its work-list entry when it has one.
+__device__ __forceinline__ int64_t ds_offset_of(const wmx_attn_args& a, int grp, const int32_t* entry) {
+  if (entry) return (int64_t)(uint32_t)entry[WMX_UNIT_DS_LO] | ((int64_t)entry[WMX_UNIT_DS_HI] << 32);
+  return a.ds_offsets[grp];
+}
+
 // ---------------------------------------------------------------- delta ----
 // 16 lanes per row, 8 elements per lane; a thread takes kDeltaRows rows (16
 // apart) with all their loads issued before any is used, so each thread has
@@ -99,7 +105,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
 
   // this workgroup's unit: 128 query rows of one (batch row or segment, query head)
   TileUnit tu;
-  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true,  // heaviest (last) query tiles first
+            MODE == kVarlen ? a.unit_fields : 2);
   if (!tu.ok) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
@@ -107,7 +114,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   const int h = tu.head, grp = tu.grp;
   const int hk = h / (a.q_heads / a.kv_heads);
   Problem<MODE> pb;
-  pb.init(a, grp);
+  pb.init(a, grp, tu.entry);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
   if (q0 >= nq) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
@@ -313,7 +320,8 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
   const int32_t* list = a.q_units;  // (batch row or segment, tile) pairs, heaviest first
   const uint32_t count = list ? (uint32_t)a.num_q_units : (uint32_t)qtiles * outer;
   TileUnit tu;
-  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true,  // heaviest (last) query tiles first
+            MODE == kVarlen ? a.unit_fields : 2);
   if (!tu.ok) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
@@ -321,7 +329,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
   const int h = tu.head, grp = tu.grp;
   const int hk = h / (a.q_heads / a.kv_heads);
   Problem<MODE> pb;
-  pb.init(a, grp);
+  pb.init(a, grp, tu.entry);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
   if (q0 >= nq) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
@@ -370,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
   const int64_t ld = ds_ld(nq);
   const bf16* ds = (const bf16*)((const char*)a.workspace + bwd_ds_offset(a)) + q0;
   if constexpr (MODE == kVarlen) {
-    ds += h * a.ds_elements + a.ds_offsets[grp];
+    ds += h * a.ds_elements + ds_offset_of(a, grp, tu.entry);
   } else {
     ds += ((int64_t)b * a.q_heads + h) * a.kv_len * ld;
   }
@@ -521,7 +529,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
 
   // this workgroup's unit: 128 keys of one (batch row or segment, kv head)
   TileUnit tu;
-  tu.decode(a.kv_heads, count, list != nullptr, ktiles, list, (int)outer, false);  // low key tiles see the most queries
+  tu.decode(a.kv_heads, count, list != nullptr, ktiles, list, (int)outer, false,  // low key tiles see the most queries
+            MODE == kVarlen ? a.unit_fields : 2);
   if (!tu.ok) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
@@ -530,7 +539,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   const int n0 = tu.tile * BNK;
   const int hk = tu.head, grp = tu.grp;
   Problem<MODE> pb;
-  pb.init(a, grp);
+  pb.init(a, grp, tu.entry);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
   if (n0 >= nk) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
@@ -574,7 +583,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     bf16* ds = (bf16*)((char*)a.workspace + bwd_ds_offset(a));
     if constexpr (MODE == kVarlen) {
       ds_head = a.ds_elements;
-      ds += a.ds_offsets[grp];
+      ds += ds_offset_of(a, grp, tu.entry);
     } else {
       ds_head = (int64_t)a.kv_len * ld;
       ds += (int64_t)b * a.q_heads * ds_head;

@@ -61,7 +61,8 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void attn_fwd_kernel(cons
 
   // this workgroup's unit: BM query rows of one (batch row or segment, query head)
   TileUnit tu;
-  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true);  // heaviest (last) query tiles first
+  tu.decode(a.q_heads, count, list != nullptr, qtiles, list, (int)outer, true,  // heaviest (last) query tiles first
+            MODE == kVarlen ? a.unit_fields : 2);
   if (!tu.ok) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
@@ -69,7 +70,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void attn_fwd_kernel(cons
   const int h = tu.head, grp = tu.grp;
   const int hk = h / (a.q_heads / a.kv_heads);
   Problem<MODE> pb;
-  pb.init(a, grp);
+  pb.init(a, grp, tu.entry);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
   if (q0 >= nq) return;
   auto lim_of = [&](int i) { return pb.bound.lim(i); };

@@ -33,8 +33,13 @@ namespace wmx {
 struct TileUnit {
   int grp, tile, head;
   bool ok;
+  // the work-list entry with the segment's bounds (WMX_UNIT_FIELDS ints), or
+  // nullptr when the list holds (segment or row, tile) pairs only
+  const int32_t* entry;
+  // fields: ints per list entry (2, or WMX_UNIT_FIELDS)
   __device__ __forceinline__ void decode(int heads, uint32_t count, bool unit_major, int tiles,
-                                         const int32_t* list, int num_groups, bool descending) {
+                                         const int32_t* list, int num_groups, bool descending, int fields = 2) {
+    entry = nullptr;
     const uint32_t b = blockIdx.x, nh = (uint32_t)heads;
     uint32_t u;
     if ((nh & 7u) == 0) {
@@ -54,8 +59,10 @@ struct TileUnit {
     ok = u < count && head < heads;
     if (!ok) return;
     if (list) {
-      grp = __builtin_amdgcn_readfirstlane(list[2 * u]);
-      tile = __builtin_amdgcn_readfirstlane(list[2 * u + 1]);
+      const int32_t* e = list + (size_t)(fields >= WMX_UNIT_FIELDS ? WMX_UNIT_FIELDS : 2) * u;
+      grp = __builtin_amdgcn_readfirstlane(e[WMX_UNIT_SEGMENT]);
+      tile = __builtin_amdgcn_readfirstlane(e[WMX_UNIT_TILE]);
+      if (fields >= WMX_UNIT_FIELDS) entry = e;
     } else {
       const int t = (int)(u / (uint32_t)num_groups);
       grp = (int)(u - (uint32_t)t * num_groups);
@@ -91,19 +98,35 @@ struct Problem {
   Bounds bound;
   SegmentRows qrows, krows;  // varlen only
 
-  // grp = batch row or segment index. Returns false for an empty segment side.
-  __device__ __forceinline__ void init(const wmx_attn_args& a, int grp) {
+  // grp = batch row or segment index; entry = the unit's work-list entry
+  // with the segment's bounds, or nullptr (they are then read from
+  // cu_queries, cu_keys and the index arrays: three dependent loads).
+  __device__ __forceinline__ void init(const wmx_attn_args& a, int grp, const int32_t* entry = nullptr) {
     b = grp;
     if constexpr (MODE == kVarlen) {
-      const int qs = a.cu_queries[grp], ks = a.cu_keys[grp];
-      nq = a.cu_queries[grp + 1] - qs;
-      nk = a.cu_keys[grp + 1] - ks;
-      if (nq > 0)
-        qrows.init(a.query_indices + qs, nq, a.query_extent, a.segment_layout & kQueriesConsecutive,
-                   a.segment_layout & kQueriesOneRow, false);
-      if (nk > 0)
-        krows.init(a.key_indices + ks, nk, a.key_extent, a.segment_layout & kKeysConsecutive,
-                   a.segment_layout & kKeysOneRow, true);
+      if (entry) {
+        const int qs = entry[WMX_UNIT_QUERY_START], ks = entry[WMX_UNIT_KEY_START];
+        nq = entry[WMX_UNIT_QUERIES];
+        nk = entry[WMX_UNIT_KEYS];
+        if (nq > 0)
+          qrows.set(a.query_indices + qs, a.query_extent, a.segment_layout & kQueriesConsecutive,
+                    a.segment_layout & kQueriesOneRow, false, entry[WMX_UNIT_QUERY_ROW], entry[WMX_UNIT_QUERY_SLOT0],
+                    entry[WMX_UNIT_QUERY_SLOT1]);
+        if (nk > 0)
+          krows.set(a.key_indices + ks, a.key_extent, a.segment_layout & kKeysConsecutive,
+                    a.segment_layout & kKeysOneRow, true, entry[WMX_UNIT_KEY_ROW], entry[WMX_UNIT_KEY_SLOT0],
+                    entry[WMX_UNIT_KEY_SLOT1]);
+      } else {
+        const int qs = a.cu_queries[grp], ks = a.cu_keys[grp];
+        nq = a.cu_queries[grp + 1] - qs;
+        nk = a.cu_keys[grp + 1] - ks;
+        if (nq > 0)
+          qrows.init(a.query_indices + qs, nq, a.query_extent, a.segment_layout & kQueriesConsecutive,
+                     a.segment_layout & kQueriesOneRow, false);
+        if (nk > 0)
+          krows.init(a.key_indices + ks, nk, a.key_extent, a.segment_layout & kKeysConsecutive,
+                     a.segment_layout & kKeysOneRow, true);
+      }
       // query i sees keys 0 .. nk - 1 - stride * (nq - 1 - i): the last query
       // sees every key of the segment (bottom-right causal at stride 1)
       bound = Bounds{(int64_t)nk - 1 - (int64_t)a.query_stride * (nq - 1), INT_MAX, a.query_stride, nk};

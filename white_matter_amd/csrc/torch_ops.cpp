@@ -223,6 +223,8 @@ void fill_visibility(wmx_attn_args& a, const Schedule* s, int64_t stride, int64_
     a.num_q_units = (int32_t)s->q_units.size(0);
     a.k_units = s->k_units.data_ptr<int32_t>();
     a.num_k_units = (int32_t)s->k_units.size(0);
+    TORCH_CHECK(s->q_units.size(1) == s->k_units.size(1), "q_units and k_units must have entries of one width");
+    a.unit_fields = (int32_t)s->q_units.size(1);
     if (backward) {
       a.ds_offsets = s->ds_offsets.data_ptr<int64_t>();
       a.ds_elements = s->ds_elements;

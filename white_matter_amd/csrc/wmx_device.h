@@ -152,6 +152,18 @@ struct SegmentRows {
     slot0 = t0;
     slot1 = count > 1 ? (int)(first[1] - row_base) : t0 + 1;
   }
+  // The same from the entry's precomputed row and slots of elements 0 and 1.
+  __device__ __forceinline__ void set(const int64_t* first, int extent_, bool consecutive, bool one_row, bool from_one_,
+                                      int row_, int slot0_, int slot1_) {
+    idx = first;
+    extent = extent_;
+    layout = (consecutive ? 1 : 0) | (one_row ? 2 : 0);
+    from_one = from_one_;
+    row = row_;
+    row_base = (int64_t)row * extent;
+    slot0 = slot0_;
+    slot1 = slot1_;
+  }
   __device__ __forceinline__ void locate(int j, int& b, int& t) const {
     if (layout & 1) {
       b = row;

@@ -224,7 +224,7 @@ def _cyclic_schedule(
         # every row with atomics; the document-mode kernels keep one key row
         # per slot (dummy slots alone go through small accumulators)
         return [facts(0)]
-    q_units, k_units, ds_offsets, ds_elements = _work_units(schedule, stride)
+    q_units, k_units, ds_offsets, ds_elements = _work_units(schedule, stride, query_extent=q_len)
     return [
         facts(2, schedule.cu_queries.numel() - 1, max_q, max_k, flags & 15, unique, ds_elements),
         schedule.query_indices, schedule.key_indices, schedule.cu_queries, schedule.cu_keys,

@@ -233,7 +233,7 @@ class TorchFlashVarlen(torch.autograd.Function):
         q, k, v = (_kernels.pad_head_dim(t, size).unsqueeze(0).transpose(1, 2) for t in (query, key, value))
         schedule = _packed_schedule(cu_q, cu_k, max_q, max_k, key.shape[0])
         max_q_, max_k_, flags = _schedule_flags(schedule)
-        units = _work_units(schedule)
+        units = _work_units(schedule, query_extent=query.shape[0])
         none = _empty_rows(query.device)
         out, lse = strict_varlen_fwd(
             q, k, v, schedule.query_indices, schedule.key_indices, schedule.cu_queries, schedule.cu_keys,
@@ -255,7 +255,7 @@ class TorchFlashVarlen(torch.autograd.Function):
         none = _empty_rows(query.device)
         dq, dk, dv = strict_varlen_bwd(
             q, k, v, out, lse, dout, s.query_indices, s.key_indices, s.cu_queries, s.cu_keys,
-            max_q, max_k, flags, ctx.scale, none, none, *_work_units(s),
+            max_q, max_k, flags, ctx.scale, none, none, *_work_units(s, query_extent=query.shape[0]),
         )
         return (
             dq[0].transpose(0, 1)[..., :dim].to(query.dtype),

@@ -24,7 +24,7 @@ from typing import Literal
 
 import torch
 
-from . import _kernels, portable
+from . import _kernels, _native, portable
 
 _BACKENDS = ("auto", "reference", "torch_flash", "flash_attention_2")
 
@@ -548,21 +548,28 @@ def _covering_schedule(metadata: StrictCausalMetadata, batch: int, length: int, 
 
 
 def _work_units(
-    metadata: StrictCausalMetadata, stride: int = 1
+    metadata: StrictCausalMetadata, stride: int = 1, query_extent: int | None = None
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
     """The kernels' work lists and dS layout, cached on the metadata object per
-    query stride: the (segment, tile) units of the query-tiled kernels
-    (forward, dQ: 128 rows) and of the key-tiled kernel (dK/dV: 128 keys),
-    heaviest first, as int32 (n, 2) device tensors, and the int64
+    query stride and entry form: the (segment, tile) units of the query-tiled
+    kernels (forward, dQ: 128 rows) and of the key-tiled kernel (dK/dV: 128
+    keys), heaviest first, as int32 device tensors, and the int64
     (num_segments + 1) offsets of the segments' dS blocks (keys x queries
     rounded up to 128 elements each) with their total. A unit's cost is the
     number of 64-row tiles its loop visits (then its row count): query i of a
     segment with nq queries and nk keys sees keys 0 .. nk - 1 - stride *
     (nq - 1 - i) (bottom-right causal at stride 1); a query tile visits the
     key tiles up to its last row's bound, a key tile the query tiles from the
-    one holding the first row that sees its first key."""
+    one holding the first row that sees its first key.
+
+    Without `query_extent` an entry is the (segment, tile) pair. With it (the
+    query rows' storage width, query.shape[2] of the call) an entry holds
+    _native.UNIT_FIELDS ints that also carry the segment's bounds, its first
+    query and key rows and slots, and its dS offset (wmx_attn_args
+    unit_fields): a workgroup then reads its entry alone before loading rows,
+    not cu_queries, cu_keys and the index arrays one after another."""
     by_stride = metadata.__dict__.setdefault("_units", {})
-    units = by_stride.get(stride)
+    units = by_stride.get((stride, query_extent))
     if units is None:
         _kernels.guard_capture("building the work lists of a packed-document schedule")
         q_units, k_units, ds_blocks = [], [], []
@@ -580,15 +587,55 @@ def _work_units(
                 steps = -(-(nq - first // _STEP * _STEP) // _STEP) if first < nq else 0
                 k_units.append(((steps, keys), s, t))
         device = metadata.query_indices.device
+        offsets = torch.tensor([0] + ds_blocks, dtype=torch.int64).cumsum(0)
+        fields = None if query_extent is None else _segment_fields(metadata, query_extent, offsets)
 
         def table(entries):
             entries.sort(key=lambda e: (-e[0][0], -e[0][1], e[1], e[2]))
-            flat = [v for _, seg, tile in entries for v in (seg, tile)]
-            return torch.tensor(flat, dtype=torch.int32).view(-1, 2).to(device)
+            if fields is None:
+                flat = [v for _, seg, tile in entries for v in (seg, tile)]
+                return torch.tensor(flat, dtype=torch.int32).view(-1, 2).to(device)
+            seg = torch.tensor([seg for _, seg, _ in entries], dtype=torch.long)
+            out = fields.index_select(0, seg)
+            out[:, 1] = torch.tensor([tile for _, _, tile in entries], dtype=torch.int32)
+            return out.to(device)
 
-        offsets = torch.tensor([0] + ds_blocks, dtype=torch.int64).cumsum(0)
-        units = by_stride[stride] = (table(q_units), table(k_units), offsets.to(device), int(offsets[-1]))
+        units = by_stride[(stride, query_extent)] = (table(q_units), table(k_units), offsets.to(device), int(offsets[-1]))
     return units
+
+
+def _segment_fields(metadata: StrictCausalMetadata, query_extent: int, ds_offsets: torch.Tensor) -> torch.Tensor:
+    """Per segment the int32 fields of a work-list entry (wmx_attn_args
+    unit_fields, WMX_UNIT_* in wmx_attn.h): segment, tile (filled per entry),
+    query start and count, key start and count, the row and the slots of
+    index elements 0 and 1 of each side (slot 1 = slot 0 + 1 for a
+    one-element side; zeros for an empty side), and the dS offset's halves."""
+    segments = torch.tensor(metadata.segments, dtype=torch.int64).view(-1, 4)
+    count = segments.shape[0]
+    out = torch.zeros(count, _native.UNIT_FIELDS, dtype=torch.int64)
+    out[:, 0] = torch.arange(count)
+    out[:, 2], out[:, 3] = segments[:, 0], segments[:, 1] - segments[:, 0]
+    out[:, 4], out[:, 5] = segments[:, 2], segments[:, 3] - segments[:, 2]
+    for column, start, n, index, extent in (
+        (6, out[:, 2], out[:, 3], metadata.query_indices, query_extent),
+        (9, out[:, 4], out[:, 5], metadata.key_indices, metadata.key_extent),
+    ):
+        if index.numel():
+            last = index.numel() - 1
+            picked = index.index_select(0, torch.cat((start.clamp_max(last), (start + 1).clamp_max(last))).to(index.device))
+            e0, e1 = picked.cpu().view(2, count)
+            row = torch.div(e0, extent, rounding_mode="floor")
+            slot0 = e0 - row * extent
+            slot1 = torch.where(n > 1, e1 - row * extent, slot0 + 1)
+            live = n > 0
+            out[:, column] = torch.where(live, row, 0)
+            out[:, column + 1] = torch.where(live, slot0, 0)
+            out[:, column + 2] = torch.where(live, slot1, 0)
+    ds = ds_offsets[:-1]
+    out[:, 12], out[:, 13] = ds & 0xFFFFFFFF, ds >> 32
+    if bool((out[:, :12].abs() > torch.iinfo(torch.int32).max).any()):
+        raise ValueError("packed-document schedule fields exceed int32")
+    return out.to(torch.int32)  # the offset's low half wraps into int32 bit for bit
 
 
 def _varlen(
@@ -809,7 +856,7 @@ def _packed_plan(qi, ki, cq, ck, max_queries, max_keys, batch, length, key_slots
     plan.cover = None if cover is metadata else cover
     plan.max_q, plan.max_k, plan.flags = _schedule_flags(cover)
     plan.gaps = _schedule_gaps(cover, batch, length, heads, key_slots, kv_heads)
-    plan.units = _work_units(cover)
+    plan.units = _work_units(cover, query_extent=length)
     by_shape[shape] = plan
     return plan
 

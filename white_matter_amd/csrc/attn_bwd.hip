@@ -32,9 +32,8 @@
 namespace wmx {
 
 // Segment grp's dS block offset: from its work-list entry when it has one.
-__device__ __forceinline__ int64_t ds_offset_of(const wmx_attn_args& a, int grp, const int32_t* entry) {
-  if (entry) return (int64_t)(uint32_t)entry[WMX_UNIT_DS_LO] | ((int64_t)entry[WMX_UNIT_DS_HI] << 32);
-  return a.ds_offsets[grp];
+__device__ __forceinline__ int64_t ds_offset_of(const wmx_attn_args& a, int grp, const TileUnit& tu) {
+  return tu.has_fields ? tu.ds_off : a.ds_offsets[grp];
 }
 
 // ---------------------------------------------------------------- delta ----
@@ -114,7 +113,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_kernel(const wmx_attn_args
   const int h = tu.head, grp = tu.grp;
   const int hk = h / (a.q_heads / a.kv_heads);
   Problem<MODE> pb;
-  pb.init(a, grp, tu.entry);
+  pb.init(a, grp, tu);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
   if (q0 >= nq) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
@@ -329,7 +328,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
   const int h = tu.head, grp = tu.grp;
   const int hk = h / (a.q_heads / a.kv_heads);
   Problem<MODE> pb;
-  pb.init(a, grp, tu.entry);
+  pb.init(a, grp, tu);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
   if (q0 >= nq) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
@@ -378,7 +377,7 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
   const int64_t ld = ds_ld(nq);
   const bf16* ds = (const bf16*)((const char*)a.workspace + bwd_ds_offset(a)) + q0;
   if constexpr (MODE == kVarlen) {
-    ds += h * a.ds_elements + ds_offset_of(a, grp, tu.entry);
+    ds += h * a.ds_elements + ds_offset_of(a, grp, tu);
   } else {
     ds += ((int64_t)b * a.q_heads + h) * a.kv_len * ld;
   }
@@ -539,7 +538,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   const int n0 = tu.tile * BNK;
   const int hk = tu.head, grp = tu.grp;
   Problem<MODE> pb;
-  pb.init(a, grp, tu.entry);
+  pb.init(a, grp, tu);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
   if (n0 >= nk) return;
   const bool slot0 = a.keep_slot0 && nk > 0;
@@ -583,7 +582,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     bf16* ds = (bf16*)((char*)a.workspace + bwd_ds_offset(a));
     if constexpr (MODE == kVarlen) {
       ds_head = a.ds_elements;
-      ds += ds_offset_of(a, grp, tu.entry);
+      ds += ds_offset_of(a, grp, tu);
     } else {
       ds_head = (int64_t)a.kv_len * ld;
       ds += (int64_t)b * a.q_heads * ds_head;

@@ -70,7 +70,7 @@ __global__ __launch_bounds__(64 * NW, NW == 4 ? 2 : 1) void attn_fwd_kernel(cons
   const int h = tu.head, grp = tu.grp;
   const int hk = h / (a.q_heads / a.kv_heads);
   Problem<MODE> pb;
-  pb.init(a, grp, tu.entry);
+  pb.init(a, grp, tu);
   const int b = pb.b, nq = pb.nq, nk = pb.nk;
   if (q0 >= nq) return;
   auto lim_of = [&](int i) { return pb.bound.lim(i); };

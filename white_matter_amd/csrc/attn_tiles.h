@@ -33,13 +33,16 @@ namespace wmx {
 struct TileUnit {
   int grp, tile, head;
   bool ok;
-  // the work-list entry with the segment's bounds (WMX_UNIT_FIELDS ints), or
-  // nullptr when the list holds (segment or row, tile) pairs only
-  const int32_t* entry;
+  // the segment's bounds from a work-list entry that carries them (read
+  // together, kept in scalar registers); has_fields is false when the list
+  // holds (segment or row, tile) pairs only
+  bool has_fields;
+  int qs, nq, ks, nk, qrow, qslot0, qslot1, krow, kslot0, kslot1;
+  int64_t ds_off;
   // fields: ints per list entry (2, or WMX_UNIT_FIELDS)
   __device__ __forceinline__ void decode(int heads, uint32_t count, bool unit_major, int tiles,
                                          const int32_t* list, int num_groups, bool descending, int fields = 2) {
-    entry = nullptr;
+    has_fields = false;
     const uint32_t b = blockIdx.x, nh = (uint32_t)heads;
     uint32_t u;
     if ((nh & 7u) == 0) {
@@ -60,9 +63,23 @@ struct TileUnit {
     if (!ok) return;
     if (list) {
       const int32_t* e = list + (size_t)(fields >= WMX_UNIT_FIELDS ? WMX_UNIT_FIELDS : 2) * u;
+      if (fields >= WMX_UNIT_FIELDS) {
+        has_fields = true;
+        auto rd = [&](int f) { return __builtin_amdgcn_readfirstlane(e[f]); };
+        qs = rd(WMX_UNIT_QUERY_START);
+        nq = rd(WMX_UNIT_QUERIES);
+        ks = rd(WMX_UNIT_KEY_START);
+        nk = rd(WMX_UNIT_KEYS);
+        qrow = rd(WMX_UNIT_QUERY_ROW);
+        qslot0 = rd(WMX_UNIT_QUERY_SLOT0);
+        qslot1 = rd(WMX_UNIT_QUERY_SLOT1);
+        krow = rd(WMX_UNIT_KEY_ROW);
+        kslot0 = rd(WMX_UNIT_KEY_SLOT0);
+        kslot1 = rd(WMX_UNIT_KEY_SLOT1);
+        ds_off = (int64_t)(uint32_t)rd(WMX_UNIT_DS_LO) | ((int64_t)rd(WMX_UNIT_DS_HI) << 32);
+      }
       grp = __builtin_amdgcn_readfirstlane(e[WMX_UNIT_SEGMENT]);
       tile = __builtin_amdgcn_readfirstlane(e[WMX_UNIT_TILE]);
-      if (fields >= WMX_UNIT_FIELDS) entry = e;
     } else {
       const int t = (int)(u / (uint32_t)num_groups);
       grp = (int)(u - (uint32_t)t * num_groups);
@@ -85,7 +102,12 @@ struct Bounds {
   __device__ __forceinline__ int first_row(int j, int nq) const {
     if (j > nk - 1 || limit < j) return nq;
     const int64_t need = (int64_t)j - offset;
-    const int64_t m = need <= 0 ? 0 : (need + stride - 1) / stride;
+    if (need <= 0) return 0;
+    if (stride == 1) return need < nq ? (int)need : nq;
+    const int64_t num = need + stride - 1;
+    // a 32-bit division where the operands fit (the 64-bit one is a long
+    // instruction sequence in every workgroup's setup)
+    const int64_t m = num <= INT32_MAX ? (int64_t)((uint32_t)num / (uint32_t)stride) : num / stride;
     return m < nq ? (int)m : nq;
   }
 };
@@ -98,24 +120,21 @@ struct Problem {
   Bounds bound;
   SegmentRows qrows, krows;  // varlen only
 
-  // grp = batch row or segment index; entry = the unit's work-list entry
-  // with the segment's bounds, or nullptr (they are then read from
-  // cu_queries, cu_keys and the index arrays: three dependent loads).
-  __device__ __forceinline__ void init(const wmx_attn_args& a, int grp, const int32_t* entry = nullptr) {
+  // grp = batch row or segment index; the bounds come from the unit's
+  // work-list entry when it carries them, else from cu_queries, cu_keys and
+  // the index arrays (three dependent loads).
+  __device__ __forceinline__ void init(const wmx_attn_args& a, int grp, const TileUnit& tu) {
     b = grp;
     if constexpr (MODE == kVarlen) {
-      if (entry) {
-        const int qs = entry[WMX_UNIT_QUERY_START], ks = entry[WMX_UNIT_KEY_START];
-        nq = entry[WMX_UNIT_QUERIES];
-        nk = entry[WMX_UNIT_KEYS];
+      if (tu.has_fields) {
+        nq = tu.nq;
+        nk = tu.nk;
         if (nq > 0)
-          qrows.set(a.query_indices + qs, a.query_extent, a.segment_layout & kQueriesConsecutive,
-                    a.segment_layout & kQueriesOneRow, false, entry[WMX_UNIT_QUERY_ROW], entry[WMX_UNIT_QUERY_SLOT0],
-                    entry[WMX_UNIT_QUERY_SLOT1]);
+          qrows.set(a.query_indices + tu.qs, a.query_extent, a.segment_layout & kQueriesConsecutive,
+                    a.segment_layout & kQueriesOneRow, false, tu.qrow, tu.qslot0, tu.qslot1);
         if (nk > 0)
-          krows.set(a.key_indices + ks, a.key_extent, a.segment_layout & kKeysConsecutive,
-                    a.segment_layout & kKeysOneRow, true, entry[WMX_UNIT_KEY_ROW], entry[WMX_UNIT_KEY_SLOT0],
-                    entry[WMX_UNIT_KEY_SLOT1]);
+          krows.set(a.key_indices + tu.ks, a.key_extent, a.segment_layout & kKeysConsecutive,
+                    a.segment_layout & kKeysOneRow, true, tu.krow, tu.kslot0, tu.kslot1);
       } else {
         const int qs = a.cu_queries[grp], ks = a.cu_keys[grp];
         nq = a.cu_queries[grp + 1] - qs;

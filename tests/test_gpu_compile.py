@@ -134,3 +134,60 @@ def test_fullgraph_cyclic_with_documents(dummy):
         strict_past=not dummy, metadata=tuple(t.cpu() for t in meta),
     )
     torch.testing.assert_close(actual.double().cpu(), expected, atol=0.03, rtol=0.03)
+
+
+def test_fullgraph_k_norm_rope_forward_and_backward():
+    """The store's key transform as the registered operator
+    (white_matter::k_norm_rope) traced whole, forward and backward, equal to
+    eager bit for bit (training projects keys through it,
+    modules/kv_pool.py:213-216)."""
+    from white_matter_amd import kv_pool
+
+    torch._dynamo.reset()
+    gen = torch.Generator().manual_seed(4)
+    key = torch.randn(2, 3, 2, 40, 64, generator=gen).to(DEV).requires_grad_()
+    weight = (1 + 0.1 * torch.randn(3, 64, generator=gen)).to(DEV).requires_grad_()
+    angle = torch.rand(2, 40, 32, generator=gen).to(DEV) * 7.0
+    angle = torch.cat((angle, angle), -1)
+    cos, sin = angle.cos(), angle.sin()
+
+    def run(key, weight):
+        return kv_pool.k_norm_rope(key, weight, cos, sin)
+
+    actual = torch.compile(run, fullgraph=True)(key, weight)
+    eager = run(key, weight)
+    torch.testing.assert_close(actual, eager, atol=0, rtol=0)
+    probe = torch.randn(actual.shape, generator=gen).to(DEV, torch.bfloat16)
+    ga = torch.autograd.grad(actual, (key, weight), probe)
+    ge = torch.autograd.grad(eager, (key, weight), probe)
+    for a, e in zip(ga, ge, strict=True):
+        torch.testing.assert_close(a, e, atol=0, rtol=0)
+
+
+@torch.no_grad()
+def test_fullgraph_kv_producer():
+    """kv_pool.projection_inputs (the HIP producer around the router GEMM:
+    the operators white_matter::kv_premix and white_matter::kv_mix) traced
+    whole, equal to eager bit for bit."""
+    from white_matter_amd import kv_pool
+
+    torch._dynamo.reset()
+    gen = torch.Generator().manual_seed(8)
+    batch, tokens, sources, hidden, channels = 2, 5, 7, 256, 3
+    stacked = torch.randn(batch, tokens, sources, hidden, generator=gen).to(DEV)
+    pre_mix = tuple((1 + 0.2 * torch.randn(sources, hidden, generator=gen)).bfloat16().to(DEV) for _ in range(2))
+    router = tuple(
+        ((torch.randn(channels * sources, sources * hidden, generator=gen) * 0.01).bfloat16().to(DEV),
+         (torch.randn(channels * sources, generator=gen) * 0.25).bfloat16().to(DEV))
+        for _ in range(2)
+    )
+    gain = tuple((1 + 0.2 * torch.randn(channels, hidden, generator=gen)).bfloat16().to(DEV) for _ in range(2))
+
+    def run(x):
+        return kv_pool.projection_inputs(x, pre_mix, router, gain, eps=1e-6, mix_eps=1e-4)
+
+    compiled = torch.compile(run, fullgraph=True)(stacked)
+    eager = run(stacked)
+    for c, e in zip(compiled, eager, strict=True):
+        assert c.shape == (channels, batch * tokens, hidden)
+        torch.testing.assert_close(c, e, atol=0, rtol=0)

@@ -184,6 +184,75 @@ def _weights(t: torch.Tensor, dtype: torch.dtype) -> torch.Tensor:
     return t.to(dtype).contiguous()
 
 
+def _weight_dtype(*weights: torch.Tensor) -> torch.dtype:
+    return torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in weights) else torch.float32
+
+
+@torch.library.custom_op("white_matter::kv_premix", mutates_args=())
+def kv_premix(stacked: torch.Tensor, pre_mix_k: torch.Tensor, pre_mix_v: torch.Tensor, eps: float) -> torch.Tensor:
+    """Both premixed stacks (2, B*T, S*hidden) bf16 of (B, T, S, hidden)
+    sources (wmx_kv_premix; shapes checked by `projection_inputs`)."""
+    batch, tokens, sources, hidden = stacked.shape
+    ok = stacked.stride(-1) == 1 and stacked.data_ptr() % 16 == 0 and all(st % 8 == 0 for st in stacked.stride()[:3])
+    x = stacked if ok else stacked.contiguous()
+    wdtype = _weight_dtype(pre_mix_k, pre_mix_v)
+    pre = [_weights(w, wdtype) for w in (pre_mix_k, pre_mix_v)]
+    premixed = torch.empty(2, batch * tokens, sources * hidden, device=stacked.device, dtype=torch.bfloat16)
+    a = _native.KvMixArgs()
+    a.sources, a.source_stride = x.data_ptr(), x.stride()[:3]
+    a.source_dtype, a.weight_dtype = _DTYPES[x.dtype], _DTYPES[wdtype]
+    a.batch, a.tokens, a.num_sources, a.hidden, a.channels = batch, tokens, sources, hidden, 1
+    a.eps = float(eps)
+    for side in range(2):
+        a.pre_mix[side] = pre[side].data_ptr()
+        a.premixed[side] = premixed[side].data_ptr()
+    _native.kv_premix(a, stacked.device)
+    return premixed
+
+
+@kv_premix.register_fake
+def _(stacked, pre_mix_k, pre_mix_v, eps):
+    batch, tokens, sources, hidden = stacked.shape
+    return stacked.new_empty((2, batch * tokens, sources * hidden), dtype=torch.bfloat16)
+
+
+@torch.library.custom_op("white_matter::kv_mix", mutates_args=())
+def kv_mix(
+    premixed: torch.Tensor, alpha_k: torch.Tensor, alpha_v: torch.Tensor, gain_k: torch.Tensor, gain_v: torch.Tensor,
+    mix_eps: float,
+) -> torch.Tensor:
+    """The channel rows (2, C, B*T, hidden) bf16 (wmx_kv_mix) from both
+    premixed stacks (2, B*T, S*hidden) and both sides' (B*T, C*S) logits."""
+    _, rows, width = premixed.shape
+    channels, hidden = gain_k.shape
+    sources = width // hidden
+    wdtype = _weight_dtype(gain_k, gain_v)
+    gains = [_weights(g, wdtype) for g in (gain_k, gain_v)]
+    alphas = [t if t.stride(-1) == 1 else t.contiguous() for t in (alpha_k, alpha_v)]
+    if rows > 1 and alphas[0].stride(0) != alphas[1].stride(0):
+        alphas = [t.contiguous() for t in alphas]
+    premixed = premixed.contiguous()
+    mixed = torch.empty(2, channels, rows, hidden, device=premixed.device, dtype=torch.bfloat16)
+    a = _native.KvMixArgs()
+    a.weight_dtype, a.source_dtype = _DTYPES[wdtype], _native.DTYPE_BF16
+    a.batch, a.tokens, a.num_sources, a.hidden, a.channels = 1, rows, sources, hidden, channels
+    a.mix_eps = float(mix_eps)
+    a.alpha_stride = alphas[0].stride(0) if rows > 1 else channels * sources
+    for side in range(2):
+        a.premixed[side] = premixed[side].data_ptr()
+        a.alpha[side] = alphas[side].data_ptr()
+        a.gain[side] = gains[side].data_ptr()
+        a.mixed[side] = mixed[side].data_ptr()
+    _native.kv_mix(a, premixed.device)
+    return mixed
+
+
+@kv_mix.register_fake
+def _(premixed, alpha_k, alpha_v, gain_k, gain_v, mix_eps):
+    channels, hidden = gain_k.shape
+    return premixed.new_empty((2, channels, premixed.shape[1], hidden), dtype=torch.bfloat16)
+
+
 def projection_inputs(
     stacked: torch.Tensor,
     pre_mix: tuple[torch.Tensor, torch.Tensor],
@@ -206,6 +275,8 @@ def projection_inputs(
       m = bf16(sum_s alpha[c, s] * p[s])               (HIP, wmx_kv_mix)
       h = bf16(rms_norm(m, mix_eps) * gain[c])
     Forward only (the reference's training form runs under checkpointing).
+    The two HIP steps are the operators white_matter::kv_premix and
+    white_matter::kv_mix, so the whole function traces under torch.compile.
     """
     if torch.is_grad_enabled() and any(
         t.requires_grad for t in (stacked, *pre_mix, *gain, *router[0], *router[1])
@@ -213,7 +284,7 @@ def projection_inputs(
         raise RuntimeError("projection_inputs is forward-only; use the reference's eager sequence under autograd")
     if stacked.ndim != 4:
         raise ValueError("stacked must be (B, T, S, hidden)")
-    batch, tokens, sources, hidden = stacked.shape
+    sources, hidden = stacked.shape[2:]
     if not stacked.is_cuda:
         raise RuntimeError("projection_inputs runs on the HIP kernels: stacked must be a GPU tensor")
     if stacked.dtype not in _DTYPES:
@@ -233,37 +304,10 @@ def projection_inputs(
     for weight, bias in router:
         if weight.shape != (channels * sources, sources * hidden) or bias.shape != (channels * sources,):
             raise ValueError("router weights must be (C*S, S*hidden) with a (C*S,) bias")
-    device = stacked.device
-    ok = stacked.stride(-1) == 1 and stacked.data_ptr() % 16 == 0 and all(s % 8 == 0 for s in stacked.stride()[:3])
-    x = stacked if ok else stacked.contiguous()
-    wdtype = torch.bfloat16 if all(t.dtype == torch.bfloat16 for t in (*pre_mix, *gain)) else torch.float32
-    pre = [_weights(w, wdtype) for w in pre_mix]
-    gains = [_weights(g, wdtype) for g in gain]
-    rows = batch * tokens
-    premixed = torch.empty(2, rows, sources * hidden, device=device, dtype=torch.bfloat16)
-    mixed = torch.empty(2, channels, rows, hidden, device=device, dtype=torch.bfloat16)
-    a = _native.KvMixArgs()
-    a.sources, a.source_stride = x.data_ptr(), x.stride()[:3]
-    a.source_dtype, a.weight_dtype = _DTYPES[x.dtype], _DTYPES[wdtype]
-    a.batch, a.tokens, a.num_sources, a.hidden, a.channels = batch, tokens, sources, hidden, channels
-    a.eps, a.mix_eps = float(eps), float(mix_eps)
-    for side in range(2):
-        a.pre_mix[side] = pre[side].data_ptr()
-        a.premixed[side] = premixed[side].data_ptr()
-        a.gain[side] = gains[side].data_ptr()
-        a.mixed[side] = mixed[side].data_ptr()
-    _native.kv_premix(a, device)
+    premixed = torch.ops.white_matter.kv_premix(stacked, pre_mix[0], pre_mix[1], float(eps))
     alphas = [
         F.linear(premixed[side], weight.to(torch.bfloat16), bias.to(torch.bfloat16))
         for side, (weight, bias) in enumerate(router)
     ]
-    for side in range(2):
-        if alphas[side].stride(-1) != 1:
-            alphas[side] = alphas[side].contiguous()
-        a.alpha[side] = alphas[side].data_ptr()
-    if alphas[0].stride(0) != alphas[1].stride(0):
-        alphas = [t.contiguous() for t in alphas]
-        a.alpha[0], a.alpha[1] = alphas[0].data_ptr(), alphas[1].data_ptr()
-    a.alpha_stride = alphas[0].stride(0) if rows > 1 else channels * sources
-    _native.kv_mix(a, device)
+    mixed = torch.ops.white_matter.kv_mix(premixed, alphas[0], alphas[1], gain[0], gain[1], float(mix_eps))
     return mixed[0], mixed[1]

@@ -272,17 +272,25 @@ __device__ __forceinline__ bf16x8 lds_row_operand(const bf16* t, int ld, int row
 }
 
 // Store an accumulator holding X^T (rows d, column = this lane's row) as
-// bf16 row x[d] scaled by `scale`: 4 consecutive d per 8-byte store.
+// bf16 row x[d] scaled by `scale`. Lane (row, half) holds, per block d and
+// group g, the columns d 32 + 8 g + 4 half + [0, 4); swapping dwords with its
+// partner (lane ^ 32, the same row) gives it the 8 columns
+// d 32 + 16 t + 8 half + [0, 8) of group pair t: one 16-byte store each. Both
+// lanes of a pair must be active (they hold the same row).
 template <int DB>
 __device__ __forceinline__ void store_acc_row(bf16* row, const f32x16 (&acc)[DB], float scale, int half) {
 #pragma unroll
   for (int d = 0; d < DB; ++d) {
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      u32x2 w;
-      w[0] = pack_bf16x2(acc[d][4 * g + 0] * scale, acc[d][4 * g + 1] * scale);
-      w[1] = pack_bf16x2(acc[d][4 * g + 2] * scale, acc[d][4 * g + 3] * scale);
-      store8(row + d * 32 + 8 * g + 4 * half, w);
+    for (int t = 0; t < 2; ++t) {
+      const int r = 8 * t;
+      const u32x4 w = {pack_bf16x2(acc[d][r + 0] * scale, acc[d][r + 1] * scale),
+                       pack_bf16x2(acc[d][r + 2] * scale, acc[d][r + 3] * scale),
+                       pack_bf16x2(acc[d][r + 4] * scale, acc[d][r + 5] * scale),
+                       pack_bf16x2(acc[d][r + 6] * scale, acc[d][r + 7] * scale)};
+      const auto lo = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
+      const auto hi = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
+      *reinterpret_cast<u32x4*>(row + d * 32 + 16 * t + 8 * half) = u32x4{lo[0], hi[0], lo[1], hi[1]};
     }
   }
 }

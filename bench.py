@@ -53,6 +53,8 @@ KERNEL_NAMES = {  # rocprof kernel name prefix -> bench kernel key
     "wmx::decode_combine_kernel": "decode_combine",
     "wmx::kv_premix_kernel": "kv_premix",
     "wmx::kv_mix_kernel": "kv_mix",
+    "wmx::kv_router_kernel": "kv_router",
+    "wmx::kv_router_reduce_kernel": "kv_router_reduce",
 }
 METRIC = "attn fwd+bwd TFLOP/s (bf16, T=2048) and % MFMA peak; decode GB/s"
 

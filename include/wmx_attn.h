@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 7
+#define WMX_ABI_VERSION 8
 
 enum {
   WMX_OK = 0,
@@ -342,6 +342,30 @@ typedef struct wmx_kv_mix_args {
 } wmx_kv_mix_args;
 
 /*
+ * The router logits between the two producer steps, for both sides in one
+ * launch: alpha[side] = bf16(premixed[side] . weight[side]^T + bias[side])
+ * (reference modules/routing.py:77-115 `Router.forward`, the bf16 nn.Linear
+ * over the premixed row). Each workgroup multiplies 128 rows by all logits
+ * over one 1024-input chunk on the MFMA units (fp32 sums of bf16 products);
+ * the chunks' fp32 partial sums go to the workspace and a second kernel adds
+ * them in chunk order with the bias and rounds once to bf16. The library GEMM
+ * of this shape (few logits, long inputs) runs on 32 workgroups.
+ */
+#define WMX_KV_ROUTER_MAX_LOGITS 256
+
+typedef struct wmx_kv_router_args {
+  const void* premixed[2];    /* bf16 (rows, inputs) contiguous, K side and V side */
+  const void* weight[2];      /* bf16 (logits, inputs) contiguous */
+  const void* bias[2];        /* bf16 (logits,), or NULL for none */
+  void* alpha[2];             /* bf16 (rows, logits) contiguous */
+  void* workspace;            /* wmx_kv_router_workspace_size bytes, 16-byte aligned */
+  int64_t workspace_bytes;
+  int32_t rows;               /* B*T */
+  int32_t inputs;             /* S*hidden, a positive multiple of 64 */
+  int32_t logits;             /* C*S, 1 .. WMX_KV_ROUTER_MAX_LOGITS */
+} wmx_kv_router_args;
+
+/*
  * Packed-document schedule builder on the device: the reference's
  * prepare_strict_causal_metadata (ops/strict_causal_attention.py:75-155),
  * whose torch sequence synchronises with the host at every data-dependent
@@ -426,6 +450,7 @@ size_t wmx_decode_args_size(void);
 size_t wmx_kv_store_args_size(void);
 size_t wmx_kv_mix_args_size(void);
 size_t wmx_kv_store_bwd_args_size(void);
+size_t wmx_kv_router_args_size(void);
 size_t wmx_strict_meta_args_size(void);
 size_t wmx_feedback_meta_args_size(void);
 const char* wmx_last_error(void);
@@ -516,6 +541,13 @@ int wmx_kv_store_bwd(const wmx_kv_store_bwd_args* args, void* stream);
  * `_projection_input`, :129-136). Outputs are fully overwritten. */
 int wmx_kv_premix(const wmx_kv_mix_args* args, void* stream);
 int wmx_kv_mix(const wmx_kv_mix_args* args, void* stream);
+
+/* Router logits of both sides (see wmx_kv_router_args): replace the two
+ * nn.Linear calls of the reference's routers (modules/routing.py:108-115).
+ * The workspace holds 2 x ceil(inputs / 1024) x rows x logits fp32 partial
+ * sums. */
+int64_t wmx_kv_router_workspace_size(const wmx_kv_router_args* args);
+int wmx_kv_router(const wmx_kv_router_args* args, void* stream);
 
 /* Packed-document schedule (see wmx_strict_meta_args): replaces the torch
  * sequence of prepare_strict_causal_metadata (reference

@@ -32,6 +32,7 @@ def test_library_loads_and_exports_every_declared_symbol():
     assert lib.wmx_decode_args_size() == ctypes.sizeof(_native.DecodeArgs)
     assert lib.wmx_kv_mix_args_size() == ctypes.sizeof(_native.KvMixArgs)
     assert lib.wmx_kv_store_bwd_args_size() == ctypes.sizeof(_native.KvStoreBwdArgs)
+    assert lib.wmx_kv_router_args_size() == ctypes.sizeof(_native.KvRouterArgs)
 
 
 def test_argument_checks_return_errors_without_launching():
@@ -97,6 +98,23 @@ def test_argument_checks_return_errors_without_launching():
     mix.sources, mix.source_stride = 0x1000, (25 * 1024, 1024, 1028)
     assert lib.wmx_kv_premix(ctypes.byref(mix), None) == -1
     assert b"strides" in lib.wmx_last_error()
+    router = _native.KvRouterArgs()
+    router.rows, router.inputs, router.logits = 2048, 25 * 1024 + 8, 200
+    assert lib.wmx_kv_router(ctypes.byref(router), None) == -2
+    assert b"multiple of 64" in lib.wmx_last_error()
+    router.inputs, router.logits = 25 * 1024, _native.KV_ROUTER_MAX_LOGITS + 1
+    assert lib.wmx_kv_router(ctypes.byref(router), None) == -2
+    assert b"logits" in lib.wmx_last_error()
+    router.logits = 200
+    assert lib.wmx_kv_router(ctypes.byref(router), None) == -1
+    assert b"NULL" in lib.wmx_last_error()
+    for side in range(2):
+        router.premixed[side] = router.weight[side] = router.alpha[side] = 0x1000
+    # 2 sides x 25 chunks of 1024 inputs x 2048 rows x 200 logits, fp32
+    assert lib.wmx_kv_router_workspace_size(ctypes.byref(router)) == 2 * 25 * 2048 * 200 * 4
+    router.workspace, router.workspace_bytes = 0x1000, 2 * 25 * 2048 * 200 * 4 - 1
+    assert lib.wmx_kv_router(ctypes.byref(router), None) == -3
+    assert b"workspace" in lib.wmx_last_error()
 
 
 def test_workspace_sizes():

@@ -6,7 +6,7 @@ summed in another order, so a rare rounding step lands one ulp apart (and
 RoPE's sum can cancel, which magnifies that ulp relative to the result);
 values: exact.
 
-The producer kernels (wmx_kv_premix, wmx_kv_mix around the router GEMM)
+The producer kernels (wmx_kv_premix, the router GEMM wmx_kv_router, wmx_kv_mix)
 against the float64 oracle of kv_pool.py:103-136 / routing.py:108-124 and
 against the torch formulation of the harness on the GPU: the bf16 bar and
 >= 97% of the outputs bit-exact (a premixed row or a mixture summed in
@@ -186,6 +186,25 @@ def test_producer_matches_torch_formulation_at_c5_width():
     k_eager, v_eager = model.project(stacked)
     assert_bf16_close(k_fused.double().cpu(), k_eager.double().cpu(), what="projected keys")
     assert_bf16_close(v_fused.double().cpu(), v_eager.double().cpu(), what="projected values")
+
+
+@pytest.mark.parametrize(("rows", "inputs", "logits"), [(300, 25 * 1024, 200), (130, 1088, 37), (5, 64, 256)])
+def test_router_logits_match_fp32_product(rows, inputs, logits):
+    """wmx_kv_router: bf16(p . W^T + b) over 1024-input chunks summed in order,
+    against the fp32 product of the same bf16 operands (rows not a multiple
+    of 128, a partial last chunk, the widest logit count): within one bf16
+    rounding step of the fp32 result, and the same bits on a second run."""
+    gen = torch.Generator().manual_seed(rows)
+    p = torch.randn(2, rows, inputs, generator=gen).bfloat16().to(DEV)
+    w = [(torch.randn(logits, inputs, generator=gen) * inputs**-0.5).bfloat16().to(DEV) for _ in range(2)]
+    b = [torch.randn(logits, generator=gen).bfloat16().to(DEV) for _ in range(2)]
+    alpha = torch.ops.white_matter.kv_router(p, w[0], b[0], w[1], b[1])
+    assert alpha.shape == (2, rows, logits) and alpha.dtype == torch.bfloat16
+    for side in range(2):
+        exact = p[side].double() @ w[side].double().t() + b[side].double()
+        err = (alpha[side].double() - exact).abs()
+        assert bool((err <= exact.abs() * 2.0**-8 + 1e-3).all()), f"side {side}: max error {err.max().item():.3e}"
+    assert torch.equal(torch.ops.white_matter.kv_router(p, w[0], b[0], w[1], b[1]), alpha)
 
 
 def test_producer_rejects_autograd_and_bad_shapes():

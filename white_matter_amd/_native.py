@@ -19,7 +19,7 @@ import torch
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
 # the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
 OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -150,6 +150,22 @@ class KvMixArgs(ctypes.Structure):
     ]
 
 
+class KvRouterArgs(ctypes.Structure):
+    """Mirror of wmx_kv_router_args (index 0 of each pair: the K side, 1: V)."""
+
+    _fields_ = [
+        ("premixed", _vp2),
+        ("weight", _vp2),
+        ("bias", _vp2),
+        ("alpha", _vp2),
+        ("workspace", _vp),
+        ("workspace_bytes", ctypes.c_int64),
+        ("rows", ctypes.c_int32),
+        ("inputs", ctypes.c_int32),
+        ("logits", ctypes.c_int32),
+    ]
+
+
 class KvStoreBwdArgs(ctypes.Structure):
     """Mirror of wmx_kv_store_bwd_args."""
 
@@ -181,6 +197,7 @@ class KvStoreBwdArgs(ctypes.Structure):
 
 KV_MIX_MAX_SOURCES = 512
 KV_MIX_MAX_HIDDEN = 4096
+KV_ROUTER_MAX_LOGITS = 256  # WMX_KV_ROUTER_MAX_LOGITS
 
 
 class KvStoreArgs(ctypes.Structure):
@@ -288,6 +305,9 @@ EXPORTS = (
     "wmx_kv_store_args_size",
     "wmx_kv_pool_store",
     "wmx_kv_mix_args_size",
+    "wmx_kv_router_args_size",
+    "wmx_kv_router_workspace_size",
+    "wmx_kv_router",
     "wmx_kv_store_bwd_args_size",
     "wmx_kv_store_bwd_workspace_size",
     "wmx_kv_store_bwd",
@@ -345,6 +365,11 @@ def load() -> ctypes.CDLL:
     for name in ("wmx_kv_premix", "wmx_kv_mix"):
         getattr(lib, name).argtypes = [ctypes.POINTER(KvMixArgs), _vp]
         getattr(lib, name).restype = ctypes.c_int
+    lib.wmx_kv_router_args_size.restype = ctypes.c_size_t
+    lib.wmx_kv_router_workspace_size.argtypes = [ctypes.POINTER(KvRouterArgs)]
+    lib.wmx_kv_router_workspace_size.restype = ctypes.c_int64
+    lib.wmx_kv_router.argtypes = [ctypes.POINTER(KvRouterArgs), _vp]
+    lib.wmx_kv_router.restype = ctypes.c_int
     lib.wmx_strict_meta_args_size.restype = ctypes.c_size_t
     lib.wmx_strict_meta_workspace_size.argtypes = [ctypes.POINTER(StrictMetaArgs)]
     lib.wmx_strict_meta_workspace_size.restype = ctypes.c_int64
@@ -370,6 +395,8 @@ def load() -> ctypes.CDLL:
         raise RuntimeError("wmx_kv_store_bwd_args layout differs between the library and the binding")
     if lib.wmx_kv_mix_args_size() != ctypes.sizeof(KvMixArgs):
         raise RuntimeError("wmx_kv_mix_args layout differs between the library and the binding")
+    if lib.wmx_kv_router_args_size() != ctypes.sizeof(KvRouterArgs):
+        raise RuntimeError("wmx_kv_router_args layout differs between the library and the binding")
     if lib.wmx_feedback_meta_args_size() != ctypes.sizeof(FeedbackMetaArgs):
         raise RuntimeError("wmx_feedback_meta_args layout differs between the library and the binding")
     if lib.wmx_strict_meta_args_size() != ctypes.sizeof(StrictMetaArgs):
@@ -481,6 +508,15 @@ def kv_premix(args: KvMixArgs, device: torch.device) -> None:
 def kv_mix(args: KvMixArgs, device: torch.device) -> None:
     lib = load()
     _check(lib, lib.wmx_kv_mix(ctypes.byref(args), _stream(device)), "wmx_kv_mix")
+
+
+def kv_router_workspace_size(args: KvRouterArgs) -> int:
+    return int(load().wmx_kv_router_workspace_size(ctypes.byref(args)))
+
+
+def kv_router(args: KvRouterArgs, device: torch.device) -> None:
+    lib = load()
+    _check(lib, lib.wmx_kv_router(ctypes.byref(args), _stream(device)), "wmx_kv_router")
 
 
 def strict_meta_workspace_size(args: StrictMetaArgs) -> int:

@@ -314,6 +314,37 @@ int wmx_kv_mix(const wmx_kv_mix_args* a, void* stream) {
   return launched(wmx::launch_kv_mix(*a, (hipStream_t)stream));
 }
 
+static int check_kv_router(const wmx_kv_router_args* a) {
+  if (!a) return fail(WMX_E_INVALID, "args is NULL");
+  if (a->rows < 0) return fail(WMX_E_INVALID, "negative shape");
+  if (a->inputs < 64 || a->inputs % 64)
+    return fail(WMX_E_UNSUPPORTED, "kv router inputs %d is not a positive multiple of 64", a->inputs);
+  if (a->logits < 1 || a->logits > WMX_KV_ROUTER_MAX_LOGITS)
+    return fail(WMX_E_UNSUPPORTED, "kv router logits %d is not in [1, %d]", a->logits, WMX_KV_ROUTER_MAX_LOGITS);
+  return WMX_OK;
+}
+
+int64_t wmx_kv_router_workspace_size(const wmx_kv_router_args* a) {
+  return check_kv_router(a) == WMX_OK ? wmx::kv_router_workspace_size(*a) : 0;
+}
+
+int wmx_kv_router(const wmx_kv_router_args* a, void* stream) {
+  int rc = check_kv_router(a);
+  if (rc != WMX_OK || a->rows == 0) return rc;
+  for (int side = 0; side < 2; ++side) {
+    if (!a->premixed[side] || !a->weight[side] || !a->alpha[side]) return fail(WMX_E_INVALID, "kv router pointer is NULL");
+    if (!aligned16(a->premixed[side]) || !aligned16(a->weight[side]) || ((uintptr_t)a->alpha[side] & 1u) ||
+        ((uintptr_t)a->bias[side] & 1u))
+      return fail(WMX_E_INVALID, "kv router operands must be 16-byte aligned (alpha and bias 2-byte)");
+  }
+  const int64_t need = wmx::kv_router_workspace_size(*a);
+  if (!a->workspace || a->workspace_bytes < need || !aligned16(a->workspace))
+    return fail(WMX_E_WORKSPACE, "kv router needs %lld workspace bytes", (long long)need);
+  return launched(wmx::launch_kv_router(*a, (hipStream_t)stream));
+}
+
+size_t wmx_kv_router_args_size(void) { return sizeof(wmx_kv_router_args); }
+
 size_t wmx_kv_store_args_size(void) { return sizeof(wmx_kv_store_args); }
 
 size_t wmx_kv_mix_args_size(void) { return sizeof(wmx_kv_mix_args); }

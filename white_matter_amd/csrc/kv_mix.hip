@@ -199,6 +199,137 @@ __global__ __launch_bounds__(256) void kv_mix_kernel(const wmx_kv_mix_args a) {
   }
 }
 
+// Router GEMM, one workgroup per (128-row tile, 1024-input chunk, side): four
+// waves of 32 rows each, every logit of the tile in NB blocks of 32 columns.
+// The weight rows of the chunk stream through LDS in stages of 64 inputs
+// (double-buffered, 16-byte chunks swizzled by row so a wave's 32 rows read
+// distinct banks); each lane reads its row's 8 inputs per product straight
+// from HBM, one stage ahead. Partial sums, fp32, go to
+// part[side][chunk][row][logit].
+constexpr int kRouterRows = 128;
+constexpr int kRouterStage = 64;
+
+template <int NB>
+__global__ __launch_bounds__(256, 2) void kv_router_kernel(const wmx_kv_router_args a, int chunks) {
+  __shared__ __attribute__((aligned(16))) u32x4 w_lds[2][NB * 32][kRouterStage / 8];
+  const int side = blockIdx.z, chunk = blockIdx.y;
+  const int m0 = blockIdx.x * kRouterRows;
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6, col = lane & 31, half = lane >> 5;
+  const int k0 = chunk * kRouterChunk, k1 = min(k0 + kRouterChunk, a.inputs);
+  const int stages = (k1 - k0) / kRouterStage;
+  const int row = m0 + wave * 32 + col;
+  const bool row_ok = row < a.rows;
+  const bf16* arow = (const bf16*)a.premixed[side] + (int64_t)(row_ok ? row : 0) * a.inputs + 8 * half;
+  const bf16* wgt = (const bf16*)a.weight[side];
+  const u32x4 z = {0u, 0u, 0u, 0u};
+  // this thread's weight chunks of a stage: chunk c = i * 256 + tid of the
+  // stage's NB * 32 rows x 8 chunks
+  auto load_w = [&](int k, u32x4 (&r)[NB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int c = i * 256 + tid, n = c >> 3;
+      r[i] = n < a.logits ? load16(wgt + (int64_t)n * a.inputs + k + 8 * (c & 7)) : z;
+    }
+  };
+  auto store_w = [&](int buf, const u32x4 (&r)[NB]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < NB; ++i) {
+      const int c = i * 256 + tid, n = c >> 3;
+      w_lds[buf][n][(c & 7) ^ (n & 7)] = r[i];
+    }
+  };
+  auto load_a = [&](int k, bf16x8 (&r)[kRouterStage / 16]) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < kRouterStage / 16; ++s) r[s] = as_bf16x8(row_ok ? load16(arow + k + 16 * s) : z);
+  };
+
+  f32x16 acc[NB];
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) acc[nb] = f32x16{};
+  u32x4 wr[NB];
+  bf16x8 aop[kRouterStage / 16], anext[kRouterStage / 16];
+  load_w(k0, wr);
+  load_a(k0, aop);
+  store_w(0, wr);
+  __syncthreads();
+  for (int t = 0; t < stages; ++t) {
+    const int buf = t & 1;
+    const bool more = t + 1 < stages;
+    if (more) {
+      load_w(k0 + (t + 1) * kRouterStage, wr);
+      load_a(k0 + (t + 1) * kRouterStage, anext);
+    }
+#pragma unroll
+    for (int s = 0; s < kRouterStage / 16; ++s) {
+#pragma unroll
+      for (int nb = 0; nb < NB; ++nb) {
+        const int n = nb * 32 + col;
+        const bf16x8 wop = as_bf16x8(w_lds[buf][n][(2 * s + half) ^ (n & 7)]);
+        acc[nb] = mfma32(aop[s], wop, acc[nb]);
+      }
+    }
+    if (more) {
+      store_w(buf ^ 1, wr);
+#pragma unroll
+      for (int s = 0; s < kRouterStage / 16; ++s) aop[s] = anext[s];
+    }
+    __syncthreads();
+  }
+  // element r of block nb: row m0 + 32 wave + 8 (r / 4) + 4 half + r % 4,
+  // logit 32 nb + col
+  float* part = (float*)a.workspace + ((int64_t)side * chunks + chunk) * a.rows * (int64_t)a.logits;
+#pragma unroll
+  for (int nb = 0; nb < NB; ++nb) {
+    const int n = nb * 32 + col;
+    if (n >= a.logits) continue;
+#pragma unroll
+    for (int r = 0; r < 16; ++r) {
+      const int m = m0 + wave * 32 + 8 * (r >> 2) + 4 * half + (r & 3);
+      if (m < a.rows) part[(int64_t)m * a.logits + n] = acc[nb][r];
+    }
+  }
+}
+
+// alpha[side][m, n] = bf16(sum over chunks ascending of part + bias[n])
+__global__ __launch_bounds__(256) void kv_router_reduce_kernel(const wmx_kv_router_args a, int chunks) {
+  const int64_t per = (int64_t)a.rows * a.logits;
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  const int side = blockIdx.y;
+  if (i >= per) return;
+  const float* part = (const float*)a.workspace + (int64_t)side * chunks * per + i;
+  float sum = 0.f;
+  // loads issued eight at a time, added in chunk order
+#pragma unroll 8
+  for (int c = 0; c < chunks; ++c) sum += part[(int64_t)c * per];
+  const int n = (int)(i % a.logits);
+  if (a.bias[side]) sum += (float)((const bf16*)a.bias[side])[n];
+  ((bf16*)a.alpha[side])[i] = (bf16)sum;
+}
+
+int launch_kv_router(const wmx_kv_router_args& a, hipStream_t stream) {
+  if (a.rows == 0) return WMX_OK;
+  const int64_t chunks = kv_router_chunks(a);
+  const int64_t tiles = (a.rows + kRouterRows - 1) / kRouterRows;
+  const int64_t per = (int64_t)a.rows * a.logits;
+  if (tiles > UINT32_MAX || chunks > 65535 || (per + 255) / 256 > UINT32_MAX) return WMX_E_UNSUPPORTED;
+  const dim3 grid((unsigned)tiles, (unsigned)chunks, 2);
+  const int nb = (a.logits + 31) / 32;
+  switch (nb) {
+    case 1: hipLaunchKernelGGL((kv_router_kernel<1>), grid, dim3(256), 0, stream, a, (int)chunks); break;
+    case 2: hipLaunchKernelGGL((kv_router_kernel<2>), grid, dim3(256), 0, stream, a, (int)chunks); break;
+    case 3: hipLaunchKernelGGL((kv_router_kernel<3>), grid, dim3(256), 0, stream, a, (int)chunks); break;
+    case 4: hipLaunchKernelGGL((kv_router_kernel<4>), grid, dim3(256), 0, stream, a, (int)chunks); break;
+    case 5: hipLaunchKernelGGL((kv_router_kernel<5>), grid, dim3(256), 0, stream, a, (int)chunks); break;
+    case 6: hipLaunchKernelGGL((kv_router_kernel<6>), grid, dim3(256), 0, stream, a, (int)chunks); break;
+    case 7: hipLaunchKernelGGL((kv_router_kernel<7>), grid, dim3(256), 0, stream, a, (int)chunks); break;
+    case 8: hipLaunchKernelGGL((kv_router_kernel<8>), grid, dim3(256), 0, stream, a, (int)chunks); break;
+    default: return WMX_E_UNSUPPORTED;
+  }
+  hipLaunchKernelGGL(kv_router_reduce_kernel, dim3((unsigned)((per + 255) / 256), 2), dim3(256), 0, stream, a,
+                     (int)chunks);
+  return WMX_OK;
+}
+
 template <int CH>
 static void launch_premix_ch(const wmx_kv_mix_args& a, int64_t rows, hipStream_t stream) {
   const dim3 grid((unsigned)((rows + 3) / 4));

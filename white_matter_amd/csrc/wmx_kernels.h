@@ -61,6 +61,12 @@ int launch_kv_store_bwd(const wmx_kv_store_bwd_args& a, hipStream_t stream);
 int64_t kv_store_bwd_workspace_size(const wmx_kv_store_bwd_args& a);
 int launch_kv_premix(const wmx_kv_mix_args& a, hipStream_t stream);
 int launch_kv_mix(const wmx_kv_mix_args& a, hipStream_t stream);
+constexpr int kRouterChunk = 1024;  // inputs per partial sum of the router GEMM
+inline int64_t kv_router_chunks(const wmx_kv_router_args& a) { return (a.inputs + kRouterChunk - 1) / kRouterChunk; }
+inline int64_t kv_router_workspace_size(const wmx_kv_router_args& a) {
+  return 2 * kv_router_chunks(a) * (int64_t)a.rows * a.logits * (int64_t)sizeof(float);
+}
+int launch_kv_router(const wmx_kv_router_args& a, hipStream_t stream);
 int64_t strict_meta_workspace_size(const wmx_strict_meta_args& a);
 int launch_strict_meta(const wmx_strict_meta_args& a, bool fill, hipStream_t stream);
 int64_t feedback_meta_workspace_size(const wmx_feedback_meta_args& a);

@@ -8,8 +8,10 @@ inference form; modules/routing.py:77-124 `Router`, `_RoutedMixer`): an RMS
 norm of every source row, the K- and V-side pre-mix products cast to bf16,
 a router linear over the premixed row, the routed sum over the sources, the
 mix norm and the channel gain cast to bf16 and permuted to (channel, token,
-hidden). `projection_inputs` runs that as two HIP kernels (wmx_kv_premix,
-wmx_kv_mix) around the router GEMM, which stays a library GEMM (F.linear).
+hidden). `projection_inputs` runs that as three HIP steps: wmx_kv_premix, the
+router logits (wmx_kv_router: a split-K MFMA GEMM, since the library GEMM of
+this shape, few logits over long rows, runs on a few workgroups) and
+wmx_kv_mix.
 
 The reference produces a group's keys with an eager sequence
 (src/white_matter/modules/kv_pool.py:163-172 `_apply_k_norm_rope`, the
@@ -253,6 +255,38 @@ def _(premixed, alpha_k, alpha_v, gain_k, gain_v, mix_eps):
     return premixed.new_empty((2, channels, premixed.shape[1], hidden), dtype=torch.bfloat16)
 
 
+@torch.library.custom_op("white_matter::kv_router", mutates_args=())
+def kv_router(
+    premixed: torch.Tensor, weight_k: torch.Tensor, bias_k: torch.Tensor, weight_v: torch.Tensor, bias_v: torch.Tensor
+) -> torch.Tensor:
+    """Both sides' router logits (2, B*T, C*S) bf16 = bf16(premixed[side] .
+    W_side^T + b_side) (wmx_kv_router) from both premixed stacks (2, B*T,
+    S*hidden) and bf16 weights (C*S, S*hidden) and biases (C*S,)."""
+    _, rows, inputs = premixed.shape
+    logits = weight_k.shape[0]
+    premixed = premixed.contiguous()
+    weights = [w.to(torch.bfloat16).contiguous() for w in (weight_k, weight_v)]
+    biases = [b.to(torch.bfloat16).contiguous() for b in (bias_k, bias_v)]
+    alpha = torch.empty(2, rows, logits, device=premixed.device, dtype=torch.bfloat16)
+    a = _native.KvRouterArgs()
+    a.rows, a.inputs, a.logits = rows, inputs, logits
+    for side in range(2):
+        a.premixed[side] = premixed[side].data_ptr()
+        a.weight[side] = weights[side].data_ptr()
+        a.bias[side] = biases[side].data_ptr()
+        a.alpha[side] = alpha[side].data_ptr()
+    need = _native.kv_router_workspace_size(a)
+    workspace = torch.empty(max(need, 16), device=premixed.device, dtype=torch.uint8)
+    a.workspace, a.workspace_bytes = workspace.data_ptr(), need
+    _native.kv_router(a, premixed.device)
+    return alpha
+
+
+@kv_router.register_fake
+def _(premixed, weight_k, bias_k, weight_v, bias_v):
+    return premixed.new_empty((2, premixed.shape[1], weight_k.shape[0]), dtype=torch.bfloat16)
+
+
 def projection_inputs(
     stacked: torch.Tensor,
     pre_mix: tuple[torch.Tensor, torch.Tensor],
@@ -271,12 +305,15 @@ def projection_inputs(
     b_V)) with W (C*S, S*hidden) and b (C*S,), the logits of channel c and
     source s at c*S + s; gain (K, V) (C, hidden). Per side:
       p = bf16(rms_norm(x, eps) * pre_mix)           (HIP, wmx_kv_premix)
-      alpha = F.linear(p, W, b) in bf16                (library GEMM)
+      alpha = bf16(p . W^T + b)                       (HIP, wmx_kv_router)
       m = bf16(sum_s alpha[c, s] * p[s])               (HIP, wmx_kv_mix)
       h = bf16(rms_norm(m, mix_eps) * gain[c])
     Forward only (the reference's training form runs under checkpointing).
-    The two HIP steps are the operators white_matter::kv_premix and
-    white_matter::kv_mix, so the whole function traces under torch.compile.
+    The three HIP steps are the operators white_matter::kv_premix,
+    white_matter::kv_router and white_matter::kv_mix, so the whole function
+    traces under torch.compile. Router widths C*S beyond
+    _native.KV_ROUTER_MAX_LOGITS, or S*hidden not a multiple of 64, take the
+    library GEMM (F.linear) for the logits.
     """
     if torch.is_grad_enabled() and any(
         t.requires_grad for t in (stacked, *pre_mix, *gain, *router[0], *router[1])
@@ -305,9 +342,13 @@ def projection_inputs(
         if weight.shape != (channels * sources, sources * hidden) or bias.shape != (channels * sources,):
             raise ValueError("router weights must be (C*S, S*hidden) with a (C*S,) bias")
     premixed = torch.ops.white_matter.kv_premix(stacked, pre_mix[0], pre_mix[1], float(eps))
-    alphas = [
-        F.linear(premixed[side], weight.to(torch.bfloat16), bias.to(torch.bfloat16))
-        for side, (weight, bias) in enumerate(router)
-    ]
+    if channels * sources <= _native.KV_ROUTER_MAX_LOGITS and (sources * hidden) % 64 == 0:
+        (w_k, b_k), (w_v, b_v) = router
+        alphas = torch.ops.white_matter.kv_router(premixed, w_k, b_k, w_v, b_v).unbind(0)
+    else:
+        alphas = [
+            F.linear(premixed[side], weight.to(torch.bfloat16), bias.to(torch.bfloat16))
+            for side, (weight, bias) in enumerate(router)
+        ]
     mixed = torch.ops.white_matter.kv_mix(premixed, alphas[0], alphas[1], gain[0], gain[1], float(mix_eps))
     return mixed[0], mixed[1]

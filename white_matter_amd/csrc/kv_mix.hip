@@ -98,16 +98,17 @@ __global__ __launch_bounds__(256) void kv_premix_kernel(const wmx_kv_mix_args a,
   }
 }
 
-// Workgroup (token n, side, channel group); thread i holds elements
-// 1024 c + 4 i + [0, 4) for c < CH (hidden <= 1024 CH). For each channel j of
-// the group: m = bf16(sum over s ascending of alpha[n, j, s] * p[n, s, :])
-// (fp32 products and sums), then out = bf16((m * (1 / sqrt(mean(m^2) +
-// mix_eps))) * gain[j]).
-template <int CH, bool W_BF16>
-__global__ __launch_bounds__(256) void kv_mix_kernel(const wmx_kv_mix_args a) {
+// Workgroup (token n, side, channel group) of NT threads; thread i holds
+// elements 8 NT c + 8 i + [0, 8) for c < CH (hidden <= 8 NT CH), read and
+// written as 16-byte vectors. For each channel j of the group:
+// m = bf16(sum over s ascending of alpha[n, j, s] * p[n, s, :]) (fp32 products
+// and sums), then out = bf16((m * (1 / sqrt(mean(m^2) + mix_eps))) * gain[j]).
+template <int CH, bool W_BF16, int NT>
+__global__ __launch_bounds__(NT) void kv_mix_kernel(const wmx_kv_mix_args a) {
 #pragma clang fp contract(off)
+  constexpr int NWV = NT / 64, CW = 8 * NT;
   __shared__ float alpha_lds[kMixChannels * WMX_KV_MIX_MAX_SOURCES];
-  __shared__ float red[4][kMixChannels];
+  __shared__ float red[NWV][kMixChannels];
   const int64_t n = blockIdx.x;
   const int side = blockIdx.y;
   const int c0 = blockIdx.z * kMixChannels;
@@ -116,29 +117,29 @@ __global__ __launch_bounds__(256) void kv_mix_kernel(const wmx_kv_mix_args a) {
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   // this group's logits: channels c0 .. c0 + nc - 1 are contiguous rows of S
   const bf16* alpha = (const bf16*)a.alpha[side] + n * a.alpha_stride + (int64_t)c0 * S;
-  for (int i = tid; i < nc * S; i += 256) alpha_lds[i] = (float)alpha[i];
+  for (int i = tid; i < nc * S; i += NT) alpha_lds[i] = (float)alpha[i];
   __syncthreads();
 
-  float acc[kMixChannels][CH][4];
+  float acc[kMixChannels][CH][8];
 #pragma unroll
   for (int j = 0; j < kMixChannels; ++j)
 #pragma unroll
     for (int c = 0; c < CH; ++c)
 #pragma unroll
-      for (int e = 0; e < 4; ++e) acc[j][c][e] = 0.f;
+      for (int e = 0; e < 8; ++e) acc[j][c][e] = 0.f;
   const bf16* p = (const bf16*)a.premixed[side] + n * S * H;
   for (int s0 = 0; s0 < S; s0 += kMixBatch) {
-    float pv[kMixBatch][CH][4];
+    float pv[kMixBatch][CH][8];
 #pragma unroll
     for (int u = 0; u < kMixBatch; ++u) {
 #pragma unroll
       for (int c = 0; c < CH; ++c) {
-        const int d0 = 1024 * c + 4 * tid;
+        const int d0 = CW * c + 8 * tid;
         if (s0 + u < S && d0 < H) {
-          load4(p, (int64_t)(s0 + u) * H + d0, true, pv[u][c]);
+          load8(p, (int64_t)(s0 + u) * H + d0, true, pv[u][c]);
         } else {
 #pragma unroll
-          for (int e = 0; e < 4; ++e) pv[u][c][e] = 0.f;
+          for (int e = 0; e < 8; ++e) pv[u][c][e] = 0.f;
         }
       }
     }
@@ -152,7 +153,7 @@ __global__ __launch_bounds__(256) void kv_mix_kernel(const wmx_kv_mix_args a) {
 #pragma unroll
             for (int c = 0; c < CH; ++c)
 #pragma unroll
-              for (int e = 0; e < 4; ++e) acc[j][c][e] = fmaf(al, pv[u][c][e], acc[j][c][e]);
+              for (int e = 0; e < 8; ++e) acc[j][c][e] = fmaf(al, pv[u][c][e], acc[j][c][e]);
           }
         }
       }
@@ -165,9 +166,9 @@ __global__ __launch_bounds__(256) void kv_mix_kernel(const wmx_kv_mix_args a) {
     ss[j] = 0.f;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const bool in = 1024 * c + 4 * tid < H;
+      const bool in = CW * c + 8 * tid < H;
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
+      for (int e = 0; e < 8; ++e) {
         const float m = in ? round_bf16(acc[j][c][e]) : 0.f;
         acc[j][c][e] = m;
         ss[j] = fmaf(m, m, ss[j]);
@@ -182,18 +183,20 @@ __global__ __launch_bounds__(256) void kv_mix_kernel(const wmx_kv_mix_args a) {
 #pragma unroll
   for (int j = 0; j < kMixChannels; ++j) {
     if (j >= nc) break;
-    const float total = red[0][j] + red[1][j] + red[2][j] + red[3][j];
+    float total = 0.f;
+#pragma unroll
+    for (int v = 0; v < NWV; ++v) total += red[v][j];
     const float inv = 1.f / sqrtf(total / (float)H + a.mix_eps);
     const int64_t row = ((int64_t)(c0 + j) * tokens_total + n) * H;
 #pragma unroll
     for (int c = 0; c < CH; ++c) {
-      const int d0 = 1024 * c + 4 * tid;
+      const int d0 = CW * c + 8 * tid;
       if (d0 < H) {
-        float g[4];
-        load4(a.gain[side], (int64_t)(c0 + j) * H + d0, W_BF16, g);
-        const u32x2 o = {pack_bf16x2((acc[j][c][0] * inv) * g[0], (acc[j][c][1] * inv) * g[1]),
-                         pack_bf16x2((acc[j][c][2] * inv) * g[2], (acc[j][c][3] * inv) * g[3])};
-        *reinterpret_cast<u32x2*>((bf16*)a.mixed[side] + row + d0) = o;
+        float g[8], o[8];
+        load8(a.gain[side], (int64_t)(c0 + j) * H + d0, W_BF16, g);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) o[e] = (acc[j][c][e] * inv) * g[e];
+        store8_bf16(a.mixed[side], row + d0, o);
       }
     }
   }
@@ -351,10 +354,10 @@ int launch_kv_premix(const wmx_kv_mix_args& a, hipStream_t stream) {
   return WMX_OK;
 }
 
-template <int CH>
+template <int CH, int NT>
 static void launch_mix_ch(const wmx_kv_mix_args& a, dim3 grid, hipStream_t stream) {
-  if (a.weight_dtype == WMX_DTYPE_BF16) hipLaunchKernelGGL((kv_mix_kernel<CH, true>), grid, dim3(256), 0, stream, a);
-  else hipLaunchKernelGGL((kv_mix_kernel<CH, false>), grid, dim3(256), 0, stream, a);
+  if (a.weight_dtype == WMX_DTYPE_BF16) hipLaunchKernelGGL((kv_mix_kernel<CH, true, NT>), grid, dim3(NT), 0, stream, a);
+  else hipLaunchKernelGGL((kv_mix_kernel<CH, false, NT>), grid, dim3(NT), 0, stream, a);
 }
 
 int launch_kv_mix(const wmx_kv_mix_args& a, hipStream_t stream) {
@@ -362,9 +365,9 @@ int launch_kv_mix(const wmx_kv_mix_args& a, hipStream_t stream) {
   if (tokens == 0) return WMX_OK;
   if (tokens > UINT32_MAX) return WMX_E_UNSUPPORTED;
   const dim3 grid((unsigned)tokens, 2, (unsigned)((a.channels + kMixChannels - 1) / kMixChannels));
-  if (a.hidden <= 1024) launch_mix_ch<1>(a, grid, stream);
-  else if (a.hidden <= 2048) launch_mix_ch<2>(a, grid, stream);
-  else launch_mix_ch<4>(a, grid, stream);
+  if (a.hidden <= 1024) launch_mix_ch<1, 128>(a, grid, stream);
+  else if (a.hidden <= 2048) launch_mix_ch<1, 256>(a, grid, stream);
+  else launch_mix_ch<2, 256>(a, grid, stream);
   return WMX_OK;
 }
 

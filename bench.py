@@ -1,6 +1,6 @@
 """Benchmark of WhiteMatter's attention hot path on one MI355X.
 
-Headline ("C2"): bf16 strict_causal_attention in
+Headline (the "C2" configuration the baseline metric is quoted on): bf16 strict_causal_attention in
 Jacobi mode, Q/K/V (8, 16, 2048, 128) ~ N(0,1)/sqrt(D), use_dummy_token=False,
 packed documents per row with geometric lengths (mean 512, clipped to
 [16, 2048], filled to exactly T), metadata from prepare_strict_causal_metadata,

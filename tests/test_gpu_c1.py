@@ -1,4 +1,4 @@
-"""BASELINE configs[0] (C1) in the GPU session: fp32 cyclic_attention on the
+"""The C1 case (the reference's CPU-runnable configuration) in the GPU session: fp32 cyclic_attention on the
 portable backend, (1, 4, 64, 64) queries over 2 KV heads of 256 keys at
 query_stride 4, one document; output and gradients of sum(output) within
 1e-5 relative L2 of the float64 oracle, on the GPU box's host cores and on

@@ -192,7 +192,7 @@ def test_portable_cyclic_matches_oracle(document_masked, offset):
 
 
 def test_config_c1_cpu_fp32_cyclic():
-    """fp32 (1,4,64,64) queries over 2 KV heads of 256 keys,
+    """The C1 case: fp32 (1,4,64,64) queries over 2 KV heads of 256 keys,
     stride 4, one document; output and gradients of sum(output) within 1e-5
     relative of the float64 oracle."""
     gen = torch.Generator().manual_seed(0)

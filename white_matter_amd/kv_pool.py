@@ -255,6 +255,22 @@ def _(premixed, alpha_k, alpha_v, gain_k, gain_v, mix_eps):
     return premixed.new_empty((2, channels, premixed.shape[1], hidden), dtype=torch.bfloat16)
 
 
+_ROUTER_WORKSPACE: dict[tuple[int, int], torch.Tensor] = {}
+
+
+def _router_workspace(device: torch.device, need: int) -> torch.Tensor:
+    """The router's fp32 partial sums (tens of MB at the model's width), kept
+    per device and stream and grown when a call needs more, so that repeated
+    calls do not churn the caching allocator with large blocks. Calls on one
+    stream run in order, so they may share it."""
+    key = (device.index if device.index is not None else torch.cuda.current_device(), torch.cuda.current_stream(device).cuda_stream)
+    buf = _ROUTER_WORKSPACE.get(key)
+    if buf is None or buf.numel() < need:
+        buf = torch.empty(max(need, 16), device=device, dtype=torch.uint8)
+        _ROUTER_WORKSPACE[key] = buf
+    return buf
+
+
 @torch.library.custom_op("white_matter::kv_router", mutates_args=())
 def kv_router(
     premixed: torch.Tensor, weight_k: torch.Tensor, bias_k: torch.Tensor, weight_v: torch.Tensor, bias_v: torch.Tensor
@@ -276,7 +292,7 @@ def kv_router(
         a.bias[side] = biases[side].data_ptr()
         a.alpha[side] = alpha[side].data_ptr()
     need = _native.kv_router_workspace_size(a)
-    workspace = torch.empty(max(need, 16), device=premixed.device, dtype=torch.uint8)
+    workspace = _router_workspace(premixed.device, need)
     a.workspace, a.workspace_bytes = workspace.data_ptr(), need
     _native.kv_router(a, premixed.device)
     return alpha

@@ -49,7 +49,7 @@ __device__ __forceinline__ void store8_bf16_cached(void* base, int64_t off, cons
 }
 
 constexpr int kMixChannels = 8;  // channels per mix workgroup
-constexpr int kMixBatch = 8;     // source rows whose loads are in flight together
+constexpr int kMixBatch = 2;     // source rows whose loads are in flight together (few registers: more resident waves)
 
 }  // namespace
 

@@ -22,7 +22,6 @@
 
 namespace wmx {
 
-constexpr int kDecodeUnroll = 8;
 constexpr int kDecodeChunkMin = 256;
 
 struct DecodeLen {
@@ -54,6 +53,9 @@ template <int D, int G>
 __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args a, int chunk, int head_offset) {
   constexpr int LPR = D <= 64 ? 8 : 16;   // lanes per key row
   constexpr int RPW = 64 / LPR;           // rows per wave load
+  // key rows in flight per lane: eight for one head; four for a head group,
+  // whose accumulators take the registers (fewer rows, more resident waves)
+  constexpr int kDecodeUnroll = G == 1 ? 8 : 4;
   constexpr int ROWS_ITER = 4 * RPW * kDecodeUnroll;
   __shared__ float lds_m[4][G], lds_l[4][G];
   __shared__ __attribute__((aligned(16))) float lds_o[4][G][D];

@@ -191,3 +191,46 @@ def test_fullgraph_kv_producer():
     for c, e in zip(compiled, eager, strict=True):
         assert c.shape == (channels, batch * tokens, hidden)
         torch.testing.assert_close(c, e, atol=0, rtol=0)
+
+
+@pytest.mark.parametrize("batch", [1, 3])
+@pytest.mark.parametrize("strided", [False, True])
+@pytest.mark.parametrize("static_cache", [False, True])
+@pytest.mark.parametrize("dim", [8, 63])
+@torch.inference_mode()
+def test_torch_flash_decode_cache_reuses_graphs(batch, strided, static_cache, dim):
+    """reference tests/unit/test_compilation_policy.py:35-89: torch_flash_decode
+    compiled with fullgraph=True and dynamic=True over caches of growing
+    capacity (5..16 slots, or a fixed 20 with static_cache) compiles at most two
+    graphs, the outputs match math SDPA under the lengths mask, and the graphs
+    build no offsets on the device (no arange node: the decode kernel reads the
+    cache through its strides)."""
+    from white_matter_amd.flash_attention import torch_flash_decode
+
+    torch.compiler.reset()
+    graphs = []
+
+    def backend(graph, inputs):
+        graphs.append(graph)
+        return graph.forward
+
+    compiled = torch.compile(torch_flash_decode, backend=backend, dynamic=True, fullgraph=True)
+    torch.manual_seed(5 + batch + dim)
+    q = torch.randn(batch, 4, 1, dim, device=DEV, dtype=torch.bfloat16)
+    for length in range(5, 17):
+        capacity = 20 if static_cache else length
+        k, v = (torch.randn(batch, 4 if strided else 2, capacity, dim, device=DEV, dtype=q.dtype) for _ in range(2))
+        if strided:  # a pool view: the batch stride spans heads this call does not read
+            k, v = k[:, :2], v[:, :2]
+        lengths = length - torch.arange(batch, device=DEV, dtype=torch.int32)
+        keep = torch.arange(capacity, device=DEV)[None, :] < lengths[:, None]
+        expected = torch.nn.functional.scaled_dot_product_attention(
+            q.float(), k.float(), v.float(), attn_mask=keep[:, None, None, :], scale=0.5, enable_gqa=True
+        ).transpose(1, 2)
+        actual = compiled(q, k, v, lengths, 0.5, static_cache=static_cache)
+        assert actual.shape == (batch, 1, 4, dim) and actual.dtype == q.dtype
+        torch.testing.assert_close(actual.float(), expected, atol=0.03, rtol=0.03)
+    assert 1 <= len(graphs) <= 2
+    for graph in graphs:
+        assert sum(node.target is torch.arange for node in graph.graph.nodes) == 0
+    torch.compiler.reset()

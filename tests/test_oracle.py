@@ -98,6 +98,18 @@ def test_strict_metadata_hand_worked_example():
     assert dummy["cu_keys"].tolist() == [0, 3, 5]
 
 
+def _query_run_and_end(docs, b, pos, kv_lengths):
+    """For the query at slot `pos` of row b: its run (the slot where walking back
+    over padding and its own id stops: one value per run, padding inside a run
+    not breaking it) and its visible end (present slots before min(pos, kv_len)),
+    the two quantities that decide segment membership."""
+    first = pos
+    while first and (docs[b, first - 1] < 0 or docs[b, first - 1] == docs[b, pos]):
+        first -= 1
+    cap = pos if kv_lengths is None else min(pos, int(kv_lengths[b]))
+    return (b, first), int((docs[b, :cap] >= 0).sum())
+
+
 def _schedule_invariants(out, docs, query_length, starts, kv_lengths, dummy):
     qi, ki = out["query_indices"], out["key_indices"]
     cq, ck = out["cu_queries"], out["cu_keys"]
@@ -105,6 +117,19 @@ def _schedule_invariants(out, docs, query_length, starts, kv_lengths, dummy):
     assert cq[0] == 0 and ck[0] == 0 and cq[-1] == qi.size and ck[-1] == ki.size
     assert (np.diff(cq) > 0).all() and (np.diff(ck) >= 0).all()
     assert (np.diff(qi) > 0).all()
+    facts = []
+    for i in qi:
+        b, t = divmod(int(i), query_length)
+        facts.append(_query_run_and_end(docs, b, int(starts[b]) + t, kv_lengths))
+    for s in range(len(cq) - 1):
+        # inside a segment consecutive queries share a run and see one more key each
+        for a in range(int(cq[s]), int(cq[s + 1]) - 1):
+            assert facts[a + 1][0] == facts[a][0], "a segment spans two runs"
+            assert facts[a + 1][1] == facts[a][1] + 1, "visible ends inside a segment are not +1 apart"
+        # segments are maximal: the next segment's first query could not have joined this one
+        if s + 2 < len(cq):
+            last, nxt = facts[int(cq[s + 1]) - 1], facts[int(cq[s + 1])]
+            assert not (nxt[0] == last[0] and nxt[1] == last[1] + 1), "segment is not maximal"
     for s in range(len(cq) - 1):
         rows = {int(i) // query_length for i in qi[cq[s] : cq[s + 1]]}
         assert len(rows) == 1
@@ -136,6 +161,38 @@ def test_strict_metadata_invariants_random(dummy):
         kv = None if trial % 3 else rng.integers(0, extent + 1, size=batch)
         out = meta.strict_metadata(docs, length, starts, kv, dummy)
         _schedule_invariants(out, docs, length, starts, kv, dummy)
+
+
+def test_planted_over_split_fails_invariants():
+    """A schedule with one segment cut in two (each part keyed by its last
+    query's visible set) implies the same attention, so only maximality and
+    the +1 rule catch it; both fail it."""
+    docs = np.array([[0, 0, 0, 0, 0, 0, 1, 1]])
+    starts = np.array([0])
+    good = meta.strict_metadata(docs, 8, starts, None, False)
+    _schedule_invariants(good, docs, 8, starts, None, False)
+    assert good["cu_queries"].tolist() == [0, 5, 6]  # queries 1..5 of document 0, then query 7
+    qi, ki, cq = good["query_indices"], good["key_indices"], good["cu_queries"]
+    # split segment 0 after its second query: part one ends at query 2 (keys 0, 1)
+    bad = dict(good)
+    bad["cu_queries"] = np.array([0, 2, 5, 6], dtype=np.int32)
+    bad["key_indices"] = np.concatenate((ki[:2], ki))
+    bad["cu_keys"] = np.array([0, 2, 2 + good["cu_keys"][1], 2 + good["cu_keys"][2]], dtype=np.int32)
+    q = torch.randn(1, 2, 8, 8, dtype=torch.float64)
+    k = torch.randn(1, 2, 8, 8, dtype=torch.float64)
+    v = torch.randn_like(k)
+    same = ref.strict_attention(q, k, v, metadata=bad)
+    torch.testing.assert_close(same, ref.strict_attention(q, k, v, metadata=good), rtol=1e-12, atol=1e-12)
+    with pytest.raises(AssertionError, match="not maximal"):
+        _schedule_invariants(bad, docs, 8, starts, None, False)
+    # a merge across the document boundary breaks the run rule instead
+    merged = dict(good)
+    merged["cu_queries"] = np.array([0, 6], dtype=np.int32)
+    merged["key_indices"] = ki[good["cu_keys"][1] :]
+    merged["cu_keys"] = np.array([0, merged["key_indices"].size], dtype=np.int32)
+    with pytest.raises(AssertionError, match="two runs"):
+        _schedule_invariants(merged, docs, 8, starts, None, False)
+    assert qi.tolist() == [1, 2, 3, 4, 5, 7]
 
 
 def test_with_key_extent_closed_form():

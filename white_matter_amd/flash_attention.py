@@ -109,8 +109,14 @@ def torch_flash_decode(
     """Single-query attention over (B, Hkv, N, D) caches (channel views of a
     pool with any strides are read in place) with device-resident lengths:
     query (B, H, 1, D) sees slots j < lengths[b]. Returns (B, 1, H, D) in the
-    query dtype (reference flash_attention.py:52-103; ``static_cache`` is
-    accepted for compatibility: no offsets are built here)."""
+    query dtype (reference flash_attention.py:52-103). With ``static_cache``
+    a compiled caller specialises on the batch, KV-head and capacity sizes as
+    the reference's does; no offsets are built either way (the kernel reads
+    the cache through its strides)."""
+    if static_cache and torch.compiler.is_compiling():
+        torch._dynamo.mark_static(query, 0)
+        torch._dynamo.mark_static(key, 1)
+        torch._dynamo.mark_static(key, 2)
     dim = query.shape[-1]
     size = _padded(dim)
     q, k, v = (_kernels.pad_head_dim(t, size) for t in (query, key, value))

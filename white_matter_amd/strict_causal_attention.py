@@ -18,7 +18,6 @@ PyTorch math path.
 
 from __future__ import annotations
 
-import weakref
 from dataclasses import dataclass
 from typing import Literal
 
@@ -321,120 +320,14 @@ def _schedule_facts(metadata: StrictCausalMetadata) -> tuple[int, int, int, int,
     return facts
 
 
-# ------------------------------------------------------------ custom ops ----
-def _dense_visibility(
-    query_offset: int, row_offset: torch.Tensor | None, row_limit: torch.Tensor | None, key_mask, keep_slot0: bool
-) -> _kernels.Visibility:
-    return _kernels.Visibility(
-        query_stride=1,
-        query_offset=query_offset,
-        row_offset=row_offset,
-        row_limit=row_limit,
-        keep_slot0=keep_slot0,
-        key_mask=None if key_mask is None else key_mask.contiguous().view(torch.uint8),
-    )
-
-
-@torch.library.custom_op("white_matter::strict_dense_fwd", mutates_args=())
-def strict_dense_fwd(
-    query: torch.Tensor,
-    key: torch.Tensor,
-    value: torch.Tensor,
-    query_offset: int,
-    row_offset: torch.Tensor | None,
-    row_limit: torch.Tensor | None,
-    key_mask: torch.Tensor | None,
-    keep_slot0: bool,
-    scale: float,
-) -> tuple[torch.Tensor, torch.Tensor]:
-    """Strict-causal attention with per-row bounds; output (B, T, H, D) bf16.
-
-    Key slot j is visible to query i of row b iff j <= min(offset_b + i, limit_b),
-    or j == 0 with keep_slot0, and key_mask[b, j] when given.
-    """
-    q, k, v = (_kernels.operand(t) for t in (query, key, value))
-    batch, heads, length, dim = q.shape
-    out = torch.empty(batch, length, heads, dim, device=q.device, dtype=torch.bfloat16)
-    lse = torch.empty(batch, heads, length, device=q.device, dtype=torch.float32)
-    vis = _dense_visibility(query_offset, row_offset, row_limit, key_mask, keep_slot0)
-    # a chunk of queries after a long cached prefix: 256-row workgroups read
-    # each key/value tile once for twice the rows (the prefix dominates)
-    vis.query_tile = 256 if length > _kernels.QUERY_TILE and k.shape[2] >= 4 * length else 0
-    if row_offset is not None or row_limit is not None:
-        # ragged rows (cached prefixes): heaviest tiles first
-        vis.q_units = _kernels.dense_units(
-            batch, length, k.shape[2], query_offset, row_offset, row_limit, q.device, vis.query_tile or _kernels.QUERY_TILE
-        )
-    _kernels.forward(q, k, v, out.transpose(1, 2), lse, scale, vis)
-    return out, lse
-
-
-@strict_dense_fwd.register_fake
-def _(query, key, value, query_offset, row_offset, row_limit, key_mask, keep_slot0, scale):
-    batch, heads, length, dim = query.shape
-    return (
-        query.new_empty(batch, length, heads, dim, dtype=torch.bfloat16),
-        query.new_empty(batch, heads, length, dtype=torch.float32),
-    )
-
-
-@torch.library.custom_op("white_matter::strict_dense_bwd", mutates_args=())
-def strict_dense_bwd(
-    query: torch.Tensor,
-    key: torch.Tensor,
-    value: torch.Tensor,
-    out: torch.Tensor,
-    lse: torch.Tensor,
-    dout: torch.Tensor,
-    query_offset: int,
-    row_offset: torch.Tensor | None,
-    row_limit: torch.Tensor | None,
-    key_mask: torch.Tensor | None,
-    keep_slot0: bool,
-    scale: float,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    q, k, v = (_kernels.operand(t) for t in (query, key, value))
-    o = _kernels.operand(out.transpose(1, 2))
-    g = _kernels.operand(dout.transpose(1, 2))
-    dq = torch.empty(q.shape, device=q.device, dtype=torch.bfloat16)
-    dk = torch.empty(k.shape, device=q.device, dtype=torch.bfloat16)
-    dv = torch.empty(v.shape, device=q.device, dtype=torch.bfloat16)
-    vis = _dense_visibility(query_offset, row_offset, row_limit, key_mask, keep_slot0)
-    _kernels.backward(q, k, v, o, lse, g, dq, dk, dv, scale, vis)
-    return dq, dk, dv
-
-
-@strict_dense_bwd.register_fake
-def _(query, key, value, out, lse, dout, *args):
-    return (
-        query.new_empty(query.shape, dtype=torch.bfloat16),
-        key.new_empty(key.shape, dtype=torch.bfloat16),
-        value.new_empty(value.shape, dtype=torch.bfloat16),
-    )
-
-
-def _dense_setup(ctx, inputs, output):
-    query, key, value, ctx.query_offset, row_offset, row_limit, key_mask, ctx.keep_slot0, ctx.scale = inputs
-    ctx.has = (row_offset is not None, row_limit is not None, key_mask is not None)
-    extras = [t for t in (row_offset, row_limit, key_mask) if t is not None]
-    ctx.dtypes = (query.dtype, key.dtype, value.dtype)
-    ctx.save_for_backward(query, key, value, *output, *extras)
-    ctx.set_materialize_grads(False)  # the LSE output has no gradient: no zero fill for it
-
-
-def _dense_backward(ctx, dout, dlse):
-    query, key, value, out, lse, *extras = ctx.saved_tensors
-    if dout is None:
-        dout = torch.zeros_like(out)
-    it = iter(extras)
-    row_offset, row_limit, key_mask = (next(it) if flag else None for flag in ctx.has)
-    dq, dk, dv = strict_dense_bwd(
-        query, key, value, out, lse, dout, ctx.query_offset, row_offset, row_limit, key_mask, ctx.keep_slot0, ctx.scale
-    )
-    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2]), None, None, None, None, None, None)
-
-
-strict_dense_fwd.register_autograd(_dense_backward, setup_context=_dense_setup)
+# ------------------------------------------------------------ operators ----
+# strict_packed_fwd/bwd, strict_dense_fwd/bwd and strict_decode are registered
+# from C++ (libwmx_torch.so, csrc/torch_ops.cpp): their host work per call
+# (operand checks, allocation, the argument block, the launches, autograd)
+# runs without the Python interpreter. Their fakes are registered below; the
+# packed operators' planner (_packed_plan) is the Python step they call once
+# per schedule and call shape.
+_native.load_ops()
 
 
 _KEYS_UNIQUE = 16  # schedule_flags bits above the four segment-layout bits
@@ -812,85 +705,58 @@ strict_varlen_fwd.register_autograd(_varlen_backward, setup_context=_varlen_setu
 
 
 # ------------------------------------------------- packed-document plans ----
-class _PackedPlan:
-    """What the kernels need beyond a schedule's own tensors, derived on the
-    host once per schedule and call shape: the covering schedule (None when
-    it is the schedule itself), its flags, the rows no segment writes and the
-    work lists. It keeps only weak references to the schedule's tensors, so a
-    plan lives exactly as long as its schedule."""
-
-    __slots__ = ("others", "cover", "max_q", "max_k", "flags", "gaps", "units")
-
-    def schedule(self, qi, ki, cq, ck):
-        c = self.cover
-        return (qi, ki, cq, ck) if c is None else (c.query_indices, c.key_indices, c.cu_queries, c.cu_keys)
-
-
-# plans by id of the schedule's query_indices tensor: (weak reference to it,
-# plans by call shape); an entry is dropped when that tensor is freed
-_PLANS: dict[int, tuple[weakref.ref, dict]] = {}
-
-
-def _packed_plan(qi, ki, cq, ck, max_queries, max_keys, batch, length, key_slots, heads, kv_heads) -> _PackedPlan:
-    """The plan of a packed-document schedule given as its tensors (as the
-    packed operators receive it, also from a compiled graph), built on a miss
-    and kept until the schedule's tensors are freed or changed in place."""
-    shape = (max_queries, max_keys, batch, length, key_slots, heads, kv_heads)
-    entry = _PLANS.get(id(qi))
-    if entry is None or entry[0]() is not qi:
-        entry = _PLANS[id(qi)] = (weakref.ref(qi), {})
-        weakref.finalize(qi, _PLANS.pop, id(qi), None)
-    by_shape = entry[1]
-    plan = by_shape.get(shape)
-    versions = (qi._version, ki._version, cq._version, ck._version)
-    if plan is not None and plan.others[1] == versions and all(r() is t for r, t in zip(plan.others[0], (ki, cq, ck))):
-        return plan
-    _kernels.guard_capture("planning a packed-document schedule")
-    metadata = StrictCausalMetadata(qi, ki, cq, ck, max_queries, max_keys, key_slots)
-    top_q, top_k = _schedule_facts(metadata)[3:5]
-    if max_queries != length or top_q >= batch * length or top_k >= batch * key_slots:
-        raise ValueError("metadata was prepared for other query/key shapes")
-    cover = _covering_schedule(metadata, batch, length, key_slots)
-    plan = _PackedPlan()
-    plan.others = (tuple(weakref.ref(t) for t in (ki, cq, ck)), versions)
-    plan.cover = None if cover is metadata else cover
-    plan.max_q, plan.max_k, plan.flags = _schedule_flags(cover)
-    plan.gaps = _schedule_gaps(cover, batch, length, heads, key_slots, kv_heads)
-    plan.units = _work_units(cover, query_extent=length)
-    by_shape[shape] = plan
-    return plan
-
-
-@torch.library.custom_op("white_matter::strict_packed_fwd", mutates_args=())
-def strict_packed_fwd(
-    query: torch.Tensor,
-    key: torch.Tensor,
-    value: torch.Tensor,
+@torch.library.custom_op("white_matter::_packed_plan", mutates_args=())
+def _packed_plan(
     query_indices: torch.Tensor,
     key_indices: torch.Tensor,
     cu_queries: torch.Tensor,
     cu_keys: torch.Tensor,
     max_queries: int,
     max_keys: int,
-    scale: float,
-) -> tuple[torch.Tensor, torch.Tensor]:
-    """Attention over a packed-document schedule given as its own tensors
-    (StrictCausalMetadata's fields): the host work the kernels need is planned
-    inside the operator, so a compiled graph holds this call and nothing
-    data-dependent. Output (B, T, H, D) bf16 and LSE (B, H, T) fp32."""
-    batch, heads, length, _ = query.shape
-    plan = _packed_plan(
-        query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, batch, length, key.shape[2], heads,
-        key.shape[1],
+    batch: int,
+    length: int,
+    key_slots: int,
+    heads: int,
+    kv_heads: int,
+) -> list[torch.Tensor]:
+    """The plan of a packed-document schedule for one call shape, built when
+    the C++ packed operators miss their plan cache (which holds it until one
+    of the schedule's tensors is freed or changed in place): a CPU int64 facts
+    tensor {num_segments, max_queries, max_keys, segment_layout, keys_unique,
+    ds_elements, covered}, the covering schedule's query_indices, key_indices,
+    cu_queries and cu_keys (empty when it is the schedule itself: covered 0),
+    the rows no segment writes (out_gaps, dq_gaps, dkv_gaps, see
+    _schedule_gaps) and the work lists q_units, k_units, ds_offsets (see
+    _work_units)."""
+    _kernels.guard_capture("planning a packed-document schedule")
+    metadata = StrictCausalMetadata(query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, key_slots)
+    top_q, top_k = _schedule_facts(metadata)[3:5]
+    if max_queries != length or top_q >= batch * length or top_k >= batch * key_slots:
+        raise ValueError("metadata was prepared for other query/key shapes")
+    cover = _covering_schedule(metadata, batch, length, key_slots)
+    max_q, max_k, flags = _schedule_flags(cover)
+    gaps = _schedule_gaps(cover, batch, length, heads, key_slots, kv_heads)
+    q_units, k_units, ds_offsets, ds_elements = _work_units(cover, query_extent=length)
+    covered = cover is not metadata
+    facts = torch.tensor(
+        [cover.cu_queries.numel() - 1, max_q, max_k, flags & 15, _keys_unique_code(flags), ds_elements, int(covered)],
+        dtype=torch.int64,
     )
-    qi, ki, cq, ck = plan.schedule(query_indices, key_indices, cu_queries, cu_keys)
-    return _varlen_forward(
-        query, key, value, qi, ki, cq, ck, plan.max_q, plan.max_k, plan.flags, scale, plan.gaps[0], *plan.units[:2]
+    device = query_indices.device
+
+    def fresh(t: torch.Tensor) -> torch.Tensor:
+        # outputs of an operator may not alias its inputs or each other
+        return t.clone() if t.numel() == 0 else t
+
+    schedule = (
+        [cover.query_indices, cover.key_indices, cover.cu_queries, cover.cu_keys]
+        if covered
+        else [torch.empty(0, dtype=torch.int64, device=device) for _ in range(4)]
     )
+    return [facts, *schedule, *(fresh(g) for g in gaps), q_units, k_units, ds_offsets]
 
 
-@strict_packed_fwd.register_fake
-def _(query, key, value, *args):
+def _fake_packed_fwd(query, key, value, *args):
     batch, heads, length, dim = query.shape
     return (
         query.new_empty(batch, length, heads, dim, dtype=torch.bfloat16),
@@ -898,37 +764,7 @@ def _(query, key, value, *args):
     )
 
 
-@torch.library.custom_op("white_matter::strict_packed_bwd", mutates_args=())
-def strict_packed_bwd(
-    query: torch.Tensor,
-    key: torch.Tensor,
-    value: torch.Tensor,
-    out: torch.Tensor,
-    lse: torch.Tensor,
-    dout: torch.Tensor,
-    query_indices: torch.Tensor,
-    key_indices: torch.Tensor,
-    cu_queries: torch.Tensor,
-    cu_keys: torch.Tensor,
-    max_queries: int,
-    max_keys: int,
-    scale: float,
-) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
-    """Gradients of strict_packed_fwd (the same plan)."""
-    batch, heads, length, _ = query.shape
-    plan = _packed_plan(
-        query_indices, key_indices, cu_queries, cu_keys, max_queries, max_keys, batch, length, key.shape[2], heads,
-        key.shape[1],
-    )
-    qi, ki, cq, ck = plan.schedule(query_indices, key_indices, cu_queries, cu_keys)
-    return _varlen_backward_kernels(
-        query, key, value, out, lse, dout, qi, ki, cq, ck, plan.max_q, plan.max_k, plan.flags, scale, *plan.gaps[1:],
-        *plan.units,
-    )
-
-
-@strict_packed_bwd.register_fake
-def _(query, key, value, *args):
+def _fake_grads(query, key, value, *args):
     return (
         query.new_empty(query.shape, dtype=torch.bfloat16),
         key.new_empty(key.shape, dtype=torch.bfloat16),
@@ -936,60 +772,37 @@ def _(query, key, value, *args):
     )
 
 
-def _packed_setup(ctx, inputs, output):
-    query, key, value, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.scale = inputs
-    ctx.dtypes = (query.dtype, key.dtype, value.dtype)
-    ctx.save_for_backward(query, key, value, *output, qi, ki, cq, ck)
-    ctx.set_materialize_grads(False)  # the LSE output has no gradient: no zero fill for it
-
-
-def _packed_backward(ctx, dout, dlse):
-    query, key, value, out, lse, qi, ki, cq, ck = ctx.saved_tensors
-    if dout is None:
-        dout = torch.zeros_like(out)
-    dq, dk, dv = strict_packed_bwd(query, key, value, out, lse, dout, qi, ki, cq, ck, ctx.max_q, ctx.max_k, ctx.scale)
-    return (dq.to(ctx.dtypes[0]), dk.to(ctx.dtypes[1]), dv.to(ctx.dtypes[2])) + (None,) * 7
-
-
-strict_packed_fwd.register_autograd(_packed_backward, setup_context=_packed_setup)
-
-
-@torch.library.custom_op("white_matter::strict_decode", mutates_args=())
-def strict_decode(
-    query: torch.Tensor,
-    key: torch.Tensor,
-    value: torch.Tensor,
-    query_start: torch.Tensor | None,
-    query_start_value: int,
-    kv_lengths: torch.Tensor | None,
-    key_mask: torch.Tensor | None,
-    use_dummy: bool,
-    scale: float,
-    num_splits: int,
-) -> torch.Tensor:
-    """One query token per row over the KV pool; output (B, 1, H, D) bf16."""
-    q, k, v = (_kernels.operand(t) for t in (query, key, value))
-    batch, heads, _, dim = q.shape
-    out = torch.empty(batch, 1, heads, dim, device=q.device, dtype=torch.bfloat16)
-    _kernels.decode(
-        q,
-        k,
-        v,
-        out[:, 0],
-        query_start=query_start_value if query_start is None else query_start,
-        kv_lengths=kv_lengths,
-        key_mask=None if key_mask is None else key_mask.contiguous().view(torch.uint8),
-        use_dummy=use_dummy,
-        scale=scale,
-        num_splits=num_splits,
-    )
-    return out
-
-
-@strict_decode.register_fake
-def _(query, *args):
+def _fake_decode(query, *args):
     batch, heads, _, dim = query.shape
     return query.new_empty(batch, 1, heads, dim, dtype=torch.bfloat16)
+
+
+for _name, _fake in (
+    ("strict_packed_fwd", _fake_packed_fwd),
+    ("strict_packed_bwd", _fake_grads),
+    ("strict_dense_fwd", _fake_packed_fwd),
+    ("strict_dense_bwd", _fake_grads),
+    ("strict_decode", _fake_decode),
+):
+    torch.library.register_fake(f"white_matter::{_name}", _fake)
+
+# strict_packed_fwd(query, key, value, query_indices, key_indices, cu_queries,
+#     cu_keys, max_queries, max_keys, scale) -> (out (B, T, H, D) bf16, lse)
+#     attention over a packed-document schedule given as its own tensors
+#     (StrictCausalMetadata's fields), differentiable; the plan is built inside
+#     the operator, so a compiled graph holds this call and nothing data-dependent
+strict_packed_fwd = torch.ops.white_matter.strict_packed_fwd
+strict_packed_bwd = torch.ops.white_matter.strict_packed_bwd
+# strict_dense_fwd(query, key, value, query_offset, row_offset, row_limit,
+#     key_mask, keep_slot0, scale) -> (out, lse): key slot j is visible to query
+#     i of row b iff j <= min(offset_b + i, limit_b), or j == 0 with keep_slot0,
+#     and key_mask[b, j] when given; differentiable
+strict_dense_fwd = torch.ops.white_matter.strict_dense_fwd
+strict_dense_bwd = torch.ops.white_matter.strict_dense_bwd
+# strict_decode(query, key, value, query_start, query_start_value, kv_lengths,
+#     key_mask, use_dummy, scale, num_splits) -> (B, 1, H, D) bf16: one query
+#     token per row over the KV pool (no gradient)
+strict_decode = torch.ops.white_matter.strict_decode
 
 
 # ------------------------------------------------------------ public API ----

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 8
+#define WMX_ABI_VERSION 9
 
 enum {
   WMX_OK = 0,
@@ -188,7 +188,8 @@ enum {
  * start_b is query_start[b] when given, else query_start_scalar; kvlen_b is
  * kv_lengths[b] when given, else unbounded.
  * The work is split over num_splits key ranges per (b, kv head) whose partial
- * (o, max, sum) rows live in the workspace and are merged by a second kernel.
+ * (o, max, sum) rows live in the workspace and are merged by the last split
+ * to finish (with counters) or by a second kernel (without).
  */
 typedef struct wmx_decode_args {
   const void* q;        /* bf16 (B, Hq, 1, D) */
@@ -214,6 +215,13 @@ typedef struct wmx_decode_args {
   int32_t use_dummy;
   int32_t num_splits;   /* <= 0: chosen by the library */
   float softmax_scale;
+  /* Optional, batch * kv_heads int32, zero on entry and left zero: with it
+   * the last split of each (row, KV head) to finish merges the splits (one
+   * launch per call) where the launch is short (at most 1024 workgroups, 64
+   * splits); otherwise, and without it, a second kernel does. The outputs are
+   * bit-identical. Calls that share counters must not overlap (calls in
+   * order on one stream do not). */
+  int32_t* counters;
 } wmx_decode_args;
 
 /*
@@ -507,16 +515,21 @@ int wmx_decode(const wmx_decode_args* args, void* stream);
 /*
  * wmx_decode without a workspace: the split-K partials go to a static device
  * array of WMX_DECODE_NOALLOC_MAX_BYTES that the library holds on each GPU it
- * runs on until the process ends (args->workspace and workspace_bytes are
- * ignored). No counterpart in the reference: this entry point is for callers
- * that cannot allocate device memory (code under HIP graph capture, serving
- * loops, harnesses that forbid hipMalloc). It calls no allocating routine; a
- * call whose wmx_decode_workspace_size exceeds the maximum returns
- * WMX_E_WORKSPACE. Every call on one GPU shares that GPU's array, so calls
- * that overlap on one GPU (concurrent streams, or threads) race; calls in
- * order on one stream do not. The array's first use on a device resolves its
- * address there (hipGetSymbolAddress) with that device current; the stream
- * must belong to the current device. Outputs are bit-identical to wmx_decode's.
+ * runs on until the process ends (args->workspace, workspace_bytes and
+ * counters are ignored; a second kernel merges the splits). No counterpart in
+ * the reference: this entry point is for callers that cannot allocate device
+ * memory (code under HIP graph capture, serving loops, harnesses that forbid
+ * hipMalloc). It calls no allocating routine. The partials of s splits take
+ * batch * q_heads * s * (head_dim + 2) * 4 bytes; where the split count
+ * wmx_decode would use (wmx_decode_num_splits) needs more than the maximum,
+ * this call uses the largest count that fits (at least one: a single split
+ * needs no scratch), and its outputs then differ from wmx_decode's by the
+ * summation order of the splits; otherwise they are bit-identical. Every call
+ * on one GPU shares that GPU's array, so calls that overlap on one GPU
+ * (concurrent streams, or threads) race; calls in order on one stream do not.
+ * The array's first use on a device resolves its address there
+ * (hipGetSymbolAddress) with that device current; the stream must belong to
+ * the current device.
  */
 #define WMX_DECODE_NOALLOC_MAX_BYTES ((int64_t)8 << 20)
 int wmx_decode_noalloc(const wmx_decode_args* args, void* stream);

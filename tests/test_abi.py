@@ -61,13 +61,13 @@ def test_argument_checks_return_errors_without_launching():
     assert lib.wmx_decode(ctypes.byref(dec), None) == -2
     assert b"head_dim" in lib.wmx_last_error()
     dec.head_dim, dec.kv_heads = 128, 2
-    # the allocation-free decode refuses partials beyond its static scratch
-    # before it touches a device
+    # the allocation-free decode checks its arguments before it touches a
+    # device (partials beyond its static scratch take fewer splits instead)
     dec.q_heads, dec.capacity, dec.num_splits, dec.softmax_scale = 2, 4096, 20000, 0.1
     dec.q = dec.k = dec.v = dec.o = 0x1000
-    assert lib.wmx_decode_workspace_size(ctypes.byref(dec)) > _native.DECODE_NOALLOC_MAX_BYTES
-    assert lib.wmx_decode_noalloc(ctypes.byref(dec), None) == -3
-    assert b"static scratch" in lib.wmx_last_error()
+    dec.use_dummy = 2
+    assert lib.wmx_decode_noalloc(ctypes.byref(dec), None) == -1
+    assert b"use_dummy" in lib.wmx_last_error()
     bwd = _native.KvStoreBwdArgs()
     bwd.head_dim, bwd.batch, bwd.channels, bwd.heads, bwd.tokens = 80, 1, 1, 1, 1
     assert lib.wmx_kv_store_bwd(ctypes.byref(bwd), None) == -2

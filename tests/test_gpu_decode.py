@@ -177,3 +177,32 @@ def test_torch_flash_varlen_packed_segments():
     ge = torch.autograd.grad(expected, leaves, probe.cpu().double())
     for name, a, e in zip("qkv", ga, ge):
         assert_bf16_close(a, e, what=f"TorchFlashVarlen d{name}")
+
+
+@pytest.mark.parametrize(("batch", "kv_heads", "group", "dim"), [(3, 5, 1, 128), (4, 2, 12, 64), (32, 16, 1, 128), (7, 3, 2, 96)])
+@torch.no_grad()
+def test_merge_by_last_split_matches_combine_kernel(batch, kv_heads, group, dim):
+    """The operator's decode merges the splits in the last split to finish
+    (counters kept per stream); the C ABI call without counters runs the
+    separate combine kernel. Same terms in the same order: bit-identical, on
+    repeated calls (each launch leaves its counters zero), for row and KV-head
+    counts that spread one row's splits over several XCDs (batch * kv_heads
+    not a multiple of 8) and for groups of more than 8 heads (two launches
+    sharing the counters)."""
+    from white_matter_amd import _kernels
+
+    gen = torch.Generator().manual_seed(batch * 100 + kv_heads * 10 + group)
+    heads, capacity = kv_heads * group, 5000
+    q = _normal((batch, heads, 1, dim), gen, dim)
+    k = _normal((batch, kv_heads, capacity, dim), gen, dim)
+    v = _normal((batch, kv_heads, capacity, dim), gen, dim)
+    lengths = torch.randint(0, capacity + 1, (batch,), generator=gen).to(DEV)
+    for call in range(3):
+        print(f"last-split merge B={batch} Hkv={kv_heads} G={group} D={dim} call {call}", flush=True)
+        merged = strict_causal_attention(q, k, v, query_start=lengths, kv_lengths=lengths)
+        combined = torch.empty(batch, heads, dim, device=DEV, dtype=torch.bfloat16)
+        _kernels.decode(q, k, v, combined, query_start=lengths, kv_lengths=lengths, key_mask=None, use_dummy=False,
+                        scale=dim**-0.5)
+        assert torch.equal(merged[:, 0], combined)
+    expected = ref.strict_attention(q.cpu(), k.cpu(), v.cpu(), query_start=lengths.cpu(), kv_lengths=lengths.cpu())
+    assert_bf16_close(merged, expected, what="last-split merge")

@@ -1,8 +1,10 @@
 """wmx_decode_noalloc (the allocation-free decode entry point) through the C
 ABI: on two calls in a row, the second with a smaller input, its output is
 bit-identical to wmx_decode's with a caller-allocated workspace (both run the
-same kernels; only where the split-K partials live differs), and a call whose
-partials exceed the static scratch is refused without touching the output."""
+same kernels; only where the split-K partials live differs), and where the
+split count wmx_decode would use needs more partials than the static scratch
+holds, it runs the largest count that fits: bit-identical to wmx_decode at
+that count, within the bf16 bar of wmx_decode at its own."""
 
 import ctypes
 
@@ -69,14 +71,41 @@ def test_noalloc_matches_wmx_decode_on_two_calls():
         assert torch.equal(out, ref), f"call {i}: wmx_decode_noalloc differs from wmx_decode"
 
 
-def test_noalloc_refuses_partials_beyond_the_scratch():
-    q, k, v, lengths, _ = _case(batch=2, heads=8, kv_heads=2, capacity=4096, dim=128, num_splits=0, seed=3)
+def _decode(q, k, v, lengths, num_splits, noalloc):
     lib = _native.load()
-    out = torch.zeros(2, 8, 128, device=DEV, dtype=torch.bfloat16)
-    # 2 x 8 heads x 2000 splits x 130 floats = 16.6 MB of partials > 8 MiB
-    a = _args(q, k, v, out, lengths, num_splits=2000)
-    assert int(lib.wmx_decode_workspace_size(ctypes.byref(a))) > _native.DECODE_NOALLOC_MAX_BYTES
-    rc = lib.wmx_decode_noalloc(ctypes.byref(a), torch.cuda.current_stream().cuda_stream)
-    assert rc == -3 and b"static scratch" in lib.wmx_last_error()
+    out = torch.full((q.shape[0], q.shape[1], q.shape[3]), float("nan"), device=DEV, dtype=torch.bfloat16)
+    a = _args(q, k, v, out, lengths, num_splits)
+    workspace = None
+    if not noalloc:
+        need = int(lib.wmx_decode_workspace_size(ctypes.byref(a)))
+        workspace = torch.empty(max(need, 16), device=DEV, dtype=torch.uint8)
+        a.workspace, a.workspace_bytes = workspace.data_ptr(), need
+    entry = lib.wmx_decode_noalloc if noalloc else lib.wmx_decode
+    assert entry(ctypes.byref(a), torch.cuda.current_stream().cuda_stream) == 0, lib.wmx_last_error()
     torch.cuda.synchronize()
-    assert out.count_nonzero() == 0
+    return out, a
+
+
+@pytest.mark.parametrize("requested", [0, 2000])
+def test_noalloc_clamps_splits_to_the_scratch(requested):
+    # 8 rows x 64 query heads x (128 + 2) floats = 266,240 bytes per split:
+    # 31 splits fit the 8 MiB scratch; a 33,792-slot cache asks for 33 splits
+    # by default (1024 keys a split), and 2000 are asked for explicitly
+    print(f"no-alloc clamp case: requested splits {requested}", flush=True)
+    gen = torch.Generator().manual_seed(4)
+    batch, heads, kv_heads, capacity, dim = 8, 64, 8, 33 * 1024, 128
+    q = torch.randn(batch, heads, 1, dim, generator=gen).to(DEV, torch.bfloat16)
+    k = torch.empty(batch, kv_heads, capacity, dim, device=DEV, dtype=torch.bfloat16).normal_(0, 1)
+    v = torch.empty_like(k).normal_(0, 1)
+    lengths = torch.randint(capacity // 2, capacity + 1, (batch,), generator=gen).to(DEV)
+    lib = _native.load()
+    per_split = batch * heads * (dim + 2) * 4
+    fit = _native.DECODE_NOALLOC_MAX_BYTES // per_split
+    out, a = _decode(q, k, v, lengths, requested, noalloc=True)
+    natural = int(lib.wmx_decode_num_splits(ctypes.byref(a)))
+    assert natural > fit == 31, "the case must ask for more partials than the scratch holds"
+    same, _ = _decode(q, k, v, lengths, fit, noalloc=False)
+    assert torch.equal(out, same), "the clamped call must equal wmx_decode at the clamped split count"
+    full, _ = _decode(q, k, v, lengths, requested, noalloc=False)
+    assert torch.isfinite(out.float()).all()
+    assert (out.float() - full.float()).abs().max().item() < 1e-2

@@ -19,7 +19,7 @@ import torch
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
 # the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
 OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -116,6 +116,7 @@ class DecodeArgs(ctypes.Structure):
         ("use_dummy", ctypes.c_int32),
         ("num_splits", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float),
+        ("counters", _vp),
     ]
 
 

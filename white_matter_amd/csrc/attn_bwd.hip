@@ -488,32 +488,38 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
 // One workgroup = 128 keys of one (batch row or segment, kv head) and eight
 // waves: wave pair p (waves p and p + 4, which share SIMD p) owns keys
 // 32p .. 32p + 31. The pair splits the work so each wave holds half of the
-// state and the two waves of a SIMD alternate between matrix and vector work:
+// state:
 //   wave p     ("S side")  holds K rows, computes S = Q K^T, the mask and
 //              P = exp2(S c log2e - lse), hands P to its partner through LDS
 //              and accumulates dV^T = dO^T P;
 //   wave p + 4 ("dP side") holds V rows, computes dP = dO V^T, takes P and
 //              forms dS = P (dP - delta), and accumulates dK^T = Q^T dS.
-// Query and output-gradient tiles of 64 rows for every query head of the
-// group stream through double-buffered LDS (direct-to-LDS loads); each tile
-// is read row-wise for S and dP and by transpose reads for dV and dK.
+// Query and output-gradient tiles of 32 rows for every query head of the
+// group stream through four LDS buffers (direct-to-LDS loads issued by the S
+// side two tiles ahead); each tile is read row-wise for S and dP and by
+// transpose reads for dV and dK. The dP side works one tile behind the S
+// side: in step j the S side takes tile j and the dP side tile j - 1, whose P
+// the S side left in the other of two hand-over buffers in step j - 1. The
+// two waves of a SIMD then never wait for each other inside a step (one
+// workgroup barrier per step), and one's matrix products overlap the other's
+// vector work.
 template <int D, int MODE, bool ATOMIC, bool DS>
 __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args args) {
   const wmx_attn_args& a = args;
-  constexpr int BNK = 128, BMQ = 64, NW = 8;
-  static_assert(BMQ == kTileRows, "one LDS tile per query tile");
+  constexpr int BNK = 128, BMQ = 32, NW = 8;
   constexpr int KS = D / 16, DB = D / 32;
-  // two buffers as distinct arrays with static roles (the loop is unrolled
-  // by two): prefetches into one buffer are then known not to alias reads
-  // of the other, so reads never wait for the prefetch
-  __shared__ __attribute__((aligned(1024))) bf16 q_lds0[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 q_lds1[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 g_lds0[kTileElems];
-  __shared__ __attribute__((aligned(1024))) bf16 g_lds1[kTileElems];
-  // P from the S side to the dP side: [pair][32-row half][register quad][lane]
-  __shared__ __attribute__((aligned(16))) f32x4 p_lds[4][BMQ / 32][4][64];
-  __shared__ __attribute__((aligned(16))) float stat_lds[2][2][BMQ];  // lse * log2e, delta
-  __shared__ __attribute__((aligned(16))) int qdoc_lds[2][2][BMQ];    // document id, document start
+  constexpr int kTile32 = BMQ * kRowElems;  // 8 KB: the first 32 rows of the tile layout
+  // four buffers indexed by compile-time constants only (the loop is
+  // unrolled by four): prefetches into one buffer are then known not to alias
+  // reads of the others, so reads never wait for the prefetch
+  __shared__ __attribute__((aligned(1024))) bf16 q_lds[4][kTile32];
+  __shared__ __attribute__((aligned(1024))) bf16 g_lds[4][kTile32];
+  // P of tile t from the S side to the dP side: [t % 2][pair][register quad][lane]
+  __shared__ __attribute__((aligned(16))) f32x4 p_lds[2][4][4][64];
+  // lse, delta, document id and start of the tile's rows (entries past BMQ:
+  // the 4-byte direct-to-LDS loads of lanes 32 .. 63, never read)
+  __shared__ __attribute__((aligned(16))) float stat_lds[4][2][64];
+  __shared__ __attribute__((aligned(16))) int qdoc_lds[4][2][64];
   __shared__ int red_lds[NW];
   // per key of the workgroup: first query row that sees it, document id,
   // document query end (kept in LDS rather than in registers)
@@ -612,18 +618,32 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   const int m_first = (m_begin / BMQ) * BMQ;
   const int nqt = m_end > m_first ? (m_end - m_first + BMQ - 1) / BMQ : 0;
   const int total = nqt * group;
-  TileDMA<D, NW> dma;
-  dma.init(wave, lane);
-  QueryTiles<MODE, D, NW> qrows;
-  qrows.init(a, pb, dma);
+  // the four S-side waves load every tile
+  TileDMA<D, 4, BMQ> dma;
+  dma.init(pair, lane);
+  QueryTiles<MODE, D, 4, BMQ> qrows;
+  qrows.init(a, pb);
   RowReads<KS> rrd;
   rrd.init(col, half);
   TrReads<DB> trd;
   trd.init(lane);
 
+  // tile t is (query head hk * group + t / nqt, first row m_first + BMQ (t % nqt))
+  struct Cursor {
+    int hq, m0;
+  };
+  auto advance = [&](Cursor& c) {
+    c.m0 += BMQ;
+    if (c.m0 >= m_end) {
+      c.m0 = m_first;
+      ++c.hq;
+    }
+  };
+  auto active = [&](int m0) { return pair_live && m0 + BMQ > pair_m_begin; };  // uniform over the pair
+
   // per-row statistics (and document metadata) of query tile (hq, m0), loaded
   // by wave 0 straight into LDS buffer B with the tile (one 4-byte direct-to-
-  // LDS load per array: no registers, no waits until the tile barrier). Rows
+  // LDS load per array: no registers, no waits until the step barrier). Rows
   // past nq read as zeros; their scores are masked.
   auto issue_meta = [&](auto bufc, int hq, int m0) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
@@ -634,15 +654,21 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       if (consecutive) {
         // one buffer resource per array, this lane's row at byte 4 * lane
         // (rows past nq fall outside the resource and read as zeros)
-        const int nvalid = min(max(nq - m0, 0), kTileRows) * 4;
+        const int nvalid = min(max(nq - m0, 0), BMQ) * 4;  // lanes past the tile read zeros
         const int64_t r0 = ((int64_t)qrows.qrow * a.q_heads + hq) * a.q_len + qrows.qfirst + m0;
-        const unsigned off = 4u * lane;
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.lse + r0, nvalid), (lds_void*)&stat_lds[B][0][0], 4, off, 0, 0, 0);
-        __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.delta + r0, nvalid), (lds_void*)&stat_lds[B][1][0], 4, off, 0, 0, 0);
+        const rsrc_t rl = make_rsrc(a.lse + r0, nvalid), rd = make_rsrc(a.delta + r0, nvalid);
+        rsrc_t rs, rq;
         if constexpr (MODE == kDoc) {
           const int64_t d0 = (int64_t)b * a.q_len + m0;
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.q_seg + d0, nvalid), (lds_void*)&qdoc_lds[B][0][0], 4, off, 0, 0, 0);
-          __builtin_amdgcn_raw_ptr_buffer_load_lds(make_rsrc(a.q_start + d0, nvalid), (lds_void*)&qdoc_lds[B][1][0], 4, off, 0, 0, 0);
+          rs = make_rsrc(a.q_seg + d0, nvalid);
+          rq = make_rsrc(a.q_start + d0, nvalid);
+        }
+        const unsigned off = 4u * lane;
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rl, (lds_void*)&stat_lds[B][0][0], 4, off, 0, 0, 0);
+        __builtin_amdgcn_raw_ptr_buffer_load_lds(rd, (lds_void*)&stat_lds[B][1][0], 4, off, 0, 0, 0);
+        if constexpr (MODE == kDoc) {
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (lds_void*)&qdoc_lds[B][0][0], 4, off, 0, 0, 0);
+          __builtin_amdgcn_raw_ptr_buffer_load_lds(rq, (lds_void*)&qdoc_lds[B][1][0], 4, off, 0, 0, 0);
         }
       } else if constexpr (MODE == kVarlen) {
         const int m = m0 + lane;
@@ -657,222 +683,238 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       }
     }
   };
+  // tile (hq, m0) and its statistics into buffer B (S side only)
+  auto issue_tile = [&](auto bufc, const Cursor& c) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    bf16* const qt = q_lds[B];
+    bf16* const gt = g_lds[B];
+    issue_meta(bufc, c.hq, c.m0);
+    qrows.issue(a, pb, dma, c.hq, c.m0, qt, gt);
+  };
 
   // first query row that sees this lane's key (INT_MAX for a dead key): the
   // causal/offset rule is then one comparison per score. Read back from LDS
-  // in each step (published by the first tile barrier).
+  // in each step (published by the first step barrier).
   if (!dp_side && half == 0) {
     key_lds[0][pair * 32 + col] = !k_live ? INT_MAX : (slot0 && n == 0) ? 0 : pb.bound.first_row(n, nq);
     key_lds[1][pair * 32 + col] = kseg_n;
     key_lds[2][pair * 32 + col] = kqend_n;
   }
 
-  // One query tile against the pair's 32 keys: the first half runs before
-  // the P hand-over barrier, the second after it.
-  f32x16 tacc[BMQ / 32];  // S side: P; dP side: dP, then dS
-  // Each role reads its own tile through a compile-time base (a runtime
-  // choice between two LDS arrays would hide from the compiler that the
-  // prefetch never writes them, and it would wait for the prefetch).
-  auto first_half = [&](auto bufc, auto sidec, int m0) __attribute__((always_inline)) {
+  // S side, one tile (in Q/dO buffer B, its P to hand-over buffer B % 2)
+  auto s_step = [&](auto bufc, int m0) __attribute__((always_inline)) {
     constexpr int B = decltype(bufc)::value;
-    constexpr bool DP = decltype(sidec)::value;
-    const bf16* rows = DP ? (B ? g_lds1 : g_lds0) : (B ? q_lds1 : q_lds0);  // dO rows for dP, Q rows for S
+    const bf16* const qt = q_lds[B];
+    const bf16* const gt = g_lds[B];
     rrd.refresh();
-#pragma unroll
-    for (int mb = 0; mb < BMQ / 32; ++mb) tacc[mb] = f32x16{};
-    // k-step major, each operand read PF k-steps ahead of its product (the
-    // scheduling barriers keep the compiler from sinking the reads next to
-    // their uses, where every product would wait out the LDS latency)
+    trd.refresh();
+    f32x16 sacc = f32x16{};
+    // S = Q K^T, k-step major, each Q operand read PF k-steps ahead of its
+    // product (the scheduling barriers keep the compiler from sinking the
+    // reads next to their uses, where every product would wait out the LDS
+    // latency)
     constexpr int PF = KS < 4 ? KS : 4;
-    bf16x8 op[KS][BMQ / 32];
+    bf16x8 op[KS];
 #pragma unroll
-    for (int s = 0; s < PF; ++s) {
-#pragma unroll
-      for (int mb = 0; mb < BMQ / 32; ++mb) op[s][mb] = rrd.get(rows, s, mb);
-    }
+    for (int s = 0; s < PF; ++s) op[s] = rrd.get(qt, s, 0);
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       __builtin_amdgcn_sched_barrier(0);
-      if (s + PF < KS) {
-#pragma unroll
-        for (int mb = 0; mb < BMQ / 32; ++mb) op[s + PF][mb] = rrd.get(rows, s + PF, mb);
-      }
-#pragma unroll
-      for (int mb = 0; mb < BMQ / 32; ++mb) tacc[mb] = mfma32(op[s][mb], kvf[s], tacc[mb]);
+      if (s + PF < KS) op[s + PF] = rrd.get(qt, s + PF, 0);
+      sacc = mfma32(op[s], kvf[s], sacc);
     }
     __builtin_amdgcn_sched_barrier(0);
-    if constexpr (DP) return;
-    // the rows' lse, read while the products drain
-    f32x4 l4s[BMQ / 32][4];
+    // the rows' lse and the first dO^T operands, read while the products drain
+    f32x4 l4s[4];
 #pragma unroll
-    for (int mb = 0; mb < BMQ / 32; ++mb) {
+    for (int g = 0; g < 4; ++g) l4s[g] = *reinterpret_cast<const f32x4*>(&stat_lds[B][0][8 * g + 4 * half]);
+    bf16x8 top[BMQ / 16][DB];
 #pragma unroll
-      for (int g = 0; g < 4; ++g) l4s[mb][g] = *reinterpret_cast<const f32x4*>(&stat_lds[B][0][mb * 32 + 8 * g + 4 * half]);
-    }
+    for (int d = 0; d < DB; ++d) top[0][d] = trd.get(gt, d, 0);
     // every pair of the tile is visible to this pair's keys: no per-element mask
     const bool full = (MODE == kVarlen || (MODE == kDense && !a.key_mask)) && m0 >= pair_m_begin &&
                       m0 + BMQ <= nq && pb.bound.lim(m0) >= pair_key0 + 31;
-    const int kl = pair * 32 + (__lane_id() & 31);
-    const int lo = key_lds[0][kl] - m0, hi = nq - m0;  // rows ml in [lo, hi) see the key
-    int kseg = 0, kqend = 0;
-    if constexpr (MODE == kDoc) {
-      kseg = key_lds[1][kl];
-      kqend = key_lds[2][kl];
-    }
-    // element r of block mb is row ml = 4 half + c with the constant
-    // c = 32 mb + 8 (r / 4) + r % 4: the row rules become compares of c
-    // against per-lane bounds
-    const int lo_c = lo - 4 * half, hi_c = hi - 4 * half, kqend_c = kqend - m0 - 4 * half;
-#pragma unroll
-    for (int mb = 0; mb < BMQ / 32; ++mb) {
-      if (!full) {
-        // keeps this block a real (wave-uniform) branch instead of selects
-        __asm__ volatile("");
-#pragma unroll
-        for (int r = 0; r < 16; ++r) {
-          const int c = mb * 32 + 8 * (r >> 2) + (r & 3);
-          const int ml = c + 4 * half;
-          bool keep = (c >= lo_c) & (c < hi_c);
-          if constexpr (MODE == kDoc) {
-            const int qsg = qdoc_lds[B][0][ml], qst = qdoc_lds[B][1][ml];
-            keep = keep & (((qsg == kseg) & (n >= qst)) | (kseg == -1)) & (c < kqend_c);
-          }
-          tacc[mb][r] = keep ? tacc[mb][r] : kNegInf;
-        }
+    if (!full) {
+      // keeps this block a real (wave-uniform) branch instead of selects
+      __asm__ volatile("");
+      const int kl = pair * 32 + col;
+      const int lo = key_lds[0][kl] - m0, hi = nq - m0;  // rows ml in [lo, hi) see the key
+      int kseg = 0, kqend = 0;
+      if constexpr (MODE == kDoc) {
+        kseg = key_lds[1][kl];
+        kqend = key_lds[2][kl];
       }
+      // element r is row ml = 4 half + c with the constant c = 8 (r / 4) + r % 4:
+      // the row rules become compares of c against per-lane bounds
+      const int lo_c = lo - 4 * half, hi_c = hi - 4 * half, kqend_c = kqend - m0 - 4 * half;
 #pragma unroll
-      for (int g = 0; g < 4; ++g) {
-        const f32x4 l4 = l4s[mb][g];
-        f32x4 p4;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          // a masked score is -inf and gives p = 0 exactly (lse is finite or +inf)
-          p4[e] = __builtin_amdgcn_exp2f(fmaf(tacc[mb][4 * g + e], sl2, -l4[e] * kLog2e));
-          tacc[mb][4 * g + e] = p4[e];
+      for (int r = 0; r < 16; ++r) {
+        const int c = 8 * (r >> 2) + (r & 3);
+        const int ml = c + 4 * half;
+        bool keep = (c >= lo_c) & (c < hi_c);
+        if constexpr (MODE == kDoc) {
+          const int qsg = qdoc_lds[B][0][ml], qst = qdoc_lds[B][1][ml];
+          keep = keep & (((qsg == kseg) & (n >= qst)) | (kseg == -1)) & (c < kqend_c);
         }
-        p_lds[pair][mb][g][lane] = p4;
+        sacc[r] = keep ? sacc[r] : kNegInf;
       }
     }
-  };
-  auto second_half = [&](auto bufc, auto sidec, int hq, int m0) __attribute__((always_inline)) {
-    constexpr int B = decltype(bufc)::value;
-    constexpr bool DP = decltype(sidec)::value;
-    trd.refresh();
-    const bf16* tr = DP ? (B ? q_lds1 : q_lds0) : (B ? g_lds1 : g_lds0);  // Q^T for dK, dO^T for dV
-    // transposed operands one k-step ahead of their products
-    bf16x8 top[BMQ / 16][DB];
 #pragma unroll
-    for (int d = 0; d < DB; ++d) top[0][d] = trd.get(tr, d, 0);
-    // dP side: dS = P (dP - delta) per k-step (its two register quads), P and
-    // delta read one k-step ahead
-    f32x4 d4s[BMQ / 16][2], p4s[BMQ / 16][2];
-    auto read_pd = [&](int s) __attribute__((always_inline)) {
+    for (int g = 0; g < 4; ++g) {
+      const f32x4 l4 = l4s[g];
+      f32x4 p4;
 #pragma unroll
-      for (int q = 0; q < 2; ++q) {
-        const int g = 2 * (s & 1) + q, mb = s >> 1;
-        d4s[s][q] = *reinterpret_cast<const f32x4*>(&stat_lds[B][1][mb * 32 + 8 * g + 4 * half]);
-        p4s[s][q] = p_lds[pair][mb][g][lane];
+      for (int e = 0; e < 4; ++e) {
+        // a masked score is -inf and gives p = 0 exactly (lse is finite or +inf)
+        p4[e] = __builtin_amdgcn_exp2f(fmaf(sacc[4 * g + e], sl2, -l4[e] * kLog2e));
+        sacc[4 * g + e] = p4[e];
       }
-    };
-    if constexpr (DP) read_pd(0);
-    bf16* ds_row = nullptr;
-    if constexpr (DP && DS) ds_row = ds_key + hq * ds_head + m0;
+      p_lds[B & 1][pair][g][lane] = p4;
+    }
+    // dV^T += dO^T P, the transposed operands one k-step ahead of their products
 #pragma unroll
     for (int s = 0; s < BMQ / 16; ++s) {
       __builtin_amdgcn_sched_barrier(0);
       if (s + 1 < BMQ / 16) {
-        if constexpr (DP) read_pd(s + 1);
 #pragma unroll
-        for (int d = 0; d < DB; ++d) top[s + 1][d] = trd.get(tr, d, s + 1);
+        for (int d = 0; d < DB; ++d) top[s + 1][d] = trd.get(gt, d, s + 1);
       }
-      if constexpr (DP) {
+      const bf16x8 pop = acc_kperm_operand(sacc, s);
 #pragma unroll
-        for (int q = 0; q < 2; ++q) {
-          const int g = 2 * (s & 1) + q, mb = s >> 1;
+      for (int d = 0; d < DB; ++d) acc[d] = mfma32(top[s][d], pop, acc[d]);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+  };
+
+  // dP side, one tile (in Q/dO buffer B, its P in hand-over buffer B % 2)
+  auto dp_step = [&](auto bufc, int hq, int m0) __attribute__((always_inline)) {
+    constexpr int B = decltype(bufc)::value;
+    const bf16* const qt = q_lds[B];
+    const bf16* const gt = g_lds[B];
+    rrd.refresh();
+    trd.refresh();
+    f32x16 dacc = f32x16{};
+    // dP = dO V^T
+    constexpr int PF = KS < 4 ? KS : 4;
+    bf16x8 op[KS];
 #pragma unroll
-          for (int e = 0; e < 4; ++e) tacc[mb][4 * g + e] = p4s[s][q][e] * (tacc[mb][4 * g + e] - d4s[s][q][e]);
-        }
+    for (int s = 0; s < PF; ++s) op[s] = rrd.get(gt, s, 0);
+#pragma unroll
+    for (int s = 0; s < KS; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + PF < KS) op[s + PF] = rrd.get(gt, s + PF, 0);
+      dacc = mfma32(op[s], kvf[s], dacc);
+    }
+    __builtin_amdgcn_sched_barrier(0);
+    // dS = P (dP - delta) per k-step (its two register quads), P and delta
+    // and the Q^T operands read one k-step ahead; dK^T += Q^T dS
+    bf16x8 top[BMQ / 16][DB];
+    f32x4 d4s[BMQ / 16][2], p4s[BMQ / 16][2];
+    auto read_pd = [&](int s) __attribute__((always_inline)) {
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int g = 2 * s + q;
+        d4s[s][q] = *reinterpret_cast<const f32x4*>(&stat_lds[B][1][8 * g + 4 * half]);
+        p4s[s][q] = p_lds[B & 1][pair][g][lane];
       }
-      const bf16x8 op = acc_kperm_operand(tacc[s >> 1], s);
-      if constexpr (DP && DS) {
+    };
+    read_pd(0);
+#pragma unroll
+    for (int d = 0; d < DB; ++d) top[0][d] = trd.get(qt, d, 0);
+    bf16* ds_row = nullptr;
+    if constexpr (DS) ds_row = ds_key + hq * ds_head + m0;
+#pragma unroll
+    for (int s = 0; s < BMQ / 16; ++s) {
+      __builtin_amdgcn_sched_barrier(0);
+      if (s + 1 < BMQ / 16) {
+        read_pd(s + 1);
+#pragma unroll
+        for (int d = 0; d < DB; ++d) top[s + 1][d] = trd.get(qt, d, s + 1);
+      }
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int g = 2 * s + q;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) dacc[4 * g + e] = p4s[s][q][e] * (dacc[4 * g + e] - d4s[s][q][e]);
+      }
+      const bf16x8 sop = acc_kperm_operand(dacc, s);
+      if constexpr (DS) {
         // operand element e is query m0 + 16 s + 8 (e / 4) + 4 half + e % 4;
         // swapping dwords with the partner lane (lane ^ 32) gives each lane
         // the 8 queries 16 s + 8 half .. + 7 of its key: one 16-byte store
-        const u32x4 w = __builtin_bit_cast(u32x4, op);
+        const u32x4 w = __builtin_bit_cast(u32x4, sop);
         const auto lo = __builtin_amdgcn_permlane32_swap(w[0], w[2], false, false);
         const auto hi = __builtin_amdgcn_permlane32_swap(w[1], w[3], false, false);
         if (valid_k) *reinterpret_cast<u32x4*>(ds_row + 16 * s) = u32x4{lo[0], hi[0], lo[1], hi[1]};
       }
 #pragma unroll
-      for (int d = 0; d < DB; ++d) acc[d] = mfma32(top[s][d], op, acc[d]);
+      for (int d = 0; d < DB; ++d) acc[d] = mfma32(top[s][d], sop, acc[d]);
     }
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // iteration `it` works on buffer B and prefetches iteration it + 1
-  int hq_cur = hk * group, m_cur = m_first;
-  auto advance = [&](int& hq, int& m0) {
-    m0 += BMQ;
-    if (m0 >= m_end) {
-      m0 = m_first;
-      ++hq;
-    }
-  };
-  auto iteration = [&](auto bufc, auto sidec, int it) __attribute__((always_inline)) {
-    constexpr int B = decltype(bufc)::value;
-    constexpr bool DP = decltype(sidec)::value;
-    const int m0 = m_cur;
-    int hn = hq_cur, mn = m0;
-    advance(hn, mn);
-    // tile `it` has landed; every wave is done with the other buffer and
-    // every dP-side wave has taken the previous P. A dP-side wave that stored
-    // dS in the previous step issued its 4 stores after this tile's loads:
-    // those may still be in flight.
-    if (DS && DP && pair_live && it > 0) {
-      lds_sync<4>();
-    } else {
-      lds_sync<0>();
-    }
-    const bool more = it + 1 < total;
-    if (more) {
-      qrows.issue(a, pb, dma, hn, mn, B ? q_lds0 : q_lds1, B ? g_lds0 : g_lds1);
-      issue_meta(std::integral_constant<int, B ^ 1>{}, hn, mn);
-    }
-    const bool active = pair_live && m0 + BMQ > pair_m_begin;  // uniform over the pair
-    if (active) first_half(bufc, sidec, m0);
-    lds_barrier();  // P of this tile is in LDS
-    if (active) {
-      second_half(bufc, sidec, hq_cur, m0);
-    } else if constexpr (DS && DP) {
-      // the dQ kernel reads every key row of a visited tile: zeros for a
-      // pair that sees none of its rows
-      if (valid_k) {
-        bf16* row = ds_key + hq_cur * ds_head + m0;
-#pragma unroll
-        for (int s = 0; s < BMQ / 16; ++s) *reinterpret_cast<u32x4*>(row + 16 * s) = u32x4{0u, 0u, 0u, 0u};
+  // Step j: the S side takes tile j (buffer j % 4) and issues tile j + 2;
+  // the dP side takes tile j - 1. Steps run j = 0 .. total, one workgroup
+  // barrier each: after it, tile j and P of tile j - 1 are in LDS, and tile
+  // j - 2's buffer (the next prefetch's) is free.
+  if (!dp_side) {
+    Cursor cur{hk * group, m_first}, pf = cur;
+    if (total > 0) issue_tile(std::integral_constant<int, 0>{}, pf);
+    advance(pf);
+    if (total > 1) issue_tile(std::integral_constant<int, 1>{}, pf);
+    advance(pf);
+    lgkm_settle();  // no scalar load of the prologue stays pending into the tile loop
+    auto step = [&](auto bufc, int j) __attribute__((always_inline)) {
+      constexpr int B = decltype(bufc)::value;
+      // tile j has landed (tile j + 1's loads, issued after it, may still fly)
+      if (j + 1 < total) {
+        lds_sync<2 * TileDMA<D, 4, BMQ>::kInstr>();
+      } else {
+        lds_sync<0>();
       }
+      if (j + 2 < total) {
+        issue_tile(std::integral_constant<int, (B + 2) & 3>{}, pf);
+        advance(pf);
+      }
+      if (j < total) {
+        if (active(cur.m0)) s_step(bufc, cur.m0);
+        advance(cur);
+      }
+    };
+    for (int j = 0; j <= total; j += 4) {
+      step(std::integral_constant<int, 0>{}, j);
+      if (j + 1 <= total) step(std::integral_constant<int, 1>{}, j + 1);
+      if (j + 2 <= total) step(std::integral_constant<int, 2>{}, j + 2);
+      if (j + 3 <= total) step(std::integral_constant<int, 3>{}, j + 3);
     }
-    hq_cur = hn;
-    m_cur = mn;
-  };
-
-  if (total > 0) {
-    qrows.issue(a, pb, dma, hq_cur, m_cur, q_lds0, g_lds0);
-    issue_meta(std::integral_constant<int, 0>{}, hq_cur, m_cur);
-  }
-  lgkm_settle();  // no scalar load of the prologue stays pending into the tile loop
-  // one copy of the tile loop per role, so that no role branch sits inside it
-  // (a branch there makes the compiler copy the accumulators at every merge)
-  auto run = [&](auto sidec) __attribute__((always_inline)) {
-    for (int it = 0; it < total; it += 2) {
-      iteration(std::integral_constant<int, 0>{}, sidec, it);
-      if (it + 1 < total) iteration(std::integral_constant<int, 1>{}, sidec, it + 1);
-    }
-  };
-  if (dp_side) {
-    run(std::integral_constant<bool, true>{});
   } else {
-    run(std::integral_constant<bool, false>{});
+    Cursor cur{hk * group, m_first};
+    lgkm_settle();
+    // step j works on tile j - 1 in buffer (j - 1) % 4
+    auto step = [&](auto bufc, int j) __attribute__((always_inline)) {
+      constexpr int B = decltype(bufc)::value;
+      lds_barrier();  // its own LDS reads done; the dS stores keep flying
+      if (j >= 1) {
+        if (active(cur.m0)) {
+          dp_step(bufc, cur.hq, cur.m0);
+        } else if constexpr (DS) {
+          // the dQ kernel reads every key row of a visited tile: zeros for a
+          // pair that sees none of its rows
+          if (valid_k) {
+            bf16* row = ds_key + cur.hq * ds_head + cur.m0;
+#pragma unroll
+            for (int s = 0; s < BMQ / 16; ++s) *reinterpret_cast<u32x4*>(row + 16 * s) = u32x4{0u, 0u, 0u, 0u};
+          }
+        }
+        advance(cur);
+      }
+    };
+    for (int j = 0; j <= total; j += 4) {
+      step(std::integral_constant<int, 3>{}, j);
+      if (j + 1 <= total) step(std::integral_constant<int, 0>{}, j + 1);
+      if (j + 2 <= total) step(std::integral_constant<int, 1>{}, j + 2);
+      if (j + 3 <= total) step(std::integral_constant<int, 2>{}, j + 3);
+    }
   }
 
   if (!valid_k) return;

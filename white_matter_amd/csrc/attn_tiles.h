@@ -276,11 +276,11 @@ __device__ __forceinline__ void issue_key_tile(const KeyTiles<MODE, D, NW>& kt, 
   }
 }
 
-// The query and output-gradient rows of one problem as 64-row LDS tiles (Q
-// and dO share the row addressing), for any query head. Rows past nq read as
-// zeros. Dense rows and varlen segments with consecutive query slots are
+// The query and output-gradient rows of one problem as LDS tiles of ROWS rows
+// (Q and dO share the row addressing), for any query head. Rows past nq read
+// as zeros. Dense rows and varlen segments with consecutive query slots are
 // strided loads; other varlen layouts gather each row.
-template <int MODE, int D, int NW = 4>
+template <int MODE, int D, int NW = 4, int ROWS = kTileRows>
 struct QueryTiles {
   const bf16 *qslice, *gslice;  // slot 0 of the queries' row, head 0
   int64_t qst, gst, qhs, ghs;   // slot and head strides (elements)
@@ -289,7 +289,7 @@ struct QueryTiles {
   int nq;
   bool strided;
 
-  __device__ __forceinline__ void init(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D, NW>& dma) {
+  __device__ __forceinline__ void init(const wmx_attn_args& a, const Problem<MODE>& pb) {
     nq = pb.nq;
     int qb0 = pb.b;
     qfirst = 0;
@@ -309,10 +309,11 @@ struct QueryTiles {
     strided = layout_ok && stride_ok;
   }
 
-  __device__ __forceinline__ void issue(const wmx_attn_args& a, const Problem<MODE>& pb, const TileDMA<D, NW>& dma,
-                                        int hq, int m0, bf16* qtile, bf16* gtile) const {
+  __device__ __forceinline__ void issue(const wmx_attn_args& a, const Problem<MODE>& pb,
+                                        const TileDMA<D, NW, ROWS>& dma, int hq, int m0, bf16* qtile,
+                                        bf16* gtile) const {
     if (strided) {
-      const int nvalid = min(max(nq - m0, 0), kTileRows);
+      const int nvalid = min(max(nq - m0, 0), ROWS);
       const int64_t slot = (int64_t)qfirst + m0;
       const rsrc_t rq = make_rsrc(qslice + hq * qhs + slot * qst, nvalid * (int)qst * 2);
       const rsrc_t rg = make_rsrc(gslice + hq * ghs + slot * gst, nvalid * (int)gst * 2);

@@ -442,16 +442,20 @@ int wmx_decode(const wmx_decode_args* a, void* stream) {
 
 int wmx_decode_noalloc(const wmx_decode_args* a, void* stream) {
   if (const int rc = check_decode(a)) return rc;
-  const int64_t need = wmx::decode_workspace_size(*a);
-  if (need > kDecodeScratchBytes)
-    return fail(WMX_E_WORKSPACE, "decode needs %lld scratch bytes, beyond the %lld-byte static scratch of wmx_decode_noalloc",
-                (long long)need, (long long)kDecodeScratchBytes);
-  if (a->batch == 0 || a->capacity == 0) return WMX_OK;
+  wmx_decode_args b = *a;
+  if (wmx::decode_workspace_size(b) > kDecodeScratchBytes) {
+    // fewer splits, so that their partials fit the scratch (one split needs
+    // none: it writes the output itself)
+    const int64_t per_split = (int64_t)b.batch * b.q_heads * (b.head_dim + 2) * (int64_t)sizeof(float);
+    const int64_t fit = kDecodeScratchBytes / per_split;
+    b.num_splits = (int32_t)(fit < 1 ? 1 : fit);
+  }
+  if (b.batch == 0 || b.capacity == 0) return WMX_OK;
   void* ptr = nullptr;
   if (const int rc = decode_scratch(stream, &ptr)) return rc;
-  wmx_decode_args b = *a;
   b.workspace = ptr;
   b.workspace_bytes = kDecodeScratchBytes;
+  b.counters = nullptr;  // the splits are merged by a second kernel
   return launched(wmx::launch_decode(b, (hipStream_t)stream));
 }
 

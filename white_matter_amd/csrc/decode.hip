@@ -13,9 +13,13 @@
 // UNROLL row groups are in flight per wave. Scores are dot products on the
 // VALU (arithmetic intensity ~2G flop/byte, far below the MFMA ridge).
 // K/V rows are read with nontemporal loads (streamed once). Each split writes
-// an unnormalised (o, max, sum) partial; a second kernel merges the splits in
-// log-sum-exp form and writes bf16 output. A single split writes its output
-// itself.
+// an unnormalised (o, max, sum) partial, merged in log-sum-exp form into the
+// bf16 output either by the last split of its (row, KV head) to finish (with
+// the caller's counters: a vector-memory atomic counts the finished splits,
+// the last one merges every split's partial in split order and resets the
+// counter) or by a second kernel (without). Both merges add the same terms in
+// the same order, so the outputs are bit-identical. A single split writes its
+// output itself.
 #include <climits>
 
 #include "wmx_kernels.h"
@@ -23,6 +27,19 @@
 namespace wmx {
 
 constexpr int kDecodeChunkMin = 256;
+// With counters, launches of at most kDecodeMergeBlocks workgroups (four per
+// CU) and at most kDecodeMergeSplits splits merge in the last split to
+// finish: there a second kernel's launch and tail are most of the merge's
+// cost (the C5 decode loop: 0.313 -> 0.289 ms per token). Larger launches keep
+// the combine kernel: the atomic round trip at the end of each of their many
+// workgroups costs more (C4 decode, 4096 workgroups: 0.177 -> 0.19 ms).
+constexpr int kDecodeMergeSplits = 64;
+constexpr int64_t kDecodeMergeBlocks = 4 * 256;
+
+bool decode_merges_in_split(const wmx_decode_args& a, int nsplit) {
+  return a.counters && nsplit > 1 && nsplit <= kDecodeMergeSplits &&
+         (int64_t)nsplit * a.batch * a.kv_heads <= kDecodeMergeBlocks;
+}
 
 struct DecodeLen {
   int64_t len;        // keys j < len may be visible
@@ -47,10 +64,41 @@ __device__ __forceinline__ DecodeLen decode_len(const wmx_decode_args& a, int b)
   return r;
 }
 
+// Partials that another workgroup may merge in the same launch are written
+// and read with agent-coherent accesses (relaxed agent-scope atomics: the
+// sc1 forms of global_store / global_load), which reach the point where all
+// XCDs' accesses meet without writing back or invalidating whole L2 caches.
+__device__ __forceinline__ void store_partial(float* p, float v, bool shared) {
+  if (shared) {
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  } else {
+    *p = v;  // read by the combine kernel after this launch
+  }
+}
+__device__ __forceinline__ float load_shared(const float* p) {
+  return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Merge the nsplit partials of query head h of row b in split order (the
+// log-sum-exp form of decode_combine_kernel) into output element d.
+__device__ __forceinline__ float merge_splits(const float* ws_o, const float* ws_ml, int64_t prow0, int nsplit, int D,
+                                              int d) {
+  float mx = kMaxFloor;
+  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ws_ml[(prow0 + s) * 2]);
+  float lsum = 0.f, acc = 0.f;
+  for (int s = 0; s < nsplit; ++s) {
+    const float w = __builtin_amdgcn_exp2f(ws_ml[(prow0 + s) * 2] - mx);
+    lsum += ws_ml[(prow0 + s) * 2 + 1] * w;
+    acc += ws_o[(prow0 + s) * D + d] * w;
+  }
+  return lsum > 0.f ? acc / lsum : 0.f;
+}
+
 // G query heads of one KV head per workgroup, from head head_offset of the
 // KV head's group on (groups of more than 8 heads run in several launches)
 template <int D, int G>
-__global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args a, int chunk, int head_offset) {
+__global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args a, int chunk, int head_offset,
+                                                            int32_t* counters) {
   constexpr int LPR = D <= 64 ? 8 : 16;   // lanes per key row
   constexpr int RPW = 64 / LPR;           // rows per wave load
   // key rows in flight per lane: eight for one head; four for a head group,
@@ -221,7 +269,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
 #pragma unroll
     for (int w = 0; w < 4; ++w) acc += lds_o[w][g][d] * __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
     const int64_t prow = ((int64_t)b * a.q_heads + h0 + g) * nsplit + split;
-    ws_o[prow * D + d] = acc;
+    store_partial(ws_o + prow * D + d, acc, counters != nullptr);
     if (d == 0) {
       float lsum = 0.f, mraw = kNegInf;
 #pragma unroll
@@ -229,31 +277,66 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
         lsum += lds_l[w][g] * __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
         mraw = fmaxf(mraw, lds_m[w][g]);
       }
-      ws_ml[prow * 2 + 0] = mraw == kNegInf ? kNegInf : mx;
-      ws_ml[prow * 2 + 1] = lsum;
+      store_partial(ws_ml + prow * 2 + 0, mraw == kNegInf ? kNegInf : mx, counters != nullptr);
+      store_partial(ws_ml + prow * 2 + 1, lsum, counters != nullptr);
     }
   }
+  if (!counters) return;  // decode_combine_kernel merges the splits
+  // The last split of (b, hk) to finish merges them all. Every thread waits
+  // until its coherent partial stores have completed, the workgroup meets,
+  // and one lane counts this split with a vector-memory atomic; the split
+  // that sees nsplit - 1 earlier counts reads every split's partial with
+  // coherent loads, merges, and resets the counter for the next launch.
+  __shared__ int last_lds;
+  __shared__ float ml_lds[G][kDecodeMergeSplits][2];
+  __builtin_amdgcn_s_waitcnt(0);  // vmcnt(0) expcnt(0) lgkmcnt(0): the partial stores have landed
+  __syncthreads();
+  if (tid == 0) last_lds = atomicAdd(counters + pair, 1) == nsplit - 1;
+  __syncthreads();
+  if (!last_lds) return;
+  // every split's (max, sum) of the G heads into LDS with all loads in
+  // flight at once, then each thread's output elements from 8 splits' rows
+  // at a time: the same terms in the same order as merge_splits
+  const int64_t head0 = ((int64_t)b * a.q_heads + h0) * nsplit;  // partial row of (h0, split 0)
+  for (int i = tid; i < G * nsplit * 2; i += 256) {
+    const int g = i / (nsplit * 2), r = i - g * nsplit * 2;
+    (&ml_lds[g][0][0])[r] = load_shared(ws_ml + (head0 + (int64_t)g * nsplit) * 2 + r);
+  }
+  __syncthreads();
+  for (int idx = tid; idx < G * D; idx += 256) {
+    const int g = idx / D, d = idx % D;
+    const float* orow = ws_o + (head0 + (int64_t)g * nsplit) * D + d;
+    float mx = kMaxFloor;
+    for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ml_lds[g][s][0]);
+    float lsum = 0.f, acc = 0.f;
+    for (int s0 = 0; s0 < nsplit; s0 += 8) {
+      float ov[8];
+#pragma unroll
+      for (int u = 0; u < 8; ++u) ov[u] = s0 + u < nsplit ? load_shared(orow + (int64_t)(s0 + u) * D) : 0.f;
+#pragma unroll
+      for (int u = 0; u < 8; ++u) {
+        if (s0 + u < nsplit) {
+          const float w = __builtin_amdgcn_exp2f(ml_lds[g][s0 + u][0] - mx);
+          lsum += ml_lds[g][s0 + u][1] * w;
+          acc += ov[u] * w;
+        }
+      }
+    }
+    const float r = lsum > 0.f ? acc / lsum : 0.f;
+    ((bf16*)a.o)[(int64_t)b * a.o_stride[0] + (int64_t)(h0 + g) * a.o_stride[1] + d] = (__bf16)r;
+  }
+  if (tid == 0) __hip_atomic_store(counters + pair, 0, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
 // One workgroup of D threads per (b, query head): merge the splits.
 __global__ void decode_combine_kernel(const wmx_decode_args a, int nsplit) {
   const int D = a.head_dim;
   const int h = blockIdx.x, b = blockIdx.y, d = threadIdx.x;
+  if (d >= D) return;
   const float* ws_o = (const float*)a.workspace;
   const float* ws_ml = ws_o + (int64_t)a.batch * a.q_heads * nsplit * D;
-  const int64_t prow0 = ((int64_t)b * a.q_heads + h) * nsplit;
-  float mx = kMaxFloor;
-  for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ws_ml[(prow0 + s) * 2]);
-  float lsum = 0.f, acc = 0.f;
-  for (int s = 0; s < nsplit; ++s) {
-    const float w = __builtin_amdgcn_exp2f(ws_ml[(prow0 + s) * 2] - mx);
-    lsum += ws_ml[(prow0 + s) * 2 + 1] * w;
-    if (d < D) acc += ws_o[(prow0 + s) * D + d] * w;
-  }
-  if (d < D) {
-    const float r = lsum > 0.f ? acc / lsum : 0.f;
-    ((bf16*)a.o)[(int64_t)b * a.o_stride[0] + (int64_t)h * a.o_stride[1] + d] = (__bf16)r;
-  }
+  const float r = merge_splits(ws_o, ws_ml, ((int64_t)b * a.q_heads + h) * nsplit, nsplit, D, d);
+  ((bf16*)a.o)[(int64_t)b * a.o_stride[0] + (int64_t)h * a.o_stride[1] + d] = (__bf16)r;
 }
 
 int decode_num_splits(const wmx_decode_args& a) {
@@ -279,7 +362,9 @@ int64_t decode_workspace_size(const wmx_decode_args& a) {
 template <int D, int G>
 static void launch_decode_t(const wmx_decode_args& a, int nsplit, int chunk, int head_offset, hipStream_t stream) {
   const int64_t blocks = (int64_t)nsplit * a.batch * a.kv_heads;  // <= INT32_MAX (checked by the caller)
-  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3((unsigned)blocks), dim3(256), 0, stream, a, chunk, head_offset);
+  int32_t* counters = decode_merges_in_split(a, nsplit) ? a.counters : nullptr;
+  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3((unsigned)blocks), dim3(256), 0, stream, a, chunk, head_offset,
+                     counters);
 }
 
 // Any group size: up to 8 query heads share one read of each K/V row; larger
@@ -317,7 +402,7 @@ int launch_decode(const wmx_decode_args& a, hipStream_t stream) {
     default: return WMX_E_UNSUPPORTED;
   }
   if (rc != WMX_OK) return rc;
-  if (nsplit == 1) return WMX_OK;  // the split kernel wrote the output
+  if (nsplit == 1 || decode_merges_in_split(a, nsplit)) return WMX_OK;  // the split kernel wrote the output
   const int threads = (a.head_dim + 63) / 64 * 64;
   hipLaunchKernelGGL(decode_combine_kernel, dim3(a.q_heads, a.batch), dim3(threads), 0, stream, a, nsplit);
   return WMX_OK;

@@ -147,12 +147,13 @@ __device__ __forceinline__ void lgkm_settle() {
   __asm__ volatile("" ::: "memory");
 }
 
-// This thread's 16-byte slots of a 64-row tile filled by NW waves: each wave
-// fills 64 / NW rows with 16 / NW instructions of 4 rows.
-template <int D, int NW = 4>
+// This thread's 16-byte slots of a ROWS-row tile (64, or the first 32 rows of
+// the same layout) filled by NW waves: each wave fills ROWS / NW rows with
+// ROWS / (4 NW) instructions of 4 rows.
+template <int D, int NW = 4, int ROWS = kTileRows>
 struct TileDMA {
-  static constexpr int kInstr = 16 / NW;  // instructions per wave per tile
-  static_assert(NW == 4 || NW == 8, "4 or 8 waves fill a tile");
+  static constexpr int kInstr = ROWS / (4 * NW);  // instructions per wave per tile
+  static_assert((NW == 4 || NW == 8) && (ROWS == 32 || ROWS == 64) && kInstr >= 1, "4 or 8 waves fill a tile");
   // Instruction r of wave w fills tile row 4 g + sub, g = kInstr w + r and
   // sub = lane / 16, whose swizzle is 4 sub + g % 4: the lane loads logical
   // chunk lc0 ^ (g % 4) with lc0 = (lane % 16) ^ 4 sub. Only these values are
@@ -173,7 +174,7 @@ struct TileDMA {
   }
   __device__ __forceinline__ lds_void* dst(bf16* tile, int r) const { return (lds_void*)(tile + group(r) * 512); }
   // Per-lane byte offset of instruction r of a strided tile with row stride
-  // row_bytes (0 <= row_bytes * 64 < 2^31).
+  // row_bytes (0 <= row_bytes * ROWS < 2^31).
   __device__ __forceinline__ unsigned strided_offset(int r, int row_bytes) const {
     const int c = chunk16(r);
     return c < 0 ? kOutOfRange : (unsigned)(row(r) * row_bytes + c);

@@ -30,8 +30,11 @@
 #include <cmath>
 #include <cstring>
 #include <list>
+#include <map>
 #include <memory>
 #include <mutex>
+#include <utility>
+#include <vector>
 
 #include "wmx_attn.h"
 
@@ -768,6 +771,25 @@ std::tuple<Tensor, Tensor, Tensor> strict_dense_bwd(const Tensor& query, const T
   return {dq, dk, dv};
 }
 
+// The split-merge counters of wmx_decode per (device, stream): zero when
+// created, left zero by every launch (the last split of a (row, KV head)
+// resets its counter), so calls in order on one stream share them. Buffers are
+// kept for the life of the process, also when a larger one replaces them: a
+// captured graph may hold their addresses.
+struct DecodeCounters {
+  std::mutex mutex;
+  std::map<std::pair<int, hipStream_t>, std::vector<Tensor>> by_stream;
+
+  int32_t* get(const Tensor& like, hipStream_t stream, int64_t count) {
+    std::lock_guard<std::mutex> lock(mutex);
+    auto& kept = by_stream[{(int)like.get_device(), stream}];
+    if (kept.empty() || kept.back().numel() < count)
+      kept.push_back(at::zeros({std::max<int64_t>(count, 4096)}, like.options().dtype(at::kInt)));
+    return kept.back().data_ptr<int32_t>();
+  }
+};
+DecodeCounters g_decode_counters;
+
 Tensor strict_decode(const Tensor& query, const Tensor& key, const Tensor& value,
                      const c10::optional<Tensor>& query_start, int64_t query_start_value,
                      const c10::optional<Tensor>& kv_lengths, const c10::optional<Tensor>& key_mask, bool use_dummy,
@@ -815,6 +837,7 @@ Tensor strict_decode(const Tensor& query, const Tensor& key, const Tensor& value
   a.use_dummy = use_dummy ? 1 : 0;
   a.num_splits = (int32_t)num_splits;
   a.softmax_scale = (float)scale;
+  a.counters = g_decode_counters.get(q, stream_of(q), batch * k.size(1));
   const int64_t need = wmx_decode_workspace_size(&a);
   Tensor workspace = at::empty({std::max<int64_t>(need, 16)}, q.options().dtype(at::kByte));
   a.workspace = workspace.data_ptr();

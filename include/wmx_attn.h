@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 9
+#define WMX_ABI_VERSION 10
 
 enum {
   WMX_OK = 0,
@@ -160,6 +160,10 @@ typedef struct wmx_attn_args {
    * 1, slot 1 being slot 0 + 1 for a one-element side; the dS offset is
    * ds_offsets[segment] as two int32 halves). */
   int32_t unit_fields;
+  /* dK/dV key rows per workgroup: 0 or 128 (eight waves, one workgroup per
+   * CU), or 64 (four waves, two workgroups per CU: one workgroup's setup
+   * overlaps the other's tile loop). k_units tiles count in these rows. */
+  int32_t key_tile;
 } wmx_attn_args;
 
 enum {

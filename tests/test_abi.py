@@ -47,6 +47,10 @@ def test_argument_checks_return_errors_without_launching():
     assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -1
     assert b"kv_heads" in lib.wmx_last_error()
     args.q_heads = 4
+    args.key_tile = 32  # dK/dV workgroups take 64 or 128 keys
+    assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -1
+    assert b"key_tile" in lib.wmx_last_error()
+    args.key_tile = 64
     assert lib.wmx_attn_fwd(ctypes.byref(args), None) == -2
     assert b"softmax_scale" in lib.wmx_last_error()
     args.softmax_scale = 0.125

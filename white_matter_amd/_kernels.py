@@ -89,6 +89,7 @@ class Varlen:
     k_units: torch.Tensor | None = None  # key tiles
     ds_offsets: torch.Tensor | None = None  # int64 (num_segments + 1) dS block offsets (see wmx_attn.h)
     ds_elements: int = 0  # ds_offsets[-1]
+    key_tile: int = 0  # keys per dK/dV workgroup: 0/128, or 64 (k_units then count 64-key tiles)
 
 
 @dataclass
@@ -143,6 +144,7 @@ class Visibility:
             args.unit_fields = widths.pop() if widths else 0
             if s.ds_offsets is not None:
                 args.ds_offsets, args.ds_elements = s.ds_offsets.data_ptr(), s.ds_elements
+            args.key_tile = s.key_tile
 
 
 QUERY_TILE = 128  # query rows per forward / dQ workgroup

@@ -19,7 +19,7 @@ import torch
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
 # the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
 OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -85,6 +85,7 @@ class AttnArgs(ctypes.Structure):
         ("ds_elements", ctypes.c_int64),
         ("query_tile", ctypes.c_int32),
         ("unit_fields", ctypes.c_int32),
+        ("key_tile", ctypes.c_int32),
     ]
 
 

@@ -31,11 +31,6 @@
 
 namespace wmx {
 
-// Segment grp's dS block offset: from its work-list entry when it has one.
-__device__ __forceinline__ int64_t ds_offset_of(const wmx_attn_args& a, int grp, const TileUnit& tu) {
-  return tu.has_fields ? tu.ds_off : a.ds_offsets[grp];
-}
-
 // ---------------------------------------------------------------- delta ----
 // 16 lanes per row, 8 elements per lane; a thread takes kDeltaRows rows (16
 // apart) with all their loads issued before any is used, so each thread has
@@ -485,41 +480,50 @@ __global__ __launch_bounds__(256, 2) void attn_bwd_dq_ds_kernel(const wmx_attn_a
 }
 
 // ------------------------------------------------------------------ dKV ----
-// One workgroup = 128 keys of one (batch row or segment, kv head) and eight
-// waves: wave pair p (waves p and p + 4, which share SIMD p) owns keys
-// 32p .. 32p + 31. The pair splits the work so each wave holds half of the
-// state:
+// One workgroup = 32 NP keys of one (batch row or segment, kv head) and 2 NP
+// waves: wave pair p (waves p and p + NP) owns keys 32p .. 32p + 31. NP = 4:
+// 128 keys, eight waves, one workgroup per CU (a pair shares SIMD p); NP = 2:
+// 64 keys, four waves, two workgroups per CU, so that one workgroup's setup
+// (its unit's bounds, K/V rows and first query tiles) overlaps the other's
+// tile loop. The pair splits the work so each wave holds half of the state:
 //   wave p     ("S side")  holds K rows, computes S = Q K^T, the mask and
 //              P = exp2(S c log2e - lse), hands P to its partner through LDS
 //              and accumulates dV^T = dO^T P;
 //   wave p + 4 ("dP side") holds V rows, computes dP = dO V^T, takes P and
 //              forms dS = P (dP - delta), and accumulates dK^T = Q^T dS.
 // Query and output-gradient tiles of 32 rows for every query head of the
-// group stream through four LDS buffers (direct-to-LDS loads issued by the S
-// side two tiles ahead); each tile is read row-wise for S and dP and by
-// transpose reads for dV and dK. The dP side works one tile behind the S
-// side: in step j the S side takes tile j and the dP side tile j - 1, whose P
-// the S side left in the other of two hand-over buffers in step j - 1. The
-// two waves of a SIMD then never wait for each other inside a step (one
-// workgroup barrier per step), and one's matrix products overlap the other's
-// vector work.
-template <int D, int MODE, bool ATOMIC, bool DS>
-__global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args args) {
+// group stream through four LDS buffers with NP = 4 (direct-to-LDS loads
+// issued by the S side two tiles ahead), three with NP = 2 (one tile ahead);
+// each tile is read row-wise for S and dP and by transpose reads for dV and
+// dK. The dP side works one tile behind the S side: in step j the S side
+// takes tile j and the dP side tile j - 1, whose P the S side left in that
+// tile's hand-over buffer in step j - 1. The two waves of a pair then never
+// wait for each other inside a step (one workgroup barrier per step), and
+// one's matrix products overlap the other's vector work.
+template <int D, int MODE, bool ATOMIC, bool DS, int NP>
+__global__ __launch_bounds__(128 * NP, NP == 2 ? 2 : 1) void attn_bwd_dkv_kernel(const wmx_attn_args args) {
   const wmx_attn_args& a = args;
-  constexpr int BNK = 128, BMQ = 32, NW = 8;
+  static_assert(NP == 2 || NP == 4, "two or four wave pairs");
+  constexpr int BNK = 32 * NP, BMQ = 32, NW = 2 * NP;
+  // Q/dO tile buffers, and P hand-over buffers (one per tile buffer): NBUF - 2
+  // tiles are loaded ahead of the S side's (the dP side holds the one
+  // behind). Four for eight waves (two tiles ahead); three for four waves,
+  // whose LDS then fits twice per CU (one tile ahead: the other workgroup
+  // covers the wait).
+  constexpr int NBUF = NP == 4 ? 4 : 3, DIST = NBUF - 2;
   constexpr int KS = D / 16, DB = D / 32;
   constexpr int kTile32 = BMQ * kRowElems;  // 8 KB: the first 32 rows of the tile layout
-  // four buffers indexed by compile-time constants only (the loop is
-  // unrolled by four): prefetches into one buffer are then known not to alias
-  // reads of the others, so reads never wait for the prefetch
-  __shared__ __attribute__((aligned(1024))) bf16 q_lds[4][kTile32];
-  __shared__ __attribute__((aligned(1024))) bf16 g_lds[4][kTile32];
-  // P of tile t from the S side to the dP side: [t % 2][pair][register quad][lane]
-  __shared__ __attribute__((aligned(16))) f32x4 p_lds[2][4][4][64];
+  // buffers indexed by compile-time constants only (the loop is unrolled by
+  // NBUF): prefetches into one buffer are then known not to alias reads of
+  // the others, so reads never wait for the prefetch
+  __shared__ __attribute__((aligned(1024))) bf16 q_lds[NBUF][kTile32];
+  __shared__ __attribute__((aligned(1024))) bf16 g_lds[NBUF][kTile32];
+  // P of tile t from the S side to the dP side: [t % NBUF][pair][register quad][lane]
+  __shared__ __attribute__((aligned(16))) f32x4 p_lds[NBUF][NP][4][64];
   // lse, delta, document id and start of the tile's rows (entries past BMQ:
   // the 4-byte direct-to-LDS loads of lanes 32 .. 63, never read)
-  __shared__ __attribute__((aligned(16))) float stat_lds[4][2][64];
-  __shared__ __attribute__((aligned(16))) int qdoc_lds[4][2][64];
+  __shared__ __attribute__((aligned(16))) float stat_lds[NBUF][2][64];
+  __shared__ __attribute__((aligned(16))) int qdoc_lds[NBUF][2][64];
   __shared__ int red_lds[NW];
   // per key of the workgroup: first query row that sees it, document id,
   // document query end (kept in LDS rather than in registers)
@@ -539,8 +543,8 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   if (!tu.ok) return;
   const int tid = threadIdx.x, lane = tid & 63, wave = wave_id();
   const int half = lane >> 5, col = lane & 31;
-  const int pair = wave & 3;
-  const bool dp_side = wave >= 4;  // wave-uniform role
+  const int pair = wave & (NP - 1);
+  const bool dp_side = wave >= NP;  // wave-uniform role
   const int n0 = tu.tile * BNK;
   const int hk = tu.head, grp = tu.grp;
   Problem<MODE> pb;
@@ -618,10 +622,10 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
   const int m_first = (m_begin / BMQ) * BMQ;
   const int nqt = m_end > m_first ? (m_end - m_first + BMQ - 1) / BMQ : 0;
   const int total = nqt * group;
-  // the four S-side waves load every tile
-  TileDMA<D, 4, BMQ> dma;
+  // the S-side waves load every tile
+  TileDMA<D, NP, BMQ> dma;
   dma.init(pair, lane);
-  QueryTiles<MODE, D, 4, BMQ> qrows;
+  QueryTiles<MODE, D, NP, BMQ> qrows;
   qrows.init(a, pb);
   RowReads<KS> rrd;
   rrd.init(col, half);
@@ -769,7 +773,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
         p4[e] = __builtin_amdgcn_exp2f(fmaf(sacc[4 * g + e], sl2, -l4[e] * kLog2e));
         sacc[4 * g + e] = p4[e];
       }
-      p_lds[B & 1][pair][g][lane] = p4;
+      p_lds[B][pair][g][lane] = p4;
     }
     // dV^T += dO^T P, the transposed operands one k-step ahead of their products
 #pragma unroll
@@ -815,7 +819,7 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
       for (int q = 0; q < 2; ++q) {
         const int g = 2 * s + q;
         d4s[s][q] = *reinterpret_cast<const f32x4*>(&stat_lds[B][1][8 * g + 4 * half]);
-        p4s[s][q] = p_lds[B & 1][pair][g][lane];
+        p4s[s][q] = p_lds[B][pair][g][lane];
       }
     };
     read_pd(0);
@@ -853,27 +857,35 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
     __builtin_amdgcn_sched_barrier(0);
   };
 
-  // Step j: the S side takes tile j (buffer j % 4) and issues tile j + 2;
-  // the dP side takes tile j - 1. Steps run j = 0 .. total, one workgroup
-  // barrier each: after it, tile j and P of tile j - 1 are in LDS, and tile
-  // j - 2's buffer (the next prefetch's) is free.
+  // Step j: the S side takes tile j (buffer j % NBUF) and issues tile
+  // j + DIST; the dP side takes tile j - 1. Steps run j = 0 .. total, one
+  // workgroup barrier each: after it, tile j and P of tile j - 1 are in LDS,
+  // and the buffer of tile j + DIST (last read for tile j + DIST - NBUF =
+  // j - 2) is free.
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, NBUF - 1>;  // the last buffer (3 or 2)
   if (!dp_side) {
     Cursor cur{hk * group, m_first}, pf = cur;
-    if (total > 0) issue_tile(std::integral_constant<int, 0>{}, pf);
+    if (total > 0) issue_tile(I0{}, pf);
     advance(pf);
-    if (total > 1) issue_tile(std::integral_constant<int, 1>{}, pf);
-    advance(pf);
+    if constexpr (DIST > 1) {
+      if (total > 1) issue_tile(I1{}, pf);
+      advance(pf);
+    }
     lgkm_settle();  // no scalar load of the prologue stays pending into the tile loop
     auto step = [&](auto bufc, int j) __attribute__((always_inline)) {
       constexpr int B = decltype(bufc)::value;
-      // tile j has landed (tile j + 1's loads, issued after it, may still fly)
-      if (j + 1 < total) {
-        lds_sync<2 * TileDMA<D, 4, BMQ>::kInstr>();
+      // tile j has landed (with two tiles ahead, tile j + 1's loads, issued
+      // after it, may still fly)
+      if (DIST > 1 && j + 1 < total) {
+        lds_sync<2 * TileDMA<D, NP, BMQ>::kInstr>();
       } else {
         lds_sync<0>();
       }
-      if (j + 2 < total) {
-        issue_tile(std::integral_constant<int, (B + 2) & 3>{}, pf);
+      if (j + DIST < total) {
+        issue_tile(std::integral_constant<int, (B + DIST) % NBUF>{}, pf);
         advance(pf);
       }
       if (j < total) {
@@ -881,16 +893,18 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
         advance(cur);
       }
     };
-    for (int j = 0; j <= total; j += 4) {
-      step(std::integral_constant<int, 0>{}, j);
-      if (j + 1 <= total) step(std::integral_constant<int, 1>{}, j + 1);
-      if (j + 2 <= total) step(std::integral_constant<int, 2>{}, j + 2);
-      if (j + 3 <= total) step(std::integral_constant<int, 3>{}, j + 3);
+    for (int j = 0; j <= total; j += NBUF) {
+      step(I0{}, j);
+      if (j + 1 <= total) step(I1{}, j + 1);
+      if (j + 2 <= total) step(I2{}, j + 2);
+      if constexpr (NBUF == 4) {
+        if (j + 3 <= total) step(I3{}, j + 3);
+      }
     }
   } else {
     Cursor cur{hk * group, m_first};
     lgkm_settle();
-    // step j works on tile j - 1 in buffer (j - 1) % 4
+    // step j works on tile j - 1 in buffer (j - 1) % NBUF
     auto step = [&](auto bufc, int j) __attribute__((always_inline)) {
       constexpr int B = decltype(bufc)::value;
       lds_barrier();  // its own LDS reads done; the dS stores keep flying
@@ -909,11 +923,13 @@ __global__ __launch_bounds__(512) void attn_bwd_dkv_kernel(const wmx_attn_args a
         advance(cur);
       }
     };
-    for (int j = 0; j <= total; j += 4) {
-      step(std::integral_constant<int, 3>{}, j);
-      if (j + 1 <= total) step(std::integral_constant<int, 0>{}, j + 1);
-      if (j + 2 <= total) step(std::integral_constant<int, 1>{}, j + 2);
-      if (j + 3 <= total) step(std::integral_constant<int, 2>{}, j + 3);
+    for (int j = 0; j <= total; j += NBUF) {
+      step(I3{}, j);
+      if (j + 1 <= total) step(I0{}, j + 1);
+      if (j + 2 <= total) step(I1{}, j + 2);
+      if constexpr (NBUF == 4) {
+        if (j + 3 <= total) step(I2{}, j + 3);
+      }
     }
   }
 
@@ -1094,12 +1110,17 @@ static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
 
 template <int D, int MODE, bool ATOMIC, bool DS>
 static void launch_dkv_kernel(const wmx_attn_args& a, dim3 grid, hipStream_t stream) {
-  hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, ATOMIC, DS>), grid, dim3(512), 0, stream, a);
+  if (a.key_tile == 64) {
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, ATOMIC, DS, 2>), grid, dim3(256), 0, stream, a);
+  } else {
+    hipLaunchKernelGGL((attn_bwd_dkv_kernel<D, MODE, ATOMIC, DS, 4>), grid, dim3(512), 0, stream, a);
+  }
 }
 
 template <int D, int MODE>
 static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
-  const int64_t ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + 127) / 128;
+  const int bnk = a.key_tile == 64 ? 64 : 128;
+  const int64_t ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + bnk - 1) / bnk;
   const int64_t per_head =
       (MODE == kVarlen && a.k_units) ? a.num_k_units : ktiles * (MODE == kVarlen ? a.num_segments : a.batch);
   const int64_t units = per_head * a.kv_heads;
@@ -1175,20 +1196,24 @@ int launch_bwd(const wmx_attn_args& a, hipStream_t stream) {
 // finds its host stub even where the compiler would not emit one for an
 // instantiation first seen next to a branch it folds away.
 namespace wmx {
+#define WMX_DKV_KERNELS(D, M, A, S)                                                 \
+  template __global__ void attn_bwd_dkv_kernel<D, M, A, S, 2>(const wmx_attn_args); \
+  template __global__ void attn_bwd_dkv_kernel<D, M, A, S, 4>(const wmx_attn_args);
 #define WMX_BWD_KERNELS_MODE(D, M)                                                 \
   template __global__ void attn_bwd_dq_kernel<D, M>(const wmx_attn_args);          \
   template __global__ void attn_bwd_dq_ds_kernel<D, M>(const wmx_attn_args);       \
-  template __global__ void attn_bwd_dkv_kernel<D, M, false, false>(const wmx_attn_args); \
-  template __global__ void attn_bwd_dkv_kernel<D, M, false, true>(const wmx_attn_args);
+  WMX_DKV_KERNELS(D, M, false, false)                                              \
+  WMX_DKV_KERNELS(D, M, false, true)
 #define WMX_BWD_KERNELS(D)                                                          \
   WMX_BWD_KERNELS_MODE(D, kDense)                                                   \
   WMX_BWD_KERNELS_MODE(D, kDoc)                                                     \
   WMX_BWD_KERNELS_MODE(D, kVarlen)                                                  \
-  template __global__ void attn_bwd_dkv_kernel<D, kVarlen, true, false>(const wmx_attn_args); \
-  template __global__ void attn_bwd_dkv_kernel<D, kVarlen, true, true>(const wmx_attn_args);
+  WMX_DKV_KERNELS(D, kVarlen, true, false)                                        \
+  WMX_DKV_KERNELS(D, kVarlen, true, true)
 WMX_BWD_KERNELS(64)
 WMX_BWD_KERNELS(96)
 WMX_BWD_KERNELS(128)
 #undef WMX_BWD_KERNELS
 #undef WMX_BWD_KERNELS_MODE
+#undef WMX_DKV_KERNELS
 }  // namespace wmx

@@ -42,8 +42,13 @@ struct TileUnit {
   // fields: ints per list entry (2, or WMX_UNIT_FIELDS)
   __device__ __forceinline__ void decode(int heads, uint32_t count, bool unit_major, int tiles,
                                          const int32_t* list, int num_groups, bool descending, int fields = 2) {
+    decode_at(blockIdx.x, heads, count, unit_major, tiles, list, num_groups, descending, fields);
+  }
+  // The same for logical block index b (a persistent grid's units).
+  __device__ __forceinline__ void decode_at(uint32_t b, int heads, uint32_t count, bool unit_major, int tiles,
+                                            const int32_t* list, int num_groups, bool descending, int fields = 2) {
     has_fields = false;
-    const uint32_t b = blockIdx.x, nh = (uint32_t)heads;
+    const uint32_t nh = (uint32_t)heads;
     uint32_t u;
     if ((nh & 7u) == 0) {
       const uint32_t hpx = nh >> 3, x = b & 7u, s = b >> 3;
@@ -136,9 +141,11 @@ struct Problem {
           krows.set(a.key_indices + tu.ks, a.key_extent, a.segment_layout & kKeysConsecutive,
                     a.segment_layout & kKeysOneRow, true, tu.krow, tu.kslot0, tu.kslot1);
       } else {
-        const int qs = a.cu_queries[grp], ks = a.cu_keys[grp];
-        nq = a.cu_queries[grp + 1] - qs;
-        nk = a.cu_keys[grp + 1] - ks;
+        // one address for the whole wave: uniform values, kept in scalar registers
+        const int qs = __builtin_amdgcn_readfirstlane(a.cu_queries[grp]);
+        const int ks = __builtin_amdgcn_readfirstlane(a.cu_keys[grp]);
+        nq = __builtin_amdgcn_readfirstlane(a.cu_queries[grp + 1]) - qs;
+        nk = __builtin_amdgcn_readfirstlane(a.cu_keys[grp + 1]) - ks;
         if (nq > 0)
           qrows.init(a.query_indices + qs, nq, a.query_extent, a.segment_layout & kQueriesConsecutive,
                      a.segment_layout & kQueriesOneRow, false);
@@ -152,8 +159,8 @@ struct Problem {
     } else {
       nq = a.q_len;
       nk = a.kv_len;
-      bound = Bounds{a.row_offset ? a.row_offset[b] : a.query_offset, a.row_limit ? a.row_limit[b] : INT_MAX,
-                     a.query_stride, nk};
+      bound = Bounds{a.row_offset ? __builtin_amdgcn_readfirstlane(a.row_offset[b]) : a.query_offset,
+                     a.row_limit ? __builtin_amdgcn_readfirstlane(a.row_limit[b]) : INT_MAX, a.query_stride, nk};
     }
   }
   // (row, slot) of query row i and key row j (both must be in range)
@@ -174,6 +181,11 @@ struct Problem {
     }
   }
 };
+
+// Segment grp's dS block offset: from its work-list entry when it has one.
+__device__ __forceinline__ int64_t ds_offset_of(const wmx_attn_args& a, int grp, const TileUnit& tu) {
+  return tu.has_fields ? tu.ds_off : a.ds_offsets[grp];
+}
 
 __device__ __forceinline__ const bf16* row_at(const void* base, const int64_t* st, int b, int h, int t) {
   return (const bf16*)base + (int64_t)b * st[0] + (int64_t)h * st[1] + (int64_t)t * st[2];

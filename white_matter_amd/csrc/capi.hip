@@ -50,6 +50,8 @@ int check_common(const wmx_attn_args* a, bool backward) {
   if (a->query_stride < 1) return fail(WMX_E_INVALID, "query_stride must be >= 1");
   if (a->query_tile != 0 && a->query_tile != 128 && a->query_tile != 256)
     return fail(WMX_E_INVALID, "query_tile must be 0, 128 or 256");
+  if (a->key_tile != 0 && a->key_tile != 64 && a->key_tile != 128)
+    return fail(WMX_E_INVALID, "key_tile must be 0, 64 or 128");
   if (!(a->softmax_scale > 0.f)) return fail(WMX_E_UNSUPPORTED, "softmax_scale must be positive and finite");
   if (!a->q || !a->k || !a->v || !a->o || !a->lse) return fail(WMX_E_INVALID, "q/k/v/o/lse pointer is NULL");
   if (!aligned16(a->q) || !aligned16(a->k) || !aligned16(a->v))

@@ -153,7 +153,8 @@ __device__ __forceinline__ void lgkm_settle() {
 template <int D, int NW = 4, int ROWS = kTileRows>
 struct TileDMA {
   static constexpr int kInstr = ROWS / (4 * NW);  // instructions per wave per tile
-  static_assert((NW == 4 || NW == 8) && (ROWS == 32 || ROWS == 64) && kInstr >= 1, "4 or 8 waves fill a tile");
+  static_assert((NW == 2 || NW == 4 || NW == 8) && (ROWS == 32 || ROWS == 64) && kInstr >= 1,
+                "2, 4 or 8 waves fill a tile");
   // Instruction r of wave w fills tile row 4 g + sub, g = kInstr w + r and
   // sub = lane / 16, whose swizzle is 4 sub + g % 4: the lane loads logical
   // chunk lc0 ^ (g % 4) with lc0 = (lane % 16) ^ 4 sub. Only these values are

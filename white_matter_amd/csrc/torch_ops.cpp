@@ -181,7 +181,7 @@ struct Schedule {
   int status = kDocMode;
   // packed segments (status kPacked), see wmx_attn_args
   Tensor qi, ki, cu_q, cu_k, q_units, k_units, ds_offsets;
-  int64_t num_segments = 0, max_q = 0, max_k = 0, layout = 0, keys_unique = 1, ds_elements = 0;
+  int64_t num_segments = 0, max_q = 0, max_k = 0, layout = 0, keys_unique = 1, ds_elements = 0, key_tile = 0;
   // int32 contiguous copies of the document arrays that were not (status kDocMode)
   std::array<Tensor, 4> docs;
 
@@ -195,7 +195,7 @@ WeakCache<Schedule> g_cyclic_cache;
 // (white_matter::_cyclic_schedule: [facts, query_indices, key_indices,
 // cu_queries, cu_keys, q_units, k_units, ds_offsets], facts = int64 CPU
 // {status, num_segments, max_queries, max_keys, segment_layout, keys_unique,
-// ds_elements}).
+// ds_elements, key_tile}).
 std::shared_ptr<Schedule> schedule_for(const std::array<Tensor, 4>& m, int64_t q_len, int64_t k_len, int64_t stride,
                                        int64_t offset) {
   auto same = [&](const Schedule& s) {
@@ -216,7 +216,7 @@ std::shared_ptr<Schedule> schedule_for(const std::array<Tensor, 4>& m, int64_t q
     at::AutoDispatchBelowADInplaceOrView below;
     built = packer.call(m[0], m[1], m[2], m[3], q_len, k_len, stride, offset);
   }
-  TORCH_CHECK(!built.empty() && built[0].numel() == 7, "_cyclic_schedule returned an unexpected result");
+  TORCH_CHECK(!built.empty() && built[0].numel() == 8, "_cyclic_schedule returned an unexpected result");
   const Tensor facts = built[0].to(at::kLong).contiguous();
   const int64_t* f = facts.data_ptr<int64_t>();
   s->status = (int)f[0];
@@ -228,6 +228,7 @@ std::shared_ptr<Schedule> schedule_for(const std::array<Tensor, 4>& m, int64_t q
     s->layout = f[4];
     s->keys_unique = f[5];
     s->ds_elements = f[6];
+    s->key_tile = f[7];
     s->qi = built[1].contiguous();
     s->ki = built[2].contiguous();
     s->cu_q = built[3].to(at::kInt).contiguous();
@@ -288,6 +289,7 @@ void fill_visibility(wmx_attn_args& a, const Schedule* s, const std::array<Tenso
     a.num_k_units = (int32_t)s->k_units.size(0);
     TORCH_CHECK(s->q_units.size(1) == s->k_units.size(1), "q_units and k_units must have entries of one width");
     a.unit_fields = (int32_t)s->q_units.size(1);
+    a.key_tile = (int32_t)s->key_tile;
     if (backward) {
       a.ds_offsets = s->ds_offsets.data_ptr<int64_t>();
       a.ds_elements = s->ds_elements;
@@ -518,7 +520,7 @@ struct PackedPlan {
   bool covered = false;          // false: the schedule runs as given
   Tensor qi, ki, cu_q, cu_k;     // the covering schedule (or converted copies), else undefined
   Tensor out_gaps, dq_gaps, dkv_gaps, q_units, k_units, ds_offsets;
-  int64_t num_segments = 0, max_q = 0, max_k = 0, layout = 0, keys_unique = 1, ds_elements = 0;
+  int64_t num_segments = 0, max_q = 0, max_k = 0, layout = 0, keys_unique = 1, ds_elements = 0, key_tile = 0;
 
   explicit PackedPlan(const std::array<Tensor, 4>& m) : key(m) {}
 };
@@ -526,7 +528,7 @@ struct PackedPlan {
 WeakCache<PackedPlan> g_plan_cache;
 
 // facts = int64 CPU {num_segments, max_queries, max_keys, segment_layout,
-// keys_unique, ds_elements, covered}; then query_indices, key_indices,
+// keys_unique, ds_elements, covered, key_tile}; then query_indices, key_indices,
 // cu_queries, cu_keys (of the covering schedule; the given tensors when not
 // covered), out_gaps, dq_gaps, dkv_gaps, q_units, k_units, ds_offsets
 std::shared_ptr<PackedPlan> packed_plan(const std::array<Tensor, 4>& m, int64_t max_queries, int64_t max_keys,
@@ -543,7 +545,7 @@ std::shared_ptr<PackedPlan> packed_plan(const std::array<Tensor, 4>& m, int64_t 
     at::AutoDispatchBelowADInplaceOrView below;
     built = planner.call(m[0], m[1], m[2], m[3], shape[0], shape[1], shape[2], shape[3], shape[4], shape[5], shape[6]);
   }
-  TORCH_CHECK(built.size() == 11 && built[0].numel() == 7, "_packed_plan returned an unexpected result");
+  TORCH_CHECK(built.size() == 11 && built[0].numel() == 8, "_packed_plan returned an unexpected result");
   auto p = std::make_shared<PackedPlan>(m);
   p->shape = shape;
   const Tensor facts = built[0].to(at::kLong).contiguous();
@@ -555,6 +557,7 @@ std::shared_ptr<PackedPlan> packed_plan(const std::array<Tensor, 4>& m, int64_t 
   p->keys_unique = f[4];
   p->ds_elements = f[5];
   p->covered = f[6] != 0;
+  p->key_tile = f[7];
   if (p->covered) {
     p->qi = built[1].to(at::kLong).contiguous();
     p->ki = built[2].to(at::kLong).contiguous();
@@ -597,6 +600,7 @@ void fill_plan(wmx_attn_args& a, const PackedPlan& p, const std::array<Tensor, 4
   a.num_k_units = (int32_t)p.k_units.size(0);
   TORCH_CHECK(p.q_units.size(1) == p.k_units.size(1), "q_units and k_units must have entries of one width");
   a.unit_fields = (int32_t)p.q_units.size(1);
+  a.key_tile = (int32_t)p.key_tile;
   if (backward) {
     a.ds_offsets = p.ds_offsets.data_ptr<int64_t>();
     a.ds_elements = p.ds_elements;

@@ -147,10 +147,13 @@ struct SegmentRows {
     layout = (consecutive ? 1 : 0) | (one_row ? 2 : 0);
     from_one = from_one_;
     int t0 = 0;
+    // one address for the whole wave: the values are uniform (scalar registers)
     split_flat(first[0], extent, row, t0);
+    row = __builtin_amdgcn_readfirstlane(row);
+    t0 = __builtin_amdgcn_readfirstlane(t0);
     row_base = (int64_t)row * extent;
     slot0 = t0;
-    slot1 = count > 1 ? (int)(first[1] - row_base) : t0 + 1;
+    slot1 = __builtin_amdgcn_readfirstlane(count > 1 ? (int)(first[1] - row_base) : t0 + 1);
   }
   // The same from the entry's precomputed row and slots of elements 0 and 1.
   __device__ __forceinline__ void set(const int64_t* first, int extent_, bool consecutive, bool one_row, bool from_one_,

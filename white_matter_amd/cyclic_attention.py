@@ -200,7 +200,7 @@ def _cyclic_schedule(
     """The kernel form of one residue call's document metadata, built when the
     C++ operators (csrc/torch_ops.cpp) miss their schedule cache: a CPU int64
     facts tensor {status, num_segments, max_queries, max_keys, segment_layout,
-    keys_unique, ds_elements} and, for status 2 (packed segments), the varlen
+    keys_unique, ds_elements, key_tile} and, for status 2 (packed segments), the varlen
     tensors query_indices, key_indices, cu_queries, cu_keys and the work lists
     q_units, k_units, ds_offsets. Status 1: no query sees a key; status 0: the
     metadata is not run-structured, or key rows other than the dummy slots
@@ -209,13 +209,13 @@ def _cyclic_schedule(
     schedule = _build_packed_schedule(qseg, kseg, qstart, kqend, q_len, k_len, stride, offset)
 
     def facts(*values: int) -> torch.Tensor:
-        return torch.tensor(values + (0,) * (7 - len(values)), dtype=torch.int64)
+        return torch.tensor(values + (0,) * (8 - len(values)), dtype=torch.int64)
 
     if schedule is None:
         return [facts(0)]
     if schedule == "empty":
         return [facts(1)]
-    from .strict_causal_attention import _keys_unique_code, _schedule_flags, _work_units
+    from .strict_causal_attention import _key_tile, _keys_unique_code, _schedule_flags, _work_units
 
     max_q, max_k, flags = _schedule_flags(schedule)
     unique = _keys_unique_code(flags)
@@ -224,9 +224,10 @@ def _cyclic_schedule(
         # every row with atomics; the document-mode kernels keep one key row
         # per slot (dummy slots alone go through small accumulators)
         return [facts(0)]
-    q_units, k_units, ds_offsets, ds_elements = _work_units(schedule, stride, query_extent=q_len)
+    key_tile = _key_tile(schedule, stride)
+    q_units, k_units, ds_offsets, ds_elements = _work_units(schedule, stride, query_extent=q_len, key_tile=key_tile)
     return [
-        facts(2, schedule.cu_queries.numel() - 1, max_q, max_k, flags & 15, unique, ds_elements),
+        facts(2, schedule.cu_queries.numel() - 1, max_q, max_k, flags & 15, unique, ds_elements, key_tile),
         schedule.query_indices, schedule.key_indices, schedule.cu_queries, schedule.cu_keys,
         q_units, k_units, ds_offsets,
     ]

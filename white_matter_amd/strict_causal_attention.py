@@ -441,12 +441,12 @@ def _covering_schedule(metadata: StrictCausalMetadata, batch: int, length: int, 
 
 
 def _work_units(
-    metadata: StrictCausalMetadata, stride: int = 1, query_extent: int | None = None
+    metadata: StrictCausalMetadata, stride: int = 1, query_extent: int | None = None, key_tile: int = _TILE
 ) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor, int]:
     """The kernels' work lists and dS layout, cached on the metadata object per
-    query stride and entry form: the (segment, tile) units of the query-tiled
-    kernels (forward, dQ: 128 rows) and of the key-tiled kernel (dK/dV: 128
-    keys), heaviest first, as int32 device tensors, and the int64
+    query stride, entry form and key tile: the (segment, tile) units of the
+    query-tiled kernels (forward, dQ: 128 rows) and of the key-tiled kernel
+    (dK/dV: `key_tile` keys, 128 or 64, wmx_attn_args key_tile), heaviest first, as int32 device tensors, and the int64
     (num_segments + 1) offsets of the segments' dS blocks (keys x queries
     rounded up to 128 elements each) with their total. A unit's cost is the
     number of 64-row tiles its loop visits (then its row count): query i of a
@@ -461,8 +461,10 @@ def _work_units(
     query and key rows and slots, and its dS offset (wmx_attn_args
     unit_fields): a workgroup then reads its entry alone before loading rows,
     not cu_queries, cu_keys and the index arrays one after another."""
+    if key_tile not in (64, _TILE):
+        raise ValueError(f"key_tile must be 64 or {_TILE}")
     by_stride = metadata.__dict__.setdefault("_units", {})
-    units = by_stride.get((stride, query_extent))
+    units = by_stride.get((stride, query_extent, key_tile))
     if units is None:
         _kernels.guard_capture("building the work lists of a packed-document schedule")
         q_units, k_units, ds_blocks = [], [], []
@@ -474,9 +476,9 @@ def _work_units(
                 rows = min(nq, (t + 1) * _TILE) - t * _TILE
                 reach = min(nk, max(0, off + stride * (t * _TILE + rows - 1) + 1))
                 q_units.append(((-(-reach // _STEP), rows), s, t))
-            for t in range(0, -(-nk // _TILE)):
-                keys = min(nk, (t + 1) * _TILE) - t * _TILE
-                first = max(0, -(-(t * _TILE - off) // stride))
+            for t in range(0, -(-nk // key_tile)):
+                keys = min(nk, (t + 1) * key_tile) - t * key_tile
+                first = max(0, -(-(t * key_tile - off) // stride))
                 steps = -(-(nq - first // _STEP * _STEP) // _STEP) if first < nq else 0
                 k_units.append(((steps, keys), s, t))
         device = metadata.query_indices.device
@@ -493,8 +495,20 @@ def _work_units(
             out[:, 1] = torch.tensor([tile for _, _, tile in entries], dtype=torch.int32)
             return out.to(device)
 
-        units = by_stride[(stride, query_extent)] = (table(q_units), table(k_units), offsets.to(device), int(offsets[-1]))
+        units = by_stride[(stride, query_extent, key_tile)] = (
+            table(q_units), table(k_units), offsets.to(device), int(offsets[-1])
+        )
     return units
+
+
+def _key_tile(metadata: StrictCausalMetadata, stride: int = 1) -> int:
+    """Keys per dK/dV workgroup for a packed schedule (wmx_attn_args key_tile).
+    Strided (cyclic) calls give each key tile few query tiles, so the per-unit
+    setup (bounds, K/V rows, first query tiles) dominates: 64-key workgroups,
+    two per CU, overlap one's setup with the other's loop (C3 strides 4 and 8:
+    2-3% faster passes). Full-sequence schedules keep 128 keys per workgroup,
+    whose query tiles then serve twice the keys (C2: 222 against 252 us)."""
+    return 64 if stride >= 2 else _TILE
 
 
 def _segment_fields(metadata: StrictCausalMetadata, query_extent: int, ds_offsets: torch.Tensor) -> torch.Tensor:
@@ -723,7 +737,7 @@ def _packed_plan(
     the C++ packed operators miss their plan cache (which holds it until one
     of the schedule's tensors is freed or changed in place): a CPU int64 facts
     tensor {num_segments, max_queries, max_keys, segment_layout, keys_unique,
-    ds_elements, covered}, the covering schedule's query_indices, key_indices,
+    ds_elements, covered, key_tile}, the covering schedule's query_indices, key_indices,
     cu_queries and cu_keys (empty when it is the schedule itself: covered 0),
     the rows no segment writes (out_gaps, dq_gaps, dkv_gaps, see
     _schedule_gaps) and the work lists q_units, k_units, ds_offsets (see
@@ -736,10 +750,12 @@ def _packed_plan(
     cover = _covering_schedule(metadata, batch, length, key_slots)
     max_q, max_k, flags = _schedule_flags(cover)
     gaps = _schedule_gaps(cover, batch, length, heads, key_slots, kv_heads)
-    q_units, k_units, ds_offsets, ds_elements = _work_units(cover, query_extent=length)
+    key_tile = _key_tile(cover)
+    q_units, k_units, ds_offsets, ds_elements = _work_units(cover, query_extent=length, key_tile=key_tile)
     covered = cover is not metadata
     facts = torch.tensor(
-        [cover.cu_queries.numel() - 1, max_q, max_k, flags & 15, _keys_unique_code(flags), ds_elements, int(covered)],
+        [cover.cu_queries.numel() - 1, max_q, max_k, flags & 15, _keys_unique_code(flags), ds_elements, int(covered),
+         key_tile],
         dtype=torch.int64,
     )
     device = query_indices.device

@@ -935,6 +935,7 @@ def kv_producer_line(device, batch=8, tokens=256, seed=9):
         weight, _ = model.router[side]
         weight.copy_((torch.randn(weight.shape, generator=gen, device=device) * 0.003).to(weight.dtype))
     sources, hidden, channels = config.num_sources, config.hidden_size, config.num_kv_channels
+    read = len(model.router_read)  # sources the routers read (router_layer_stride)
     stacked = torch.randn(batch, tokens, sources, hidden, generator=gen, device=device)
     with torch.no_grad():
         for _ in range(3):
@@ -945,11 +946,12 @@ def kv_producer_line(device, batch=8, tokens=256, seed=9):
     rows = batch * tokens
     premix = rows * sources * hidden * (4 + 2 * 2)
     mix = rows * (2 * sources * hidden * 2 + 2 * channels * sources * 2 + 2 * channels * hidden * 2)
-    gemm = 2 * (rows * sources * hidden * 2 + channels * sources * sources * hidden * 2)
+    gemm = 2 * (rows * read * hidden * 2 + channels * sources * read * hidden * 2)
     moved = premix + mix + gemm
     return {
         "workload": f"KV-pool producer, one C5 group: B={batch} T={tokens}, {sources} fp32 sources x {hidden}, "
-        f"{channels} channels (premix, router GEMM, routed sum, mix norm, gain)",
+        f"{channels} channels (premix, router GEMM over {read} sources: router_layer_stride "
+        f"{config.router_layer_stride}, routed sum, mix norm, gain)",
         "ms": round(ms, 4),
         "gbps": round(moved / (ms * 1e-3) / 1e9, 1),
         "frac_hbm": round(moved / (ms * 1e-3) / 1e9 / PEAK_HBM_GBPS, 4),

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 10
+#define WMX_ABI_VERSION 11
 
 enum {
   WMX_OK = 0,
@@ -373,8 +373,19 @@ typedef struct wmx_kv_router_args {
   void* workspace;            /* wmx_kv_router_workspace_size bytes, 16-byte aligned */
   int64_t workspace_bytes;
   int32_t rows;               /* B*T */
-  int32_t inputs;             /* S*hidden, a positive multiple of 64 */
+  int32_t inputs;             /* the product's width, a positive multiple of 64 */
   int32_t logits;             /* C*S, 1 .. WMX_KV_ROUTER_MAX_LOGITS */
+  /* The reference Router's strided source view (modules/routing.py:46-99,
+   * router_layer_stride): with source_width > 0 a row's inputs are its
+   * blocks of source_width elements at sources source_start,
+   * source_start + source_stride, ... (inputs / source_width of them), read
+   * in place from the premixed rows, row_stride elements apart. With
+   * source_width 0 the inputs are a row's first `inputs` elements and rows
+   * are `inputs` apart (row_stride ignored). source_width is a multiple of 64. */
+  int32_t row_stride;
+  int32_t source_width;
+  int32_t source_start;
+  int32_t source_stride;
 } wmx_kv_router_args;
 
 /*

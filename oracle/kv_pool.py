@@ -20,14 +20,16 @@ and half-turn rotations).
 `projection_inputs` follows src/white_matter/modules/kv_pool.py:97-136
 (`KVPool._project` in its bf16 inference form: rms_norm of the sources,
 `_premix` :15-19, the mixer, the mix norm with eps 1e-4, `_projection_input`
-:22-25) and src/white_matter/modules/routing.py:77-124 (`Router.forward` with
-every source in the router's context, `_RoutedMixer.forward`). Sums are
+:22-25) and src/white_matter/modules/routing.py:46-124 (`Router.forward` with
+its strided source view, `_RoutedMixer.forward`). Sums are
 taken in float64, with a bf16 rounding wherever the reference casts or a
 bf16 operation returns (premixed rows, logits, mixtures, outputs). Pinned
 (tests/test_kv_pool.py) against the reference's formulation with PyTorch's
 F.rms_norm, F.linear and einsum, against the closed form of the routing
 prior (each channel reads one source scaled by 2^-2), at magnitudes where
-both eps values move the result, and by a planted exchange of the two eps.
+both eps values move the result, by a planted exchange of the two eps, and,
+for a strided router, against the full-width router whose weight columns of
+the sources it does not read are zero (the same product).
 """
 
 from __future__ import annotations
@@ -68,12 +70,14 @@ def write_pool(key, value, weight, cos, sin, keys, values, slots, eps):
     return out_k, out_v
 
 
-def projection_inputs(stacked, pre_mix, router, gain, eps, mix_eps):
+def projection_inputs(stacked, pre_mix, router, gain, eps, mix_eps, layer_stride=1):
     """Float64 (2, C, B*T, hidden) holding bf16 values: the K-side and V-side
     inputs of the per-channel projections for sources stacked (B, T, S,
     hidden); pre_mix (2, S, hidden); router ((W_K, b_K), (W_V, b_V)) with W
-    (C*S, S*hidden) and b (C*S,) (logit of channel c, source s at c*S + s);
-    gain (2, C, hidden)."""
+    (C*S, n*hidden) and b (C*S,) (logit of channel c, source s at c*S + s);
+    gain (2, C, hidden). The router's context is the premixed sources
+    (S - 1) % layer_stride, + layer_stride, ... (n of them), concatenated
+    (reference modules/routing.py:66-72, 96-99)."""
     bf16 = torch.bfloat16
     x = stacked.to(torch.float64)
     batch, tokens, sources, hidden = x.shape
@@ -84,7 +88,8 @@ def projection_inputs(stacked, pre_mix, router, gain, eps, mix_eps):
     for side in range(2):
         premixed = _round(normed * pre_mix[side].to(torch.float64), bf16).reshape(rows, sources, hidden)
         weight, bias = (t.to(torch.float64) for t in router[side])
-        logits = _round(premixed.reshape(rows, sources * hidden) @ weight.t() + bias, bf16)
+        context = premixed[:, (sources - 1) % layer_stride :: layer_stride].reshape(rows, -1)
+        logits = _round(context @ weight.t() + bias, bf16)
         logits = logits.reshape(rows, channels, sources)
         mixed = torch.zeros(rows, channels, hidden, dtype=torch.float64)
         for s in range(sources):  # the routed sum, one source at a time

@@ -110,8 +110,21 @@ def test_argument_checks_return_errors_without_launching():
     assert lib.wmx_kv_router(ctypes.byref(router), None) == -2
     assert b"logits" in lib.wmx_last_error()
     router.logits = 200
+    # the strided source view: widths that split a 64-input stage, a start
+    # before the row, rows too short for the selected sources
+    router.inputs, router.source_width, router.source_stride = 13 * 1024, 96, 2
+    assert lib.wmx_kv_router(ctypes.byref(router), None) == -2
+    assert b"source_width" in lib.wmx_last_error()
+    router.source_width, router.source_start = 1024, -1
+    assert lib.wmx_kv_router(ctypes.byref(router), None) == -1
+    assert b"start" in lib.wmx_last_error()
+    router.source_start, router.row_stride = 0, 24 * 1024  # sources 0, 2, .., 24 need 25 blocks
+    assert lib.wmx_kv_router(ctypes.byref(router), None) == -1
+    assert b"row_stride" in lib.wmx_last_error()
+    router.row_stride = 25 * 1024
     assert lib.wmx_kv_router(ctypes.byref(router), None) == -1
     assert b"NULL" in lib.wmx_last_error()
+    router.inputs, router.source_width = 25 * 1024, 0  # every source
     for side in range(2):
         router.premixed[side] = router.weight[side] = router.alpha[side] = 0x1000
     # 2 sides x 25 chunks of 1024 inputs x 2048 rows x 200 logits, fp32

@@ -108,13 +108,14 @@ def test_matches_reference_eager_sequence_on_gpu():
     assert (keys[:, :, :, slots] == ek[:, :, :, slots]).float().mean() > 0.95
 
 
-def _producer_inputs(batch, tokens, sources, hidden, channels, seed, src_dtype, weight_dtype, scale=1.0):
+def _producer_inputs(batch, tokens, sources, hidden, channels, seed, src_dtype, weight_dtype, scale=1.0, stride=1):
     gen = torch.Generator().manual_seed(seed)
     stacked = (torch.randn(batch, tokens, sources, hidden, generator=gen) * scale).to(src_dtype)
     pre_mix = (1 + 0.2 * torch.randn(2, sources, hidden, generator=gen)).to(weight_dtype)
+    width = len(range((sources - 1) % stride, sources, stride)) * hidden  # the sources the router reads
     router = tuple(
         (
-            (torch.randn(channels * sources, sources * hidden, generator=gen) * 0.5 / (sources * hidden) ** 0.5).bfloat16(),
+            (torch.randn(channels * sources, width, generator=gen) * 0.5 / width**0.5).bfloat16(),
             (torch.randn(channels * sources, generator=gen) * 0.25).bfloat16(),
         )
         for _ in range(2)
@@ -123,11 +124,11 @@ def _producer_inputs(batch, tokens, sources, hidden, channels, seed, src_dtype, 
     return stacked, pre_mix, router, gain
 
 
-def _hip_inputs(stacked, pre_mix, router, gain):
+def _hip_inputs(stacked, pre_mix, router, gain, stride=1):
     with torch.no_grad():
         return kv_pool.projection_inputs(
             stacked.to(DEV), tuple(pre_mix.to(DEV)), tuple((w.to(DEV), b.to(DEV)) for w, b in router),
-            tuple(gain.to(DEV)), eps=1e-6, mix_eps=1e-4,
+            tuple(gain.to(DEV)), eps=1e-6, mix_eps=1e-4, router_layer_stride=stride,
         )
 
 
@@ -151,6 +152,44 @@ def test_producer_matches_oracle(batch, tokens, sources, hidden, channels, src_d
     expected = ref.projection_inputs(*inputs, 1e-6, 1e-4)
     _producer_close(hk, expected[0], "h_K")
     _producer_close(hv, expected[1], "h_V")
+
+
+@pytest.mark.parametrize(
+    ("sources", "hidden", "channels", "stride"),
+    # the model's shape (25 sources, stride 2: sources 0, 2, .., 24), a start
+    # past source 0 ((S - 1) % stride = 2), one source read, and a width that
+    # splits 64-input stages (the library GEMM path)
+    [(25, 1024, 8, 2), (9, 256, 3, 3), (4, 128, 4, 4), (7, 520, 5, 2)],
+)
+def test_producer_strided_router_matches_oracle(sources, hidden, channels, stride):
+    """router_layer_stride > 1 (reference modules/routing.py:66-99; the model
+    configuration's default is 2): the router reads every stride-th source
+    from the top, in place from the premixed rows."""
+    inputs = _producer_inputs(2, 5, sources, hidden, channels, 31 + sources, torch.float32, torch.bfloat16, stride=stride)
+    hk, hv = _hip_inputs(*inputs, stride=stride)
+    expected = ref.projection_inputs(*inputs, 1e-6, 1e-4, stride)
+    _producer_close(hk, expected[0], "h_K")
+    _producer_close(hv, expected[1], "h_V")
+
+
+def test_strided_router_logits_match_gathered_product():
+    """wmx_kv_router over a strided source view: the fp32 product of the
+    gathered sources' columns, within one bf16 step, and the same bits on a
+    second run."""
+    rows, sources, hidden, stride, logits = 300, 25, 1024, 2, 200
+    gen = torch.Generator().manual_seed(8)
+    p = torch.randn(2, rows, sources * hidden, generator=gen).bfloat16().to(DEV)
+    read = range((sources - 1) % stride, sources, stride)
+    w = [(torch.randn(logits, len(read) * hidden, generator=gen) * (len(read) * hidden) ** -0.5).bfloat16().to(DEV)
+         for _ in range(2)]
+    b = [torch.randn(logits, generator=gen).bfloat16().to(DEV) for _ in range(2)]
+    alpha = torch.ops.white_matter.kv_router(p, w[0], b[0], w[1], b[1], hidden, stride)
+    for side in range(2):
+        gathered = p[side].view(rows, sources, hidden)[:, read.start :: read.step].reshape(rows, -1)
+        exact = gathered.double() @ w[side].double().t() + b[side].double()
+        err = (alpha[side].double() - exact).abs()
+        assert bool((err <= exact.abs() * 2.0**-8 + 1e-3).all()), f"side {side}: max error {err.max().item():.3e}"
+    assert torch.equal(torch.ops.white_matter.kv_router(p, w[0], b[0], w[1], b[1], hidden, stride), alpha)
 
 
 def test_producer_repeated_source_view_and_small_magnitudes():

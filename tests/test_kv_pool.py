@@ -197,3 +197,40 @@ def test_producer_planted_mistakes_are_caught():
         for w, b in router
     )
     assert not _close_in_bf16(ref.projection_inputs(stacked, pre_mix, transposed, gain, 1e-6, 1e-4), expected)
+
+
+def _padded_router(router, sources, hidden, read):
+    """The full-width router equal to a router whose context is the sources
+    `read`: its weight columns of those sources hold that router's columns,
+    the others zero."""
+    padded = []
+    for weight, bias in router:
+        full = torch.zeros(weight.shape[0], sources, hidden, dtype=weight.dtype)
+        full[:, list(read)] = weight.view(weight.shape[0], len(read), hidden)
+        padded.append((full.reshape(weight.shape[0], -1), bias))
+    return tuple(padded)
+
+
+@pytest.mark.parametrize(("sources", "layer_stride"), [(5, 2), (7, 3), (25, 2), (4, 4), (6, 4), (8, 3)])
+def test_producer_oracle_strided_router_equals_padded_full_router(sources, layer_stride):
+    """A router reading every layer_stride-th source from (S - 1) %
+    layer_stride (routing.py:66-72, 96-99) is the full-width router whose
+    columns of the other sources are zero: the oracle's strided context gives
+    the full-width oracle's result. A context starting at source 0 instead
+    (a plausible slip where S - 1 is not a multiple of the stride) does not."""
+    hidden, channels = 64, 3
+    stacked, pre_mix, _, gain = _producer_inputs(11 + sources, sources=sources, hidden=hidden, channels=channels,
+                                                 scale=1e-3, logit_scale=0.004)
+    read = range((sources - 1) % layer_stride, sources, layer_stride)
+    gen = torch.Generator().manual_seed(sources * layer_stride)
+    router = tuple(
+        ((torch.randn(channels * sources, len(read) * hidden, generator=gen) * 0.05).bfloat16(),
+         (torch.randn(channels * sources, generator=gen) * 0.004).bfloat16())
+        for _ in range(2)
+    )
+    strided = ref.projection_inputs(stacked, pre_mix, router, gain, 1e-6, 1e-4, layer_stride)
+    full = ref.projection_inputs(stacked, pre_mix, _padded_router(router, sources, hidden, read), gain, 1e-6, 1e-4)
+    assert torch.equal(strided, full)
+    if read.start:
+        slip = _padded_router(router, sources, hidden, range(0, sources, layer_stride)[: len(read)])
+        assert not _close_in_bf16(ref.projection_inputs(stacked, pre_mix, slip, gain, 1e-6, 1e-4), full)

@@ -19,7 +19,7 @@ import torch
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
 # the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
 OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -165,6 +165,10 @@ class KvRouterArgs(ctypes.Structure):
         ("rows", ctypes.c_int32),
         ("inputs", ctypes.c_int32),
         ("logits", ctypes.c_int32),
+        ("row_stride", ctypes.c_int32),
+        ("source_width", ctypes.c_int32),
+        ("source_start", ctypes.c_int32),
+        ("source_stride", ctypes.c_int32),
     ]
 
 

@@ -323,6 +323,16 @@ static int check_kv_router(const wmx_kv_router_args* a) {
     return fail(WMX_E_UNSUPPORTED, "kv router inputs %d is not a positive multiple of 64", a->inputs);
   if (a->logits < 1 || a->logits > WMX_KV_ROUTER_MAX_LOGITS)
     return fail(WMX_E_UNSUPPORTED, "kv router logits %d is not in [1, %d]", a->logits, WMX_KV_ROUTER_MAX_LOGITS);
+  if (a->source_width != 0) {
+    if (a->source_width < 0 || a->source_width % 64 || a->inputs % a->source_width)
+      return fail(WMX_E_UNSUPPORTED, "kv router source_width %d must be a multiple of 64 dividing inputs",
+                  a->source_width);
+    if (a->source_start < 0 || a->source_stride < 1) return fail(WMX_E_INVALID, "kv router source start/stride");
+    const int64_t blocks = a->inputs / a->source_width;
+    const int64_t last = (int64_t)a->source_start + (blocks - 1) * a->source_stride;
+    if (a->row_stride < 0 || a->row_stride % 8 || (last + 1) * a->source_width > a->row_stride)
+      return fail(WMX_E_INVALID, "kv router row_stride %d does not hold the selected sources", a->row_stride);
+  }
   return WMX_OK;
 }
 

@@ -1,8 +1,6 @@
 // KV-pool producer for gfx950: the token-local steps ahead of the per-channel
 // projection (reference modules/kv_pool.py:97-160 `_project`,
-// modules/routing.py:77-124 `Router`, `_RoutedMixer`). Between the two
-// kernels the router logits are one plain GEMM of the premixed rows, left to
-// the BLAS library.
+// modules/routing.py:77-124 `Router`, `_RoutedMixer`).
 //
 //   premix: every source row of a token is RMS-normalised and scaled by the
 //           K-side and the V-side pre-mix weights, rounded to bf16: the
@@ -13,11 +11,17 @@
 //           channel gain and rounded to bf16, written in the projection's
 //           input layout (channel, token, hidden) (one workgroup per token,
 //           side and group of 8 channels; the token's premixed rows are read
-//           once for all the group's channels).
+//           once for all the group's channels);
+//   router: between the two, the router logits of both sides, a split-K
+//           MFMA GEMM over the premixed rows read in place: the whole row,
+//           or the router's strided view of it (every source_stride-th
+//           source block from source_start, routing.py:66-72) without a
+//           gathered copy, then a reduce kernel that adds the chunks' fp32
+//           partials in order with the bias and rounds once to bf16.
 //
-// Both are HBM-bound: per token the sources are read once, the premixed rows
-// written once and read twice (the GEMM and the mixture), the channels
-// written once. The eager sequence materialises the normalised sources, both
+// premix and mix are HBM-bound: per token the sources are read once, the
+// premixed rows written once and read twice (the router and the mixture),
+// the channels written once. The eager sequence materialises the normalised sources, both
 // premixed stacks, the mixtures, their normalisation and the gained copies.
 #include "wmx_kernels.h"
 
@@ -222,7 +226,16 @@ __global__ __launch_bounds__(256, 2) void kv_router_kernel(const wmx_kv_router_a
   const int stages = (k1 - k0) / kRouterStage;
   const int row = m0 + wave * 32 + col;
   const bool row_ok = row < a.rows;
-  const bf16* arow = (const bf16*)a.premixed[side] + (int64_t)(row_ok ? row : 0) * a.inputs + 8 * half;
+  // a row's inputs: its first `inputs` elements, or the blocks of the
+  // selected sources (a stage never straddles two: widths are multiples of
+  // kRouterStage)
+  const int64_t row_stride = a.source_width ? a.row_stride : a.inputs;
+  const bf16* arow = (const bf16*)a.premixed[side] + (int64_t)(row_ok ? row : 0) * row_stride + 8 * half;
+  auto input_at = [&](int k) __attribute__((always_inline)) -> int64_t {
+    if (!a.source_width) return k;
+    const int block = k / a.source_width;
+    return (int64_t)(a.source_start + block * a.source_stride) * a.source_width + (k - block * a.source_width);
+  };
   const bf16* wgt = (const bf16*)a.weight[side];
   const u32x4 z = {0u, 0u, 0u, 0u};
   // this thread's weight chunks of a stage: chunk c = i * 256 + tid of the
@@ -242,8 +255,9 @@ __global__ __launch_bounds__(256, 2) void kv_router_kernel(const wmx_kv_router_a
     }
   };
   auto load_a = [&](int k, bf16x8 (&r)[kRouterStage / 16]) __attribute__((always_inline)) {
+    const bf16* p = arow + input_at(k);
 #pragma unroll
-    for (int s = 0; s < kRouterStage / 16; ++s) r[s] = as_bf16x8(row_ok ? load16(arow + k + 16 * s) : z);
+    for (int s = 0; s < kRouterStage / 16; ++s) r[s] = as_bf16x8(row_ok ? load16(p + 16 * s) : z);
   };
 
   f32x16 acc[NB];

@@ -17,8 +17,9 @@ Inference restatement of the reference's feedback block:
     attention with a local Q projection, q-norm and RoPE, and a gated MLP;
   * the pool projection (modules/kv_pool.py:97-217 `KVPool._project`,
     `project_sequence`; modules/routing.py:46-124 `Router`, `_RoutedMixer`):
-    RMS norm, per-source premix, content routers over all L+1 sources, mix
-    norm, gains and the per-channel projection: the norms, premix, routed
+    RMS norm, per-source premix, content routers over every second of the
+    L+1 sources (router_layer_stride 2, the reference configuration's
+    default), mix norm, gains and the per-channel projection: the norms, premix, routed
     sum and gains run as two HIP kernels around the router GEMM
     (`kv_pool.projection_inputs`), the K-norm, RoPE, bf16 cast and pool write
     as one (`kv_pool.write_pool`);
@@ -67,6 +68,9 @@ class FeedbackConfig:
     rms_norm_eps: float = 1.0e-6
     mix_norm_eps: float = 1.0e-4  # kv_pool.py:58
     router_peak: float = 0.25  # the "cyclic:0.25" prior
+    # sources the router reads: every router_layer_stride-th from the top
+    # (configuration_white_matter.py:16, modules/routing.py:66-72)
+    router_layer_stride: int = 2
 
     @property
     def num_sources(self) -> int:  # the block input and every layer output
@@ -104,6 +108,7 @@ class HipKernels:
         return kv_pool.projection_inputs(
             stacked, (model.pre_mix["k"], model.pre_mix["v"]), (model.router["k"], model.router["v"]),
             (model.gain["k"], model.gain["v"]), eps=c.rms_norm_eps, mix_eps=c.mix_norm_eps,
+            router_layer_stride=c.router_layer_stride,
         )
 
 
@@ -165,8 +170,12 @@ class FeedbackModel:
         prior = torch.zeros(k, s)
         for col in range(s):  # routing.py:18-25, rows < cols
             prior[col % k, col] = c.router_peak
+        self.router_read = kv_pool.router_sources(s, c.router_layer_stride)
         self.router = {
-            side: (torch.zeros(k * s, s * d, device=self.device, dtype=dtype), prior.reshape(-1).to(self.device, dtype))
+            side: (
+                torch.zeros(k * s, len(self.router_read) * d, device=self.device, dtype=dtype),
+                prior.reshape(-1).to(self.device, dtype),
+            )
             for side in "kv"
         }
         self.gain = {side: ones(k, d) for side in "kv"}
@@ -226,7 +235,9 @@ class FeedbackModel:
         for side in "kv":
             premixed = (normed * self.pre_mix[side].to(self.residual_dtype)).to(self.dtype)  # (B, T, S, d)
             weight, bias = self.router[side]
-            alpha = F.linear(premixed.reshape(batch, length, sources * d), weight, bias)
+            read = self.router_read
+            context = premixed[:, :, read.start :: read.step].reshape(batch, length, len(read) * d)
+            alpha = F.linear(context, weight, bias)
             alpha = alpha.view(batch, length, c.num_kv_channels, sources)
             mixed = torch.matmul(alpha, premixed)  # (B, T, k, d): sum over sources
             mixed = F.rms_norm(mixed.to(self.residual_dtype), (d,), None, c.mix_norm_eps)

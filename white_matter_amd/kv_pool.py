@@ -273,19 +273,35 @@ def _router_workspace(device: torch.device, need: int) -> torch.Tensor:
 
 @torch.library.custom_op("white_matter::kv_router", mutates_args=())
 def kv_router(
-    premixed: torch.Tensor, weight_k: torch.Tensor, bias_k: torch.Tensor, weight_v: torch.Tensor, bias_v: torch.Tensor
+    premixed: torch.Tensor,
+    weight_k: torch.Tensor,
+    bias_k: torch.Tensor,
+    weight_v: torch.Tensor,
+    bias_v: torch.Tensor,
+    hidden: int = 0,
+    source_stride: int = 1,
 ) -> torch.Tensor:
-    """Both sides' router logits (2, B*T, C*S) bf16 = bf16(premixed[side] .
+    """Both sides' router logits (2, B*T, C*S) bf16 = bf16(context[side] .
     W_side^T + b_side) (wmx_kv_router) from both premixed stacks (2, B*T,
-    S*hidden) and bf16 weights (C*S, S*hidden) and biases (C*S,)."""
-    _, rows, inputs = premixed.shape
-    logits = weight_k.shape[0]
+    S*hidden) and bf16 weights (C*S, n*hidden) and biases (C*S,). The context
+    is the premixed row itself (source_stride 1), or the reference Router's
+    strided view (routing.py:66-99): the n = len(range(start, S, stride))
+    sources start, start + stride, ... with start = (S - 1) % stride, read in
+    place from the row (hidden: the sources' width)."""
+    _, rows, width = premixed.shape
+    logits, inputs = weight_k.shape
     premixed = premixed.contiguous()
     weights = [w.to(torch.bfloat16).contiguous() for w in (weight_k, weight_v)]
     biases = [b.to(torch.bfloat16).contiguous() for b in (bias_k, bias_v)]
     alpha = torch.empty(2, rows, logits, device=premixed.device, dtype=torch.bfloat16)
     a = _native.KvRouterArgs()
     a.rows, a.inputs, a.logits = rows, inputs, logits
+    if source_stride != 1:
+        sources = width // hidden
+        a.row_stride, a.source_width = width, hidden
+        a.source_start, a.source_stride = (sources - 1) % source_stride, source_stride
+    elif inputs != width:
+        raise ValueError("router weights must span the premixed row")
     for side in range(2):
         a.premixed[side] = premixed[side].data_ptr()
         a.weight[side] = weights[side].data_ptr()
@@ -299,8 +315,17 @@ def kv_router(
 
 
 @kv_router.register_fake
-def _(premixed, weight_k, bias_k, weight_v, bias_v):
+def _(premixed, weight_k, bias_k, weight_v, bias_v, hidden=0, source_stride=1):
     return premixed.new_empty((2, premixed.shape[1], weight_k.shape[0]), dtype=torch.bfloat16)
+
+
+def router_sources(sources: int, layer_stride: int) -> range:
+    """The sources a router with `layer_stride` reads (reference routing.py:
+    66-72: from (S - 1) % stride, every stride-th, so the top source is
+    always among them)."""
+    if layer_stride < 1:
+        raise ValueError("router_layer_stride must be positive")
+    return range((sources - 1) % layer_stride, sources, layer_stride)
 
 
 def projection_inputs(
@@ -311,17 +336,20 @@ def projection_inputs(
     *,
     eps: float = 1e-6,
     mix_eps: float = 1e-4,
+    router_layer_stride: int = 1,
 ) -> tuple[torch.Tensor, torch.Tensor]:
     """(h_K, h_V), each (C, B*T, hidden) bf16: the inputs of the per-channel
     K and V projections (reference kv_pool.py:103-136 with its fused bf16
-    casts, and routing.py:108-124 with the router reading every source).
+    casts, and routing.py:46-124 with the router reading every
+    `router_layer_stride`-th source, as the reference's Router).
 
     stacked (B, T, S, hidden) float32 or bfloat16 (stride 0 along S repeats
     one row); pre_mix (K, V) weights (S, hidden); router ((W_K, b_K), (W_V,
-    b_V)) with W (C*S, S*hidden) and b (C*S,), the logits of channel c and
-    source s at c*S + s; gain (K, V) (C, hidden). Per side:
+    b_V)) with W (C*S, n*hidden), n the number of sources the router reads
+    (router_sources), and b (C*S,), the logits of channel c and source s at
+    c*S + s; gain (K, V) (C, hidden). Per side:
       p = bf16(rms_norm(x, eps) * pre_mix)           (HIP, wmx_kv_premix)
-      alpha = bf16(p . W^T + b)                       (HIP, wmx_kv_router)
+      alpha = bf16(p[read sources] . W^T + b)         (HIP, wmx_kv_router)
       m = bf16(sum_s alpha[c, s] * p[s])               (HIP, wmx_kv_mix)
       h = bf16(rms_norm(m, mix_eps) * gain[c])
     Forward only (the reference's training form runs under checkpointing).
@@ -354,16 +382,27 @@ def projection_inputs(
     for g in gain:
         if g.shape != (channels, hidden):
             raise ValueError("gains must be (C, hidden), one shape for both sides")
+    read = router_sources(sources, router_layer_stride)
     for weight, bias in router:
-        if weight.shape != (channels * sources, sources * hidden) or bias.shape != (channels * sources,):
-            raise ValueError("router weights must be (C*S, S*hidden) with a (C*S,) bias")
+        if weight.shape != (channels * sources, len(read) * hidden) or bias.shape != (channels * sources,):
+            raise ValueError("router weights must be (C*S, n*hidden) with a (C*S,) bias, n the sources read")
     premixed = torch.ops.white_matter.kv_premix(stacked, pre_mix[0], pre_mix[1], float(eps))
-    if channels * sources <= _native.KV_ROUTER_MAX_LOGITS and (sources * hidden) % 64 == 0:
+    # the HIP product reads the selected sources in place when their width
+    # keeps each 64-input stage inside one source
+    gather_ok = router_layer_stride == 1 or hidden % 64 == 0
+    if channels * sources <= _native.KV_ROUTER_MAX_LOGITS and (len(read) * hidden) % 64 == 0 and gather_ok:
         (w_k, b_k), (w_v, b_v) = router
-        alphas = torch.ops.white_matter.kv_router(premixed, w_k, b_k, w_v, b_v).unbind(0)
+        alphas = torch.ops.white_matter.kv_router(
+            premixed, w_k, b_k, w_v, b_v, hidden, router_layer_stride
+        ).unbind(0)
     else:
+        rows = premixed.shape[1]
         alphas = [
-            F.linear(premixed[side], weight.to(torch.bfloat16), bias.to(torch.bfloat16))
+            F.linear(
+                premixed[side].view(rows, sources, hidden)[:, read.start :: read.step].reshape(rows, -1),
+                weight.to(torch.bfloat16),
+                bias.to(torch.bfloat16),
+            )
             for side, (weight, bias) in enumerate(router)
         ]
     mixed = torch.ops.white_matter.kv_mix(premixed, alphas[0], alphas[1], gain[0], gain[1], float(mix_eps))

@@ -13,9 +13,15 @@ pytestmark = pytest.mark.gpu
 DEV = "cuda"
 
 
-@pytest.mark.skip(reason="the process segfaulted (exit 139) in torch.cuda.graph's capture_end on the one run of this "
-                         "case: the captured backward is issued from the autograd engine's worker thread; the cause "
-                         "was not found by reading, so the case stays off the GPU")
+@pytest.mark.skip(
+    reason="its one run, on an earlier build whose operators were Python custom ops (schedule caches and gap fills in "
+    "Python), segfaulted (exit 139) in torch.cuda.graph's capture_end, with the backward issued from the autograd "
+    "engine's worker thread; no cause was identified. The operators are now C++ (csrc/torch_ops.cpp CyclicDocFn "
+    "-> forward_impl/backward_impl -> wmx_attn_fwd/bwd): on a cached schedule they reach only caching-allocator "
+    "tensors, fill kernels and kernel launches on the current stream, a cache miss raises under capture, and neither "
+    "library imports an allocating, copying or synchronising call (tests/test_capture_guard.py). That rules out "
+    "this library's host steps but names no cause, so the case stays off the GPU"
+)
 def test_captured_pass_matches_eager():
     torch.manual_seed(12)
     batch, heads, length, dim, stride = 2, 4, 512, 128, 4

@@ -79,6 +79,65 @@ __device__ __forceinline__ float load_shared(const float* p) {
   return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
 }
 
+// Cross-lane exchanges without the LDS crossbar (ds_bpermute) that
+// __shfl_xor compiles to: DPP within rows of 16 lanes, v_permlane16_swap /
+// v_permlane32_swap across them. A decode workgroup is often the only wave on
+// its SIMD, so the crossbar's latency is not hidden there.
+template <int CTRL>
+__device__ __forceinline__ float dpp_mov(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, 0xF, 0xF, false));
+}
+// x of lane l ^ OFF, exactly, for OFF in {1, 2, 8, 16, 32}
+template <int OFF>
+__device__ __forceinline__ float lane_xor(float x) {
+  if constexpr (OFF == 1) {
+    return dpp_mov<0xB1>(x);  // quad_perm [1, 0, 3, 2]
+  } else if constexpr (OFF == 2) {
+    return dpp_mov<0x4E>(x);  // quad_perm [2, 3, 0, 1]
+  } else if constexpr (OFF == 8) {
+    return dpp_mov<0x128>(x);  // row_ror:8 (rows of 16 lanes)
+  } else if constexpr (OFF == 16) {
+    // swaps rows 1 and 3 of the first operand with rows 0 and 2 of the second
+    const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 16) ? r[0] : r[1]);
+  } else {
+    static_assert(OFF == 32, "lane_xor: 1, 2, 8, 16 or 32");
+    // swaps the upper half of the first operand with the lower half of the second
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+    return __uint_as_float((threadIdx.x & 32) ? r[0] : r[1]);
+  }
+}
+
+// Sum over the LPR (8 or 16) consecutive lanes of a key row, the same value
+// in all of them: quads first (exact xor), then half rows and rows by
+// mirroring, which equals the xor partner once each quad (half row) holds one
+// value.
+template <int LPR>
+__device__ __forceinline__ float row_sum(float acc) {
+  acc += lane_xor<1>(acc);
+  acc += lane_xor<2>(acc);
+  acc += dpp_mov<0x141>(acc);  // row_half_mirror: the other quad of the half row
+  if constexpr (LPR == 16) acc += dpp_mov<0x140>(acc);  // row_mirror: the other half row
+  return acc;
+}
+
+// One step of the merge of a wave's row slots: the (m, l, o) of lane l and
+// lane l ^ OFF (same dims, another slot) combined in log-sum-exp form.
+template <int OFF, int G>
+__device__ __forceinline__ void merge_slots(float (&m)[G], float (&l)[G], float (&o)[G][8]) {
+#pragma unroll
+  for (int g = 0; g < G; ++g) {
+    const float mo = lane_xor<OFF>(m[g]);
+    const float lo = lane_xor<OFF>(l[g]);
+    const float mx = fmaxf(fmaxf(m[g], mo), kMaxFloor);
+    const float sa = __builtin_amdgcn_exp2f(m[g] - mx), sb = __builtin_amdgcn_exp2f(mo - mx);
+    l[g] = l[g] * sa + lo * sb;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) o[g][e] = o[g][e] * sa + lane_xor<OFF>(o[g][e]) * sb;
+    m[g] = fmaxf(m[g], mo);
+  }
+}
+
 // Merge the nsplit partials of query head h of row b in split order (the
 // log-sum-exp form of decode_combine_kernel) into output element d.
 __device__ __forceinline__ float merge_splits(const float* ws_o, const float* ws_ml, int64_t prow0, int nsplit, int D,
@@ -183,8 +242,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
           acc = fmaf(q[g][2 * e], bf16_lo(kw[u][e]), acc);
           acc = fmaf(q[g][2 * e + 1], bf16_hi(kw[u][e]), acc);
         }
-#pragma unroll
-        for (int off = LPR / 2; off > 0; off >>= 1) acc += __shfl_xor(acc, off);
+        acc = row_sum<LPR>(acc);
         s[u] = vis[u] ? acc : kNegInf;
         smax = fmaxf(smax, s[u]);
       }
@@ -209,20 +267,9 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
   }
 
   // merge the RPW row slots of the wave (lanes with equal dch)
-#pragma unroll
-  for (int g = 0; g < G; ++g) {
-#pragma unroll
-    for (int off = LPR; off < 64; off <<= 1) {
-      const float mo = __shfl_xor(m[g], off);
-      const float lo = __shfl_xor(l[g], off);
-      const float mx = fmaxf(fmaxf(m[g], mo), kMaxFloor);
-      const float sa = __builtin_amdgcn_exp2f(m[g] - mx), sb = __builtin_amdgcn_exp2f(mo - mx);
-      l[g] = l[g] * sa + lo * sb;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) o[g][e] = o[g][e] * sa + __shfl_xor(o[g][e], off) * sb;
-      m[g] = fmaxf(m[g], mo);
-    }
-  }
+  if constexpr (LPR == 8) merge_slots<8, G>(m, l, o);
+  merge_slots<16, G>(m, l, o);
+  merge_slots<32, G>(m, l, o);
   if (rslot == 0) {
 #pragma unroll
     for (int g = 0; g < G; ++g) {
@@ -294,10 +341,18 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
   if (tid == 0) last_lds = atomicAdd(counters + pair, 1) == nsplit - 1;
   __syncthreads();
   if (!last_lds) return;
-  // every split's (max, sum) of the G heads into LDS with all loads in
-  // flight at once, then each thread's output elements from 8 splits' rows
-  // at a time: the same terms in the same order as merge_splits
+  // every split's (max, sum) of the G heads into LDS and, in the same round
+  // trip, each thread's first output element's rows of the first 8 splits;
+  // then each output element from 8 splits' rows at a time: the same terms
+  // in the same order as merge_splits
   const int64_t head0 = ((int64_t)b * a.q_heads + h0) * nsplit;  // partial row of (h0, split 0)
+  auto orow_of = [&](int idx) { return ws_o + (head0 + (int64_t)(idx / D) * nsplit) * D + idx % D; };
+  float first[8];
+  if (tid < G * D) {
+    const float* orow = orow_of(tid);
+#pragma unroll
+    for (int u = 0; u < 8; ++u) first[u] = u < nsplit ? load_shared(orow + (int64_t)u * D) : 0.f;
+  }
   for (int i = tid; i < G * nsplit * 2; i += 256) {
     const int g = i / (nsplit * 2), r = i - g * nsplit * 2;
     (&ml_lds[g][0][0])[r] = load_shared(ws_ml + (head0 + (int64_t)g * nsplit) * 2 + r);
@@ -305,14 +360,20 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
   __syncthreads();
   for (int idx = tid; idx < G * D; idx += 256) {
     const int g = idx / D, d = idx % D;
-    const float* orow = ws_o + (head0 + (int64_t)g * nsplit) * D + d;
+    const float* orow = orow_of(idx);
     float mx = kMaxFloor;
     for (int s = 0; s < nsplit; ++s) mx = fmaxf(mx, ml_lds[g][s][0]);
     float lsum = 0.f, acc = 0.f;
     for (int s0 = 0; s0 < nsplit; s0 += 8) {
       float ov[8];
 #pragma unroll
-      for (int u = 0; u < 8; ++u) ov[u] = s0 + u < nsplit ? load_shared(orow + (int64_t)(s0 + u) * D) : 0.f;
+      for (int u = 0; u < 8; ++u) {
+        if (idx == tid && s0 == 0) {
+          ov[u] = first[u];
+        } else {
+          ov[u] = s0 + u < nsplit ? load_shared(orow + (int64_t)(s0 + u) * D) : 0.f;
+        }
+      }
 #pragma unroll
       for (int u = 0; u < 8; ++u) {
         if (s0 + u < nsplit) {

@@ -10,15 +10,18 @@ namespace wmx {
 // Value source: none (keys only), fp32 or bf16.
 enum ValueKind { kNoValue = 0, kValueF32 = 1, kValueBF16 = 2 };
 
-// One (b, c, t) per D/8 consecutive lanes (token-fastest, so neighbouring
-// lanes read and write neighbouring rows); each thread then walks the heads,
-// U at a time with all their loads issued before any is used (no branch
-// between them: the last group repeats its final head instead of testing),
-// so cos, sin, the norm weight and the slot are read once per token instead
-// of once per row. KEY_BF16 selects the reference's rounding after every
-// step.
+// One (b, c, t, head group) per D/8 consecutive lanes (token-fastest, so
+// neighbouring lanes read and write neighbouring rows); each thread then
+// walks its group's heads, U at a time with all their loads issued before any
+// is used (no branch between them: the last group repeats its final head
+// instead of testing), so cos, sin, the norm weight and the slot are read
+// once per token and group instead of once per row. One group of all heads
+// where there are many tokens; one head per group for a decode step's few
+// rows, whose latency chain is then one round trip. KEY_BF16 selects the
+// reference's rounding after every step.
 template <int D, bool KEY_BF16, int VALUE>
-__global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a, int64_t tokens_total) {
+__global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a, int64_t tokens_total,
+                                                       int head_groups) {
   // Every product and sum is rounded on its own, as the eager sequence does:
   // a fused multiply-add would skip the rounding of y * cos.
 #pragma clang fp contract(off)
@@ -26,17 +29,24 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
   constexpr int L = LD <= 8 ? 8 : 16;          // lanes per row (a power of two; D = 96 leaves 4 idle)
   constexpr int U = 4;                         // heads in flight per thread
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  const int64_t r = gid / L;
+  const int64_t unit = gid / L;
   const int l = (int)(gid % L);  // this lane's elements: 8 l .. 8 l + 7
-  // A row's L lanes are aligned and share r, so they leave together and the
-  // shuffles below never read a lane that has left.
+  const int64_t r = unit / head_groups;
+  const int hg = (int)(unit - r * head_groups);
+  // A row's L lanes are aligned and share r and hg, so they leave together
+  // and the shuffles below never read a lane that has left.
   if (r >= tokens_total) return;
   const int t = (int)(r % a.tokens);
   const int64_t bc = r / a.tokens;
   const int c = (int)(bc % a.channels);
   const int b = (int)(bc / a.channels);
+  const int per_group = (a.heads + head_groups - 1) / head_groups;
+  const int h_begin = hg * per_group, h_end = min(h_begin + per_group, a.heads);
+  if (h_begin >= h_end) return;
+  // out-of-range slots are not written; the check waits for the slot only at
+  // the stores, so the loads below do not
   const int64_t slot = a.slots[t];
-  if (slot < 0 || slot >= a.pool_slots) return;  // out-of-range slots are not written
+  const bool slot_ok = slot >= 0 && slot < a.pool_slots;
   const int d0 = 8 * l;
   // idle lanes (D = 96) take part in the shuffles with zeros and store nothing
   const bool data = l < LD;
@@ -65,11 +75,11 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
   const int64_t vpool_row =
       (int64_t)b * a.value_pool_stride[0] + (int64_t)c * a.value_pool_stride[1] + slot * a.value_pool_stride[3] + dl;
 
-  for (int h0 = 0; h0 < a.heads; h0 += U) {
+  for (int h0 = h_begin; h0 < h_end; h0 += U) {
     float x[U][8], v[U][8];
     int hu[U];
 #pragma unroll
-    for (int u = 0; u < U; ++u) hu[u] = min(h0 + u, a.heads - 1);
+    for (int u = 0; u < U; ++u) hu[u] = min(h0 + u, h_end - 1);
 #pragma unroll
     for (int u = 0; u < U; ++u) load8<true>(a.key, key_row + hu[u] * a.key_stride[2], KEY_BF16, x[u]);
     if constexpr (VALUE != kNoValue) {
@@ -95,7 +105,7 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
         const float rot = low ? -other : other;
         out[e] = rnd(rnd(y[e] * cs[e]) + rnd(rot * sn[e]));
       }
-      if (data && h0 + u < a.heads) {
+      if (data && slot_ok && h0 + u < h_end) {
         store8_bf16(a.key_pool, kpool_row + hu[u] * a.key_pool_stride[2], out);
         if constexpr (VALUE != kNoValue) store8_bf16(a.value_pool, vpool_row + hu[u] * a.value_pool_stride[2], v[u]);
       }
@@ -104,30 +114,37 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
 }
 
 template <int D, bool KEY_BF16>
-void launch_kv_store_d(const wmx_kv_store_args& a, int64_t rows, dim3 grid, hipStream_t stream) {
+void launch_kv_store_d(const wmx_kv_store_args& a, int64_t rows, int groups, dim3 grid, hipStream_t stream) {
   if (!a.value)
-    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kNoValue>), grid, dim3(256), 0, stream, a, rows);
+    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kNoValue>), grid, dim3(256), 0, stream, a, rows, groups);
   else if (a.value_dtype == WMX_DTYPE_BF16)
-    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kValueBF16>), grid, dim3(256), 0, stream, a, rows);
+    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kValueBF16>), grid, dim3(256), 0, stream, a, rows, groups);
   else
-    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kValueF32>), grid, dim3(256), 0, stream, a, rows);
+    hipLaunchKernelGGL((kv_store_kernel<D, KEY_BF16, kValueF32>), grid, dim3(256), 0, stream, a, rows, groups);
 }
 
 int launch_kv_store(const wmx_kv_store_args& a, hipStream_t stream) {
-  const int64_t rows = (int64_t)a.batch * a.channels * a.tokens;  // each thread walks the heads
+  const int64_t rows = (int64_t)a.batch * a.channels * a.tokens;
   if (rows == 0 || a.heads == 0) return WMX_OK;
-  const int64_t threads = rows * (a.head_dim <= 64 ? 8 : 16);  // lanes per row, as in the kernel
+  const int64_t lanes = a.head_dim <= 64 ? 8 : 16;  // lanes per row, as in the kernel
+  // threads walk all heads of a token where that still gives every CU four
+  // workgroups (1024 x 256 threads); fewer rows (a decode step) split the heads
+  int64_t groups = 1;
+  while (groups < a.heads && rows * groups * lanes < 1024 * 256) groups *= 2;
+  if (groups > a.heads) groups = a.heads;
+  const int64_t threads = rows * groups * lanes;
+  if ((threads + 255) / 256 > UINT32_MAX) return WMX_E_UNSUPPORTED;
   const dim3 grid((unsigned)((threads + 255) / 256));
   const bool kb = a.key_dtype == WMX_DTYPE_BF16;
   if (a.head_dim == 64) {
-    if (kb) launch_kv_store_d<64, true>(a, rows, grid, stream);
-    else launch_kv_store_d<64, false>(a, rows, grid, stream);
+    if (kb) launch_kv_store_d<64, true>(a, rows, (int)groups, grid, stream);
+    else launch_kv_store_d<64, false>(a, rows, (int)groups, grid, stream);
   } else if (a.head_dim == 96) {
-    if (kb) launch_kv_store_d<96, true>(a, rows, grid, stream);
-    else launch_kv_store_d<96, false>(a, rows, grid, stream);
+    if (kb) launch_kv_store_d<96, true>(a, rows, (int)groups, grid, stream);
+    else launch_kv_store_d<96, false>(a, rows, (int)groups, grid, stream);
   } else if (a.head_dim == 128) {
-    if (kb) launch_kv_store_d<128, true>(a, rows, grid, stream);
-    else launch_kv_store_d<128, false>(a, rows, grid, stream);
+    if (kb) launch_kv_store_d<128, true>(a, rows, (int)groups, grid, stream);
+    else launch_kv_store_d<128, false>(a, rows, (int)groups, grid, stream);
   } else {
     return WMX_E_UNSUPPORTED;
   }

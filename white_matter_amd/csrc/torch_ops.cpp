@@ -794,16 +794,22 @@ struct DecodeCounters {
 };
 DecodeCounters g_decode_counters;
 
-Tensor strict_decode(const Tensor& query, const Tensor& key, const Tensor& value,
-                     const c10::optional<Tensor>& query_start, int64_t query_start_value,
-                     const c10::optional<Tensor>& kv_lengths, const c10::optional<Tensor>& key_mask, bool use_dummy,
-                     double scale, int64_t num_splits) {
+// One query token per row into out (B, 1, H, D) bf16, any strides with a unit
+// head_dim stride.
+void decode_into(const Tensor& out, const Tensor& query, const Tensor& key, const Tensor& value,
+                 const c10::optional<Tensor>& query_start, int64_t query_start_value,
+                 const c10::optional<Tensor>& kv_lengths, const c10::optional<Tensor>& key_mask, bool use_dummy,
+                 double scale, int64_t num_splits) {
   check_strict_shapes(query, key, value);
   TORCH_CHECK_VALUE(query.size(2) == 1, "strict_decode takes one query token per row");
   c10::OptionalDeviceGuard guard(query.device());
   const Tensor q = operand(query), k = operand(key), v = operand(value);
   const int64_t batch = q.size(0), heads = q.size(1), dim = q.size(3);
-  Tensor out = at::empty({batch, 1, heads, dim}, q.options());
+  TORCH_CHECK_VALUE(out.scalar_type() == at::kBFloat16 && out.device() == q.device() && out.dim() == 4 &&
+                        out.size(0) == batch && out.size(1) == 1 && out.size(2) == heads && out.size(3) == dim &&
+                        out.stride(3) == 1,
+                    "strict_decode_out: out must be a bf16 (B, 1, H, D) tensor on the query's device with a unit "
+                    "head_dim stride");
   const Tensor o = out.select(1, 0);
   wmx_decode_args a;
   std::memset(&a, 0, sizeof(a));
@@ -847,7 +853,27 @@ Tensor strict_decode(const Tensor& query, const Tensor& key, const Tensor& value
   a.workspace = workspace.data_ptr();
   a.workspace_bytes = need;
   check_rc(wmx_decode(&a, stream_of(q)), "wmx_decode");
+}
+
+Tensor strict_decode(const Tensor& query, const Tensor& key, const Tensor& value,
+                     const c10::optional<Tensor>& query_start, int64_t query_start_value,
+                     const c10::optional<Tensor>& kv_lengths, const c10::optional<Tensor>& key_mask, bool use_dummy,
+                     double scale, int64_t num_splits) {
+  check_strict_shapes(query, key, value);
+  Tensor out = at::empty({query.size(0), 1, query.size(1), query.size(3)}, query.options().dtype(at::kBFloat16));
+  decode_into(out, query, key, value, query_start, query_start_value, kv_lengths, key_mask, use_dummy, scale,
+              num_splits);
   return out;
+}
+
+// The same into a caller's buffer (a decode loop's output rows, so the loop
+// needs no stacking copy).
+void strict_decode_out(const Tensor& out, const Tensor& query, const Tensor& key, const Tensor& value,
+                       const c10::optional<Tensor>& query_start, int64_t query_start_value,
+                       const c10::optional<Tensor>& kv_lengths, const c10::optional<Tensor>& key_mask, bool use_dummy,
+                       double scale, int64_t num_splits) {
+  decode_into(out, query, key, value, query_start, query_start_value, kv_lengths, key_mask, use_dummy, scale,
+              num_splits);
 }
 
 // ------------------------------------------------- strict autograd ----
@@ -987,6 +1013,10 @@ TORCH_LIBRARY_FRAGMENT(white_matter, m) {
   m.def(
       "strict_decode(Tensor query, Tensor key, Tensor value, Tensor? query_start, int query_start_value, "
       "Tensor? kv_lengths, Tensor? key_mask, bool use_dummy, float scale, int num_splits) -> Tensor");
+  m.def(
+      "strict_decode_out(Tensor(a!) out, Tensor query, Tensor key, Tensor value, Tensor? query_start, "
+      "int query_start_value, Tensor? kv_lengths, Tensor? key_mask, bool use_dummy, float scale, int num_splits) "
+      "-> ()");
   m.def("_packed_plan_cache_size() -> int", &packed_plan_cache_size);
   m.def("_packed_plan_cache_clear() -> ()", &packed_plan_cache_clear);
 }
@@ -1001,6 +1031,7 @@ TORCH_LIBRARY_IMPL(white_matter, CUDA, m) {
   m.impl("strict_dense_fwd", &strict_dense_fwd);
   m.impl("strict_dense_bwd", &strict_dense_bwd);
   m.impl("strict_decode", &strict_decode);
+  m.impl("strict_decode_out", &strict_decode_out);
 }
 
 TORCH_LIBRARY_IMPL(white_matter, Autograd, m) {

@@ -26,8 +26,8 @@ from collections.abc import Sequence
 
 import torch
 
-from . import kv_pool
-from .strict_causal_attention import strict_causal_attention
+from . import _kernels, kv_pool
+from .strict_causal_attention import strict_causal_attention, strict_decode_out
 
 
 class DecodeLoop:
@@ -40,7 +40,8 @@ class DecodeLoop:
         included); the next token is written there.
     layer_channels: the pool channel each layer reads.
     k_norm_weight: (k, D) per-channel key-norm weight.
-    cos_table, sin_table: (N, D) RoPE rows by slot.
+    cos_table, sin_table: (N, D) RoPE rows by slot (copied into one table at
+        construction, so one gather serves both).
     Inputs per call (static buffers, copied in by `__call__`): `query`
     (L, B, Hq, 1, D) bf16, `new_key` / `new_value` (B, k, Hkv, 1, D) raw
     projections. Output: `output` (L, B, 1, Hq, D) bf16.
@@ -93,9 +94,18 @@ class DecodeLoop:
         self.new_key = torch.zeros(batch, channels, kv_heads, 1, dim, device=device, dtype=torch.bfloat16)
         self.new_value = torch.zeros_like(self.new_key)
         self._storage = (keys.data_ptr(), values.data_ptr(), cumulative_length.data_ptr())
+        # cos and sin rows side by side: one gather per token serves both
+        self._rope = torch.stack((cos_table, sin_table), 1)
+        # the layers write their outputs here directly where the kernels take
+        # this head_dim (no stacking copy); otherwise through the public API
+        self._direct = _kernels.kernel_head_dim(dim) == dim
+        self._out = torch.empty(layers, batch, 1, query_heads, dim, device=device, dtype=torch.bfloat16)
 
         snapshot = cumulative_length.clone()
-        stream = torch.cuda.Stream(device=device)
+        # warm-up and capture on one stream the loop keeps: the decode
+        # operator's split-merge counters belong to a stream, so the graph
+        # then records no counter initialisation
+        stream = self._stream = torch.cuda.Stream(device=device)
         stream.wait_stream(torch.cuda.current_stream(device))
         with torch.cuda.stream(stream):
             for _ in range(warmup):
@@ -103,7 +113,7 @@ class DecodeLoop:
                 cumulative_length.copy_(snapshot)
         torch.cuda.current_stream(device).wait_stream(stream)
         self.graph = torch.cuda.CUDAGraph()
-        with torch.cuda.graph(self.graph):
+        with torch.cuda.graph(self.graph, stream=stream):
             self.output = self.step()
         cumulative_length.copy_(snapshot)
         torch.cuda.current_stream(device).synchronize()
@@ -113,28 +123,35 @@ class DecodeLoop:
         graph holds): returns (L, B, 1, Hq, D)."""
         batch, _, _, dim = self.keys.shape
         offset = int(self.use_dummy_token)
-        # real keys before this token, per the reference's lengths; one (B,) copy shared by all layers
-        lengths = (self.cumulative_length - offset).expand(batch).contiguous()
+        # real keys before this token, per the reference's lengths; one (B,) tensor shared by all layers
+        lengths = self.cumulative_length.expand(batch) - offset
         outs = []
         h = self._kv_heads
         for layer, channel in enumerate(self.layer_channels):
             k = self.keys[:, channel * h : (channel + 1) * h]
             v = self.values[:, channel * h : (channel + 1) * h]
-            outs.append(
-                strict_causal_attention(
-                    self.query[layer], k, v, query_start=lengths, kv_lengths=lengths,
-                    use_dummy_token=self.use_dummy_token, softmax_scale=self.scale,
+            if self._direct:
+                strict_decode_out(
+                    self._out[layer], self.query[layer], k, v, lengths, 0, lengths, None, self.use_dummy_token,
+                    self.scale, 0,
                 )
-            )
+            else:
+                outs.append(
+                    strict_causal_attention(
+                        self.query[layer], k, v, query_start=lengths, kv_lengths=lengths,
+                        use_dummy_token=self.use_dummy_token, softmax_scale=self.scale,
+                    )
+                )
         slot = self.cumulative_length
-        cos = self.cos_table.index_select(0, slot).expand(batch, 1, dim)
-        sin = self.sin_table.index_select(0, slot).expand(batch, 1, dim)
+        rope = self._rope.index_select(0, slot)  # (1, 2, D): the slot's cos and sin rows
+        cos = rope[:, 0].expand(batch, 1, dim)
+        sin = rope[:, 1].expand(batch, 1, dim)
         pool = (self.keys.unflatten(1, (self._channels, h)), self.values.unflatten(1, (self._channels, h)))
         kv_pool.write_pool(
             self.new_key, self.new_value, self.k_norm_weight, cos, sin, pool[0], pool[1], slot, eps=self.eps
         )
         self.cumulative_length.add_(1)
-        return torch.stack(outs)
+        return self._out if self._direct else torch.stack(outs)
 
     @torch.no_grad()
     def __call__(

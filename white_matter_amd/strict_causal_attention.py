@@ -793,12 +793,17 @@ def _fake_decode(query, *args):
     return query.new_empty(batch, 1, heads, dim, dtype=torch.bfloat16)
 
 
+def _fake_decode_out(out, query, *args):
+    return None
+
+
 for _name, _fake in (
     ("strict_packed_fwd", _fake_packed_fwd),
     ("strict_packed_bwd", _fake_grads),
     ("strict_dense_fwd", _fake_packed_fwd),
     ("strict_dense_bwd", _fake_grads),
     ("strict_decode", _fake_decode),
+    ("strict_decode_out", _fake_decode_out),
 ):
     torch.library.register_fake(f"white_matter::{_name}", _fake)
 
@@ -819,6 +824,9 @@ strict_dense_bwd = torch.ops.white_matter.strict_dense_bwd
 #     key_mask, use_dummy, scale, num_splits) -> (B, 1, H, D) bf16: one query
 #     token per row over the KV pool (no gradient)
 strict_decode = torch.ops.white_matter.strict_decode
+# strict_decode_out(out, query, key, value, ...same as strict_decode) -> ():
+#     the same into out (B, 1, H, D) bf16 with a unit head_dim stride
+strict_decode_out = torch.ops.white_matter.strict_decode_out
 
 
 # ------------------------------------------------------------ public API ----

@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 11
+#define WMX_ABI_VERSION 12
 
 enum {
   WMX_OK = 0,
@@ -226,6 +226,9 @@ typedef struct wmx_decode_args {
    * bit-identical. Calls that share counters must not overlap (calls in
    * order on one stream do not). */
   int32_t* counters;
+  /* Nonzero: query_start[0] and kv_lengths[0] hold every row's values (a
+   * pool's one shared length read in place, without a per-row copy). */
+  int32_t lengths_broadcast;
 } wmx_decode_args;
 
 /*
@@ -274,6 +277,10 @@ typedef struct wmx_kv_store_args {
   int32_t head_dim;          /* 64, 96 or 128 */
   int32_t pool_slots;        /* N */
   float eps;
+  /* Nonzero: cos and sin are (N, D) tables of rows by pool slot, and token t
+   * of every batch row reads row slots[t] (rope_stride[1] apart; rope_stride[0]
+   * is unused), so a decode step needs no gather of its rows. */
+  int32_t rope_by_slot;
 } wmx_kv_store_args;
 
 /*

@@ -206,3 +206,35 @@ def test_merge_by_last_split_matches_combine_kernel(batch, kv_heads, group, dim)
         assert torch.equal(merged[:, 0], combined)
     expected = ref.strict_attention(q.cpu(), k.cpu(), v.cpu(), query_start=lengths.cpu(), kv_lengths=lengths.cpu())
     assert_bf16_close(merged, expected, what="last-split merge")
+
+
+@pytest.mark.parametrize(("batch", "kv_heads", "group", "dim"), [(8, 8, 2, 64), (5, 3, 4, 128), (1, 2, 1, 96)])
+@torch.no_grad()
+def test_shared_length_and_decode_out(batch, kv_heads, group, dim):
+    """A one-element length tensor serves every row in place (the operator
+    passes it to wmx_decode with lengths_broadcast instead of copying it per
+    row) and strict_decode_out writes into a caller's buffer: both give the
+    per-row call's bits; a length tensor of another size is refused."""
+    from white_matter_amd.strict_causal_attention import strict_decode, strict_decode_out
+
+    gen = torch.Generator().manual_seed(batch + 10 * kv_heads + dim)
+    heads, capacity = kv_heads * group, 1153
+    q = _normal((batch, heads, 1, dim), gen, dim)
+    k = _normal((batch, kv_heads, capacity, dim), gen, dim)
+    v = _normal((batch, kv_heads, capacity, dim), gen, dim)
+    for length in (1, 700, capacity):
+        print(f"shared length B={batch} Hkv={kv_heads} G={group} D={dim} length {length}", flush=True)
+        one = torch.tensor([length], device=DEV)
+        rows = one.expand(batch).contiguous()
+        want = strict_decode(q, k, v, rows, 0, rows, None, False, dim**-0.5, 0)
+        got = strict_decode(q, k, v, one, 0, one, None, False, dim**-0.5, 0)
+        assert torch.equal(got, want), f"length {length}: shared length differs from per-row lengths"
+        out = torch.full((2, batch, 1, heads, dim), float("nan"), device=DEV, dtype=torch.bfloat16)
+        strict_decode_out(out[1], q, k, v, one, 0, one, None, False, dim**-0.5, 0)
+        assert torch.equal(out[1], want) and bool(out[0].isnan().all())
+        # the dummy-slot form of the same visible length: length - 1 real keys plus the dummy
+        dummy = strict_decode(q, k, v, rows - 1, 0, rows - 1, None, True, dim**-0.5, 0)
+        assert torch.equal(dummy, want)
+    if batch > 1:
+        with pytest.raises(ValueError, match="kv_lengths"):
+            strict_decode(q, k, v, rows, 0, one, None, False, dim**-0.5, 0)

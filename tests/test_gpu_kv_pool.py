@@ -258,6 +258,34 @@ def test_producer_rejects_autograd_and_bad_shapes():
 
 
 @pytest.mark.parametrize("dim", [64, 96, 128])
+@pytest.mark.parametrize("rope_dtype", [torch.float32, torch.bfloat16])
+@torch.no_grad()
+def test_store_rope_by_slot_equals_gathered_rows(dim, rope_dtype):
+    """write_pool(rope_by_slot=True) reads each token's cos/sin row at its
+    pool slot from (N, D) tables: the same bits as the gathered (B, T, D)
+    rows, for one decode token and for several tokens; slots past the pool
+    are not written either way."""
+    gen = torch.Generator().manual_seed(dim)
+    batch, channels, heads, capacity = 3, 2, 5, 40
+    weight = (1 + 0.1 * torch.randn(channels, dim, generator=gen)).to(DEV)
+    cos = torch.randn(capacity, dim, generator=gen).to(DEV, rope_dtype)
+    sin = torch.randn(capacity, dim, generator=gen).to(DEV, rope_dtype)
+    for slots in ([17], [3, 9, 38, 0], [39, 40]):
+        print(f"rope by slot D={dim} {rope_dtype} slots {slots}", flush=True)
+        slot_t = torch.tensor(slots, device=DEV)
+        tokens = len(slots)
+        key = torch.randn(batch, channels, heads, tokens, dim, generator=gen).to(DEV, torch.bfloat16)
+        value = torch.randn(batch, channels, heads, tokens, dim, generator=gen).to(DEV, torch.bfloat16)
+        pools = [torch.zeros(2, batch, channels, heads, capacity, dim, device=DEV, dtype=torch.bfloat16) for _ in range(2)]
+        rows = slot_t.clamp(max=capacity - 1)
+        kv_pool.write_pool(key, value, weight, cos[rows].expand(batch, tokens, dim), sin[rows].expand(batch, tokens, dim),
+                           pools[0][0], pools[0][1], slot_t)
+        kv_pool.write_pool(key, value, weight, cos, sin, pools[1][0], pools[1][1], slot_t, rope_by_slot=True)
+        assert torch.equal(pools[0], pools[1])
+        assert bool(pools[1][:, :, :, :, slot_t[slot_t < capacity]].ne(0).any())
+
+
+@pytest.mark.parametrize("dim", [64, 96, 128])
 @pytest.mark.parametrize("key_dtype", [torch.float32, torch.bfloat16])
 def test_k_norm_rope_backward_matches_oracle(dim, key_dtype):
     """white_matter::k_norm_rope's backward (wmx_kv_store_bwd) against float64

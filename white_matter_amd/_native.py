@@ -19,7 +19,7 @@ import torch
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
 # the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
 OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -118,6 +118,7 @@ class DecodeArgs(ctypes.Structure):
         ("num_splits", ctypes.c_int32),
         ("softmax_scale", ctypes.c_float),
         ("counters", _vp),
+        ("lengths_broadcast", ctypes.c_int32),
     ]
 
 
@@ -234,6 +235,7 @@ class KvStoreArgs(ctypes.Structure):
         ("head_dim", ctypes.c_int32),
         ("pool_slots", ctypes.c_int32),
         ("eps", ctypes.c_float),
+        ("rope_by_slot", ctypes.c_int32),
     ]
 
 

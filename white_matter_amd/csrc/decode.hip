@@ -47,9 +47,10 @@ struct DecodeLen {
 };
 
 __device__ __forceinline__ DecodeLen decode_len(const wmx_decode_args& a, int b) {
-  const int64_t start = a.query_start ? a.query_start[b] : a.query_start_scalar;
+  const int rb = a.lengths_broadcast ? 0 : b;
+  const int64_t start = a.query_start ? a.query_start[rb] : a.query_start_scalar;
   int64_t bound = start;
-  if (a.kv_lengths) bound = min(bound, a.kv_lengths[b]);
+  if (a.kv_lengths) bound = min(bound, a.kv_lengths[rb]);
   DecodeLen r;
   if (a.key_mask) {
     r.len = bound + a.use_dummy;

@@ -55,7 +55,8 @@ __global__ __launch_bounds__(256) void kv_store_kernel(const wmx_kv_store_args a
 
   float w[8], cs[8], sn[8];
   load8(a.k_norm_weight, (int64_t)c * D + dl, a.weight_dtype == WMX_DTYPE_BF16, w);
-  const int64_t ro = (int64_t)b * a.rope_stride[0] + (int64_t)t * a.rope_stride[1] + dl;
+  const int64_t ro = a.rope_by_slot ? (slot_ok ? slot : 0) * a.rope_stride[1] + dl
+                                    : (int64_t)b * a.rope_stride[0] + (int64_t)t * a.rope_stride[1] + dl;
   load8(a.cos, ro, a.rope_dtype == WMX_DTYPE_BF16, cs);
   load8(a.sin, ro, a.rope_dtype == WMX_DTYPE_BF16, sn);
 #pragma unroll

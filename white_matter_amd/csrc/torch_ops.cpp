@@ -824,16 +824,26 @@ void decode_into(const Tensor& out, const Tensor& query, const Tensor& key, cons
   a.o_stride[0] = o.stride(0);
   a.o_stride[1] = o.stride(1);
   Tensor starts, lengths;
+  // one value for every row (a pool's shared length) is read in place by
+  // all rows rather than copied out per row
+  const bool shared = batch > 1 && query_start && query_start->numel() == 1 &&
+                      (!kv_lengths || kv_lengths->numel() == 1);
   if (query_start) {
-    starts = query_start->to(q.device(), at::kLong).expand({batch}).contiguous();
+    TORCH_CHECK_VALUE(query_start->numel() == 1 || query_start->numel() == batch,
+                      "query_start must hold one value or one per batch row");
+    starts = query_start->to(q.device(), at::kLong);
+    starts = (shared ? starts.reshape({1}) : starts.expand({batch})).contiguous();
     a.query_start = starts.data_ptr<int64_t>();
   } else {
     a.query_start_scalar = query_start_value;
   }
   if (kv_lengths) {
-    lengths = kv_lengths->to(q.device(), at::kLong).contiguous();
+    TORCH_CHECK_VALUE(kv_lengths->numel() == batch || (shared && kv_lengths->numel() == 1),
+                      "kv_lengths must hold one value per batch row");
+    lengths = kv_lengths->to(q.device(), at::kLong).reshape({-1}).contiguous();
     a.kv_lengths = lengths.data_ptr<int64_t>();
   }
+  a.lengths_broadcast = shared ? 1 : 0;
   const Tensor mask = mask_bytes(key_mask);
   if (mask.defined()) {
     a.key_mask = mask.data_ptr<uint8_t>();

@@ -40,8 +40,8 @@ class DecodeLoop:
         included); the next token is written there.
     layer_channels: the pool channel each layer reads.
     k_norm_weight: (k, D) per-channel key-norm weight.
-    cos_table, sin_table: (N, D) RoPE rows by slot (copied into one table at
-        construction, so one gather serves both).
+    cos_table, sin_table: (N, D) RoPE rows by slot (the store reads the
+        token's row at its slot).
     Inputs per call (static buffers, copied in by `__call__`): `query`
     (L, B, Hq, 1, D) bf16, `new_key` / `new_value` (B, k, Hkv, 1, D) raw
     projections. Output: `output` (L, B, 1, Hq, D) bf16.
@@ -94,8 +94,6 @@ class DecodeLoop:
         self.new_key = torch.zeros(batch, channels, kv_heads, 1, dim, device=device, dtype=torch.bfloat16)
         self.new_value = torch.zeros_like(self.new_key)
         self._storage = (keys.data_ptr(), values.data_ptr(), cumulative_length.data_ptr())
-        # cos and sin rows side by side: one gather per token serves both
-        self._rope = torch.stack((cos_table, sin_table), 1)
         # the layers write their outputs here directly where the kernels take
         # this head_dim (no stacking copy); otherwise through the public API
         self._direct = _kernels.kernel_head_dim(dim) == dim
@@ -123,17 +121,21 @@ class DecodeLoop:
         graph holds): returns (L, B, 1, Hq, D)."""
         batch, _, _, dim = self.keys.shape
         offset = int(self.use_dummy_token)
-        # real keys before this token, per the reference's lengths; one (B,) tensor shared by all layers
-        lengths = self.cumulative_length.expand(batch) - offset
         outs = []
         h = self._kv_heads
+        if not self._direct:
+            # real keys before this token, per the reference's lengths; one (B,) tensor shared by all layers
+            lengths = self.cumulative_length.expand(batch) - offset
         for layer, channel in enumerate(self.layer_channels):
             k = self.keys[:, channel * h : (channel + 1) * h]
             v = self.values[:, channel * h : (channel + 1) * h]
             if self._direct:
+                # the decode sees slots [0, length) with length = real keys +
+                # the dummy: the counter itself, read in place by every row
+                # (the dummy then needs no separate term)
                 strict_decode_out(
-                    self._out[layer], self.query[layer], k, v, lengths, 0, lengths, None, self.use_dummy_token,
-                    self.scale, 0,
+                    self._out[layer], self.query[layer], k, v, self.cumulative_length, 0, self.cumulative_length,
+                    None, False, self.scale, 0,
                 )
             else:
                 outs.append(
@@ -143,12 +145,10 @@ class DecodeLoop:
                     )
                 )
         slot = self.cumulative_length
-        rope = self._rope.index_select(0, slot)  # (1, 2, D): the slot's cos and sin rows
-        cos = rope[:, 0].expand(batch, 1, dim)
-        sin = rope[:, 1].expand(batch, 1, dim)
         pool = (self.keys.unflatten(1, (self._channels, h)), self.values.unflatten(1, (self._channels, h)))
         kv_pool.write_pool(
-            self.new_key, self.new_value, self.k_norm_weight, cos, sin, pool[0], pool[1], slot, eps=self.eps
+            self.new_key, self.new_value, self.k_norm_weight, self.cos_table, self.sin_table, pool[0], pool[1], slot,
+            eps=self.eps, rope_by_slot=True,
         )
         self.cumulative_length.add_(1)
         return self._out if self._direct else torch.stack(outs)

@@ -61,6 +61,7 @@ def write_pool(
     slots: torch.Tensor,
     *,
     eps: float = 1e-6,
+    rope_by_slot: bool = False,
 ) -> None:
     """keys[:, :, :, slots] = bf16(rope(rms_norm(key) * k_norm_weight)) and
     values[:, :, :, slots] = bf16(value), in place.
@@ -68,7 +69,9 @@ def write_pool(
     key/value (B, C, H, T, D) float32 or bfloat16 (the KV pool's projected
     channels), k_norm_weight (C, D), cos/sin (B, T, D) (the group's position
     embeddings), keys/values bf16 pool tensors or views (B, C, H, N, D),
-    slots (T,) int64 distinct pool slots. head_dim 64, 96 or 128.
+    slots (T,) int64 distinct pool slots. head_dim 64, 96 or 128. With
+    rope_by_slot, cos/sin are (N, D) tables of rows by pool slot and token t
+    uses row slots[t] of them (a decode step then gathers nothing).
     """
     if torch.is_grad_enabled() and any(t is not None and t.requires_grad for t in (key, value, k_norm_weight, cos, sin)):
         raise RuntimeError("write_pool is forward-only; under autograd produce the keys with k_norm_rope")
@@ -79,7 +82,10 @@ def write_pool(
         raise ValueError(f"head_dim {dim} is not supported (64, 96 or 128)")
     if k_norm_weight.shape != (channels, dim):
         raise ValueError("k_norm_weight must be (C, D)")
-    if cos.shape != (batch, tokens, dim) or sin.shape != cos.shape or sin.dtype != cos.dtype:
+    if rope_by_slot:
+        if cos.shape != (keys.shape[3], dim) or sin.shape != cos.shape or sin.dtype != cos.dtype:
+            raise ValueError("with rope_by_slot, cos and sin must be (N, D) tables of one dtype")
+    elif cos.shape != (batch, tokens, dim) or sin.shape != cos.shape or sin.dtype != cos.dtype:
         raise ValueError("cos and sin must be (B, T, D) of one dtype")
     if keys.ndim != 5 or keys.shape[:3] != (batch, channels, heads) or keys.shape[4] != dim or keys.dtype != torch.bfloat16:
         raise ValueError("keys must be a bf16 (B, C, H, N, D) pool")
@@ -103,7 +109,9 @@ def write_pool(
         a.value, a.value_stride, a.value_dtype = value.data_ptr(), value.stride()[:4], _dtype(value, "value")
         a.value_pool, a.value_pool_stride = values.data_ptr(), values.stride()[:4]
     a.k_norm_weight, a.weight_dtype = weight.data_ptr(), _dtype(weight, "k_norm_weight")
-    a.cos, a.sin, a.rope_stride, a.rope_dtype = cos.data_ptr(), sin.data_ptr(), cos.stride()[:2], _dtype(cos, "cos")
+    rope_stride = (0, cos.stride(0)) if rope_by_slot else cos.stride()[:2]
+    a.cos, a.sin, a.rope_stride, a.rope_dtype = cos.data_ptr(), sin.data_ptr(), rope_stride, _dtype(cos, "cos")
+    a.rope_by_slot = int(rope_by_slot)
     a.key_pool, a.key_pool_stride = keys.data_ptr(), keys.stride()[:4]
     a.slots = slots.data_ptr()
     a.batch, a.channels, a.heads, a.tokens, a.head_dim = batch, channels, heads, tokens, dim

@@ -9,8 +9,9 @@
 //  backward_key_value.py:102-132, backward_preprocess.py:34-49).
 //
 // Deterministic kernels, no atomics on the dense paths:
-//   dKV : key-parallel (128 keys, 8 waves), loops over the query heads of the
-//         KV head and over the query tiles of 64 that can see the key tile;
+//   dKV : key-parallel (128 keys and 8 waves, or 64 keys and 4 waves), loops
+//         over the query heads of the KV head and over the query tiles of 32
+//         that can see the key tile;
 //         a lane owns one key column of S = Q K^T; dV^T = dO^T P and
 //         dK^T = Q^T dS accumulate in registers. With a dS buffer in the
 //         workspace it also stores dS^T (bf16, the value its dK product

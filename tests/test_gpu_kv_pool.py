@@ -246,11 +246,44 @@ def test_router_logits_match_fp32_product(rows, inputs, logits):
     assert torch.equal(torch.ops.white_matter.kv_router(p, w[0], b[0], w[1], b[1]), alpha)
 
 
-def test_producer_rejects_autograd_and_bad_shapes():
+@pytest.mark.parametrize(("sources", "hidden", "channels", "stride"), [(5, 64, 3, 1), (9, 128, 4, 2)])
+def test_producer_training_form_gradients(sources, hidden, channels, stride):
+    """Under autograd projection_inputs runs the HIP forward (the same bits as
+    without autograd) and the backward differentiates the recomputed eager
+    steps: gradients of every input against float64 autograd through the
+    oracle (bf16 rounding points as casts, which pass gradients through)."""
+    inputs = _producer_inputs(2, 4, sources, hidden, channels, 40 + sources, torch.float32, torch.float32,
+                              stride=stride)
+    stacked, pre_mix, router, gain = inputs
+    leaves = [stacked.to(DEV), pre_mix[0].to(DEV), pre_mix[1].to(DEV), router[0][0].to(DEV), router[0][1].to(DEV),
+              router[1][0].to(DEV), router[1][1].to(DEV), gain[0].to(DEV), gain[1].to(DEV)]
+    leaves = [t.clone().requires_grad_() for t in leaves]
+    hk, hv = kv_pool.projection_inputs(
+        leaves[0], (leaves[1], leaves[2]), ((leaves[3], leaves[4]), (leaves[5], leaves[6])), (leaves[7], leaves[8]),
+        eps=1e-6, mix_eps=1e-4, router_layer_stride=stride,
+    )
+    with torch.no_grad():
+        plain = _hip_inputs(*inputs, stride=stride)
+    assert torch.equal(hk, plain[0]) and torch.equal(hv, plain[1]), "the training form's forward is the HIP forward"
+    gen = torch.Generator().manual_seed(7)
+    gk = torch.randn(hk.shape, generator=gen)
+    gv = torch.randn(hv.shape, generator=gen)
+    grads = torch.autograd.grad((hk, hv), leaves, (gk.to(DEV, hk.dtype), gv.to(DEV, hv.dtype)))
+    ref_leaves = [t.detach().cpu().double().requires_grad_() for t in leaves]
+    want = ref.projection_inputs(
+        ref_leaves[0], torch.stack(ref_leaves[1:3]), ((ref_leaves[3], ref_leaves[4]), (ref_leaves[5], ref_leaves[6])),
+        torch.stack(ref_leaves[7:9]), 1e-6, 1e-4, stride,
+    )
+    ref_grads = torch.autograd.grad(want, ref_leaves, torch.stack((gk, gv)).double())
+    names = ("stacked", "pre_mix_k", "pre_mix_v", "router_w_k", "router_b_k", "router_w_v", "router_b_v", "gain_k", "gain_v")
+    for name, g, r in zip(names, grads, ref_grads):
+        err = (g.double().cpu() - r).norm() / r.norm().clamp_min(1e-30)
+        assert err <= 2e-2, f"{name}: rel-L2 {err:.3e} against float64 autograd of the oracle"
+
+
+def test_producer_rejects_bad_shapes():
     stacked, pre_mix, router, gain = _producer_inputs(1, 2, 3, 64, 2, 0, torch.float32, torch.float32)
     args = (tuple(pre_mix.to(DEV)), tuple((w.to(DEV), b.to(DEV)) for w, b in router), tuple(gain.to(DEV)))
-    with pytest.raises(RuntimeError, match="forward-only"):
-        kv_pool.projection_inputs(stacked.to(DEV).requires_grad_(), *args)
     with torch.no_grad(), pytest.raises(ValueError, match="multiples of 8"):
         kv_pool.projection_inputs(stacked[..., :60].to(DEV), tuple(p[:, :60] for p in args[0]), args[1], args[2])
     with torch.no_grad(), pytest.raises(ValueError, match="pre_mix"):

@@ -162,6 +162,50 @@ def test_producer_oracle_matches_reference_formulation(scale, logit_scale):
     assert _close_in_bf16(actual, expected)
 
 
+@pytest.mark.parametrize("stride", [1, 2])
+def test_training_recompute_matches_oracle_values_and_gradients(stride):
+    """The training form's backward differentiates kv_pool's eager recompute
+    of the producer (CPU here): its values equal the oracle's but for rare
+    bf16 roundings, and its gradients match float64 autograd through the
+    oracle (bf16 rounding points as casts, which pass gradients through). A
+    recompute with the two eps values exchanged fails the gradient check."""
+    from white_matter_amd import kv_pool
+
+    stacked, pre_mix, _, gain = _producer_inputs(11, scale=1e-2)
+    sources, hidden, channels = stacked.shape[2], stacked.shape[3], gain.shape[1]
+    read = kv_pool.router_sources(sources, stride)
+    gen = torch.Generator().manual_seed(12)
+    router = tuple(
+        ((torch.randn(channels * sources, len(read) * hidden, generator=gen) * 0.02).bfloat16(),
+         (torch.randn(channels * sources, generator=gen) * 0.25).bfloat16())
+        for _ in range(2)
+    )
+    leaves = [stacked, pre_mix[0], pre_mix[1], router[0][0], router[0][1], router[1][0], router[1][1], gain[0], gain[1]]
+
+    def eager(ts, eps=1e-6, mix_eps=1e-4):
+        return kv_pool._projection_inputs_eager(ts[0], (ts[1], ts[2]), ((ts[3], ts[4]), (ts[5], ts[6])),
+                                                (ts[7], ts[8]), eps, mix_eps, read)
+
+    def oracle(ts):
+        return ref.projection_inputs(ts[0], torch.stack(ts[1:3]), ((ts[3], ts[4]), (ts[5], ts[6])),
+                                     torch.stack(ts[7:9]), 1e-6, 1e-4, stride)
+
+    ours = [t.clone().float().requires_grad_() for t in leaves]
+    theirs = [t.clone().double().requires_grad_() for t in leaves]
+    hk, hv = eager(ours)
+    want = oracle(theirs)
+    assert _close_in_bf16(torch.stack((hk, hv)).double(), want.detach())
+    grad = torch.randn(want.shape, generator=gen)
+    g_ours = torch.autograd.grad((hk, hv), ours, (grad[0].bfloat16(), grad[1].bfloat16()))
+    g_want = torch.autograd.grad(want, theirs, grad.double())
+    for g, r in zip(g_ours, g_want):
+        assert (g.double() - r).norm() <= 2e-2 * r.norm()
+    swapped = [t.clone().float().requires_grad_() for t in leaves]
+    sk, sv = eager(swapped, eps=1e-4, mix_eps=1e-6)
+    g_swapped = torch.autograd.grad((sk, sv), swapped, (grad[0].bfloat16(), grad[1].bfloat16()))
+    assert (g_swapped[0].double() - g_want[0]).norm() > 2e-2 * g_want[0].norm()
+
+
 def test_producer_oracle_routing_prior_closed_form():
     """The reference's "cyclic" prior with C = S and zero router weights
     (routing.py:9-25, 77-80): channel c reads source c with logit 2^-2, so

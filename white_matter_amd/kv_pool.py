@@ -11,7 +11,9 @@ mix norm and the channel gain cast to bf16 and permuted to (channel, token,
 hidden). `projection_inputs` runs that as three HIP steps: wmx_kv_premix, the
 router logits (wmx_kv_router: a split-K MFMA GEMM, since the library GEMM of
 this shape, few logits over long rows, runs on a few workgroups) and
-wmx_kv_mix.
+wmx_kv_mix. Under autograd the same kernels run forward and the backward
+recomputes the eager steps and differentiates them (the reference's
+selective checkpointing of _project).
 
 The reference produces a group's keys with an eager sequence
 (src/white_matter/modules/kv_pool.py:163-172 `_apply_k_norm_rope`, the
@@ -336,6 +338,66 @@ def router_sources(sources: int, layer_stride: int) -> range:
     return range((sources - 1) % layer_stride, sources, layer_stride)
 
 
+def _projection_inputs_eager(stacked, pre_mix, router, gain, eps, mix_eps, read):
+    """The reference's _project steps up to the projection as torch operations
+    (kv_pool.py:103-136, routing.py:108-124), differentiable: the recompute
+    that the training form differentiates, as the reference's selective
+    checkpointing recomputes its eager steps. Values are rounded to bf16 where
+    the reference's bf16 steps round them; the products run in fp32 (their
+    backward then never issues a bf16 batched product over transposed views)."""
+    bf16, f32 = torch.bfloat16, torch.float32
+    batch, tokens, sources, hidden = stacked.shape
+    rows = batch * tokens
+    channels = gain[0].shape[0]
+    x = stacked.to(f32)
+    normed = x * torch.rsqrt(x.pow(2).mean(-1, keepdim=True) + eps)
+    out = []
+    for side in range(2):
+        premixed = (normed * pre_mix[side].to(f32)).to(bf16).reshape(rows, sources, hidden)
+        weight, bias = router[side]
+        context = premixed[:, read.start :: read.step].reshape(rows, -1)
+        logits = (context.to(f32) @ weight.to(bf16).to(f32).t() + bias.to(bf16).to(f32)).to(bf16)
+        mixed = torch.bmm(logits.view(rows, channels, sources).to(f32), premixed.to(f32)).to(bf16)  # (rows, C, d)
+        m = mixed.to(f32)
+        h = (m * torch.rsqrt(m.pow(2).mean(-1, keepdim=True) + mix_eps) * gain[side].to(f32)[None]).to(bf16)
+        out.append(h.permute(1, 0, 2))
+    return out[0], out[1]
+
+
+class _ProjectionInputsFn(torch.autograd.Function):
+    """Training form: the forward runs the HIP kernels; the backward
+    recomputes the reference's eager steps from the saved inputs and
+    differentiates them (the reference trains _project under selective
+    checkpointing with the same recompute)."""
+
+    @staticmethod
+    def forward(ctx, stacked, pre_k, pre_v, w_k, b_k, w_v, b_v, gain_k, gain_v, eps, mix_eps, stride):
+        with torch.no_grad():
+            h_k, h_v = _projection_inputs_hip(
+                stacked, (pre_k, pre_v), ((w_k, b_k), (w_v, b_v)), (gain_k, gain_v), eps, mix_eps, stride
+            )
+        ctx.save_for_backward(stacked, pre_k, pre_v, w_k, b_k, w_v, b_v, gain_k, gain_v)
+        ctx.config = (eps, mix_eps, stride)
+        return h_k, h_v
+
+    @staticmethod
+    def backward(ctx, grad_k, grad_v):
+        saved = ctx.saved_tensors
+        eps, mix_eps, stride = ctx.config
+        with torch.enable_grad():
+            leaves = [t.detach().requires_grad_(need) for t, need in zip(saved, ctx.needs_input_grad)]
+            stacked, pre_k, pre_v, w_k, b_k, w_v, b_v, gain_k, gain_v = leaves
+            outs = _projection_inputs_eager(
+                stacked, (pre_k, pre_v), ((w_k, b_k), (w_v, b_v)), (gain_k, gain_v), eps, mix_eps,
+                router_sources(stacked.shape[2], stride),
+            )
+            pairs = [(o, g) for o, g in zip(outs, (grad_k, grad_v)) if g is not None]
+            wanted = [t for t in leaves if t.requires_grad]
+            grads = iter(torch.autograd.grad([o for o, _ in pairs], wanted, [g for _, g in pairs], allow_unused=True))
+        out = [next(grads) if t.requires_grad else None for t in leaves]
+        return (*out, None, None, None)
+
+
 def projection_inputs(
     stacked: torch.Tensor,
     pre_mix: tuple[torch.Tensor, torch.Tensor],
@@ -360,8 +422,10 @@ def projection_inputs(
       alpha = bf16(p[read sources] . W^T + b)         (HIP, wmx_kv_router)
       m = bf16(sum_s alpha[c, s] * p[s])               (HIP, wmx_kv_mix)
       h = bf16(rms_norm(m, mix_eps) * gain[c])
-    Forward only (the reference's training form runs under checkpointing).
-    The three HIP steps are the operators white_matter::kv_premix,
+    Under autograd (any input requiring grad) the forward still runs the HIP
+    kernels and the backward recomputes the reference's eager steps and
+    differentiates them, as the reference trains _project under selective
+    checkpointing. The three HIP steps are the operators white_matter::kv_premix,
     white_matter::kv_router and white_matter::kv_mix, so the whole function
     traces under torch.compile. Router widths C*S beyond
     _native.KV_ROUTER_MAX_LOGITS, or S*hidden not a multiple of 64, take the
@@ -370,7 +434,16 @@ def projection_inputs(
     if torch.is_grad_enabled() and any(
         t.requires_grad for t in (stacked, *pre_mix, *gain, *router[0], *router[1])
     ):
-        raise RuntimeError("projection_inputs is forward-only; use the reference's eager sequence under autograd")
+        (w_k, b_k), (w_v, b_v) = router
+        return _ProjectionInputsFn.apply(
+            stacked, pre_mix[0], pre_mix[1], w_k, b_k, w_v, b_v, gain[0], gain[1], float(eps), float(mix_eps),
+            int(router_layer_stride),
+        )
+    return _projection_inputs_hip(stacked, pre_mix, router, gain, eps, mix_eps, router_layer_stride)
+
+
+def _projection_inputs_hip(stacked, pre_mix, router, gain, eps, mix_eps, router_layer_stride):
+    """projection_inputs' forward on the HIP kernels (arguments checked here)."""
     if stacked.ndim != 4:
         raise ValueError("stacked must be (B, T, S, hidden)")
     sources, hidden = stacked.shape[2:]

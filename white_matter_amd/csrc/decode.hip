@@ -155,18 +155,19 @@ __device__ __forceinline__ float merge_splits(const float* ws_o, const float* ws
 }
 
 // G query heads of one KV head per workgroup, from head head_offset of the
-// KV head's group on (groups of more than 8 heads run in several launches)
-template <int D, int G>
-__global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args a, int chunk, int head_offset,
+// KV head's group on (groups of more than 8 heads run in several launches);
+// NW waves per workgroup, each taking every NW-th group of key rows
+template <int D, int G, int NW>
+__global__ __launch_bounds__(64 * NW) void decode_split_kernel(const wmx_decode_args a, int chunk, int head_offset,
                                                             int32_t* counters) {
   constexpr int LPR = D <= 64 ? 8 : 16;   // lanes per key row
   constexpr int RPW = 64 / LPR;           // rows per wave load
   // key rows in flight per lane: eight for one head; four for a head group,
   // whose accumulators take the registers (fewer rows, more resident waves)
   constexpr int kDecodeUnroll = G == 1 ? 8 : 4;
-  constexpr int ROWS_ITER = 4 * RPW * kDecodeUnroll;
-  __shared__ float lds_m[4][G], lds_l[4][G];
-  __shared__ __attribute__((aligned(16))) float lds_o[4][G][D];
+  constexpr int ROWS_ITER = NW * RPW * kDecodeUnroll;
+  __shared__ float lds_m[NW][G], lds_l[NW][G];
+  __shared__ __attribute__((aligned(16))) float lds_o[NW][G][D];
 
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int dch = lane % LPR, rslot = lane / LPR;
@@ -217,7 +218,7 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
     bool vis[kDecodeUnroll];
 #pragma unroll
     for (int u = 0; u < kDecodeUnroll; ++u) {
-      const int64_t j = it + (int64_t)(u * 4 + wave) * RPW + rslot;
+      const int64_t j = it + (int64_t)(u * NW + wave) * RPW + rslot;
       bool ok = j < j_end;
       if (ok && dl.masked) ok = kmask[j] != 0;
       vis[u] = ok;
@@ -288,14 +289,14 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
   if (nsplit == 1) {
     // the split is the whole row: merge the 4 waves and write the bf16 output
     // (the same sums the combine kernel would form from one partial)
-    for (int idx = tid; idx < G * D; idx += 256) {
+    for (int idx = tid; idx < G * D; idx += 64 * NW) {
       const int g = idx / D, d = idx % D;
       float mx = kMaxFloor;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) mx = fmaxf(mx, lds_m[w][g]);
+      for (int w = 0; w < NW; ++w) mx = fmaxf(mx, lds_m[w][g]);
       float acc = 0.f, lsum = 0.f;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < NW; ++w) {
         const float s = __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
         acc += lds_o[w][g][d] * s;
         lsum += lds_l[w][g] * s;
@@ -308,20 +309,20 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
   // merge the 4 waves and write the split's partial row
   float* ws_o = (float*)a.workspace;
   float* ws_ml = ws_o + (int64_t)a.batch * a.q_heads * nsplit * D;
-  for (int idx = tid; idx < G * D; idx += 256) {
+  for (int idx = tid; idx < G * D; idx += 64 * NW) {
     const int g = idx / D, d = idx % D;
     float mx = kMaxFloor;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) mx = fmaxf(mx, lds_m[w][g]);
+    for (int w = 0; w < NW; ++w) mx = fmaxf(mx, lds_m[w][g]);
     float acc = 0.f;
 #pragma unroll
-    for (int w = 0; w < 4; ++w) acc += lds_o[w][g][d] * __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
+    for (int w = 0; w < NW; ++w) acc += lds_o[w][g][d] * __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
     const int64_t prow = ((int64_t)b * a.q_heads + h0 + g) * nsplit + split;
     store_partial(ws_o + prow * D + d, acc, counters != nullptr);
     if (d == 0) {
       float lsum = 0.f, mraw = kNegInf;
 #pragma unroll
-      for (int w = 0; w < 4; ++w) {
+      for (int w = 0; w < NW; ++w) {
         lsum += lds_l[w][g] * __builtin_amdgcn_exp2f(lds_m[w][g] - mx);
         mraw = fmaxf(mraw, lds_m[w][g]);
       }
@@ -354,12 +355,12 @@ __global__ __launch_bounds__(256) void decode_split_kernel(const wmx_decode_args
 #pragma unroll
     for (int u = 0; u < 8; ++u) first[u] = u < nsplit ? load_shared(orow + (int64_t)u * D) : 0.f;
   }
-  for (int i = tid; i < G * nsplit * 2; i += 256) {
+  for (int i = tid; i < G * nsplit * 2; i += 64 * NW) {
     const int g = i / (nsplit * 2), r = i - g * nsplit * 2;
     (&ml_lds[g][0][0])[r] = load_shared(ws_ml + (head0 + (int64_t)g * nsplit) * 2 + r);
   }
   __syncthreads();
-  for (int idx = tid; idx < G * D; idx += 256) {
+  for (int idx = tid; idx < G * D; idx += 64 * NW) {
     const int g = idx / D, d = idx % D;
     const float* orow = orow_of(idx);
     float mx = kMaxFloor;
@@ -425,8 +426,18 @@ template <int D, int G>
 static void launch_decode_t(const wmx_decode_args& a, int nsplit, int chunk, int head_offset, hipStream_t stream) {
   const int64_t blocks = (int64_t)nsplit * a.batch * a.kv_heads;  // <= INT32_MAX (checked by the caller)
   int32_t* counters = decode_merges_in_split(a, nsplit) ? a.counters : nullptr;
-  hipLaunchKernelGGL((decode_split_kernel<D, G>), dim3((unsigned)blocks), dim3(256), 0, stream, a, chunk, head_offset,
-                     counters);
+  // Long launches (beyond the in-split merge's 1024 workgroups, so several
+  // rounds per CU) of one head per KV head run eight waves per workgroup:
+  // twice the rows in flight per CU (C4 at Hkv 16: 0.181 -> 0.178 ms; head
+  // pairs measured slower, 0.105 -> 0.108 ms at Hkv 8). Short launches keep
+  // four, whose workgroups all fit in one round (eight-wave workgroups of
+  // ~130 registers fit one per CU).
+  if (G == 1 && blocks > kDecodeMergeBlocks)
+    hipLaunchKernelGGL((decode_split_kernel<D, G, 8>), dim3((unsigned)blocks), dim3(512), 0, stream, a, chunk,
+                       head_offset, counters);
+  else
+    hipLaunchKernelGGL((decode_split_kernel<D, G, 4>), dim3((unsigned)blocks), dim3(256), 0, stream, a, chunk,
+                       head_offset, counters);
 }
 
 // Any group size: up to 8 query heads share one read of each K/V row; larger

@@ -704,7 +704,11 @@ def cyclic_line(device, stride=4, dummy=False):
 def prefill_line(device, seed=1, batch=32, heads=16, dim=128, chunk=256):
     """C4 prefill: a chunk of 256 new queries per row after a cached prefix
     P_b ~ U{512..8192} (query_start = P as a tensor, kv_lengths = P + 256),
-    forward only, FLOPs 4*D*Hq*sum_b sum_i (P_b + i)."""
+    forward only, FLOPs 4*D*Hq*sum_b sum_i (P_b + i). The kernel's work is a
+    fixed cycle count; under sustained load the power manager first lowers
+    the GPU clock (about 2 ms into it) and then settles it, so 30 warm-up calls
+    (about 12 ms) precede the 20 timed ones, which then see the settled clock
+    a long prefill runs at rather than the transient."""
     from white_matter_amd import strict_causal_attention
 
     gen = torch.Generator().manual_seed(seed)
@@ -716,7 +720,7 @@ def prefill_line(device, seed=1, batch=32, heads=16, dim=128, chunk=256):
     start, lengths = prefix.to(device), (prefix + chunk).to(device)
     with torch.no_grad():
         fn = lambda: strict_causal_attention(q, k, v, query_start=start, kv_lengths=lengths)  # noqa: E731
-        for _ in range(3):
+        for _ in range(30):
             fn()
         ms = Timer()(fn, 20)
     pairs = int(prefix.sum()) * chunk + batch * chunk * (chunk - 1) // 2

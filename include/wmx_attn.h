@@ -39,7 +39,7 @@
 extern "C" {
 #endif
 
-#define WMX_ABI_VERSION 12
+#define WMX_ABI_VERSION 13
 
 enum {
   WMX_OK = 0,
@@ -164,6 +164,16 @@ typedef struct wmx_attn_args {
    * CU), or 64 (four waves, two workgroups per CU: one workgroup's setup
    * overlaps the other's tile loop). k_units tiles count in these rows. */
   int32_t key_tile;
+  /* Optional fused backward of short segments (13th ABI revision; varlen,
+   * q_heads == kv_heads, keys_unique 1 or 2, entries of WMX_UNIT_FIELDS ints
+   * as unit_fields): one workgroup per listed segment and head holds all of
+   * its queries (1 .. 128) and computes its dQ, dK and dV in one pass over its
+   * keys (at least one), without the dS buffer. The backward then runs the
+   * key- and query-tiled kernels on k_units and q_units only, which must be
+   * given and must not name the listed segments; the forward ignores f_units.
+   * Heaviest first (most 64-key tiles). */
+  const int32_t* f_units;
+  int32_t num_f_units;
 } wmx_attn_args;
 
 enum {

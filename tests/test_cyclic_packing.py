@@ -116,3 +116,41 @@ def test_arbitrary_metadata_is_refused_or_exact():
         else:
             packed += 1
     assert refused > 0 and packed > 0
+
+
+@pytest.mark.parametrize("dummy", [False, True])
+def test_fused_backward_lists_partition_the_segments(dummy):
+    """The fused backward takes every segment of 1 to 128 queries and at least
+    one key, heaviest first, with the segment's own work-list fields; the
+    tiled dQ and dK/dV lists keep exactly their entries for the other
+    segments, so each query and key tile has one owner."""
+    from white_matter_amd.strict_causal_attention import _FUSED_ROWS, _fused_units, _segment_fields, _work_units
+
+    rng = np.random.default_rng(11 + dummy)
+    for trial in range(6):
+        stride = int(rng.integers(1, 9))
+        batch, length = 2, int(rng.integers(300, 1400))
+        docs = _documents(rng, batch, length, int(rng.integers(20, 400)))
+        groups = [torch.arange(r, length, stride) for r in range(stride)]
+        metas = prepare_feedback_metadata(docs, groups, length + int(dummy), use_dummy_token=dummy)
+        r = int(rng.integers(0, stride))
+        q_len = groups[r].numel()
+        offset = r if dummy else r - 1
+        schedule = _check(metas[r], q_len, length + int(dummy), stride, offset, must_pack=True)
+        if schedule == "empty":
+            continue
+        key_tile = 64 if stride >= 2 else 128
+        q_units, k_units, ds_offsets, _ = _work_units(schedule, stride, query_extent=q_len, key_tile=key_tile)
+        f_units, bq_units, bk_units = _fused_units(schedule, stride, q_len, key_tile)
+        sizes = [(qe - qs, ke - ks) for qs, qe, ks, ke in schedule.segments]
+        fused = [int(s) for s in f_units[:, 0]]
+        assert sorted(fused) == [s for s, (nq, nk) in enumerate(sizes) if 1 <= nq <= _FUSED_ROWS and nk >= 1]
+        tiles = [-(-sizes[s][1] // 64) for s in fused]
+        assert tiles == sorted(tiles, reverse=True), "heaviest first"
+        fields = _segment_fields(schedule, q_len, ds_offsets.cpu())
+        expected = fields.index_select(0, torch.tensor(fused, dtype=torch.long))
+        expected[:, 1] = 0
+        assert torch.equal(f_units.cpu(), expected)
+        for full, rest in ((q_units, bq_units), (k_units, bk_units)):
+            keep = [row for row in full.tolist() if row[0] not in set(fused)]
+            assert rest.tolist() == keep

@@ -19,7 +19,7 @@ import torch
 LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_attn.so"
 # the operators registered from C++ (csrc/torch_ops.cpp), linked against LIBRARY
 OPS_LIBRARY = Path(__file__).resolve().parent / "lib" / "libwmx_torch.so"
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _c_i64_3 = ctypes.c_int64 * 3
 _c_i64_2 = ctypes.c_int64 * 2
@@ -86,6 +86,8 @@ class AttnArgs(ctypes.Structure):
         ("query_tile", ctypes.c_int32),
         ("unit_fields", ctypes.c_int32),
         ("key_tile", ctypes.c_int32),
+        ("f_units", _vp),
+        ("num_f_units", ctypes.c_int32),
     ]
 
 

@@ -1093,6 +1093,21 @@ bool bwd_uses_ds(const wmx_attn_args& a) {
   return ds > 0 && a.workspace && a.workspace_bytes >= bwd_ds_offset(a) + ds;
 }
 
+// keys_unique 2: the segments' dummy marks start at zero; after every kernel
+// that writes dummy parts, the parts are summed in segment order.
+static int launch_dummy_marks_clear(const wmx_attn_args& a, hipStream_t stream) {
+  const int64_t marks = bwd_dummy_mark_bytes(a) / (int64_t)sizeof(int32_t);
+  hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((marks / 4 + 256) / 256)), dim3(256), 0, stream,
+                     (float*)a.workspace, marks);
+  return WMX_OK;
+}
+static int launch_dummy_reduce(const wmx_attn_args& a, hipStream_t stream) {
+  const int cols = (2 * a.kv_heads * a.head_dim + 255) / 256;
+  if ((int64_t)a.batch * cols > UINT32_MAX) return WMX_E_UNSUPPORTED;
+  hipLaunchKernelGGL(dummy_reduce_kernel, dim3((unsigned)(a.batch * cols)), dim3(256), 0, stream, a, cols);
+  return WMX_OK;
+}
+
 template <int D, int MODE>
 static int launch_dq_t(const wmx_attn_args& a, hipStream_t stream) {
   const int64_t qtiles = ((MODE == kVarlen ? a.max_queries : a.q_len) + 127) / 128;
@@ -1118,8 +1133,11 @@ static void launch_dkv_kernel(const wmx_attn_args& a, dim3 grid, hipStream_t str
   }
 }
 
+// dummy_steps: with keys_unique 2, clear the segments' marks first and sum the
+// dummy's parts after (false when the caller brackets several kernels with
+// those steps itself).
 template <int D, int MODE>
-static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
+static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream, bool dummy_steps = true) {
   const int bnk = a.key_tile == 64 ? 64 : 128;
   const int64_t ktiles = ((MODE == kVarlen ? a.max_keys : a.kv_len) + bnk - 1) / bnk;
   const int64_t per_head =
@@ -1131,14 +1149,13 @@ static int launch_dkv_t(const wmx_attn_args& a, hipStream_t stream) {
   const bool ds = bwd_uses_ds(a);
   if (MODE == kVarlen && a.keys_unique == 2) {
     // slot 0 through per-segment parts and an ordered sum, every other row stored directly
-    const int cols = (2 * a.kv_heads * D + 255) / 256;
-    if ((int64_t)a.batch * cols > UINT32_MAX) return WMX_E_UNSUPPORTED;
-    const int64_t marks = bwd_dummy_mark_bytes(a) / (int64_t)sizeof(int32_t);
-    hipLaunchKernelGGL(zero_f32_kernel, dim3((unsigned)((marks / 4 + 256) / 256)), dim3(256), 0, stream,
-                       (float*)a.workspace, marks);
+    if (dummy_steps) {
+      const int rc = launch_dummy_marks_clear(a, stream);
+      if (rc != WMX_OK) return rc;
+    }
     if (ds) launch_dkv_kernel<D, MODE, false, true>(a, grid, stream);
     else launch_dkv_kernel<D, MODE, false, false>(a, grid, stream);
-    hipLaunchKernelGGL(dummy_reduce_kernel, dim3((unsigned)(a.batch * cols)), dim3(256), 0, stream, a, cols);
+    if (dummy_steps) return launch_dummy_reduce(a, stream);
   } else if (MODE == kVarlen && a.keys_unique != 1) {
     // any key row may repeat: every row through fp32 atomics
     const int64_t n = bwd_acc_bytes(a) / (int64_t)sizeof(float);
@@ -1178,8 +1195,28 @@ static int launch_bwd_part(const wmx_attn_args& a, hipStream_t stream, bool dq) 
 int launch_bwd_dq(const wmx_attn_args& a, hipStream_t stream) { return launch_bwd_part(a, stream, true); }
 int launch_bwd_dkv(const wmx_attn_args& a, hipStream_t stream) { return launch_bwd_part(a, stream, false); }
 
+// Listed short segments through the fused kernel, the rest through dK/dV and
+// dQ (the caller's k_units and q_units exclude the listed segments).
+static int launch_bwd_fused(const wmx_attn_args& a, hipStream_t stream) {
+  const bool parts = a.keys_unique == 2;
+  int rc = parts ? launch_dummy_marks_clear(a, stream) : WMX_OK;
+  if (rc == WMX_OK) rc = launch_bwd_seg(a, stream);
+  if (rc == WMX_OK) {
+    switch (a.head_dim) {
+      case 64: rc = launch_dkv_t<64, kVarlen>(a, stream, false); break;
+      case 96: rc = launch_dkv_t<96, kVarlen>(a, stream, false); break;
+      case 128: rc = launch_dkv_t<128, kVarlen>(a, stream, false); break;
+      default: rc = WMX_E_UNSUPPORTED;
+    }
+  }
+  if (rc == WMX_OK) rc = launch_bwd_dq(a, stream);
+  if (rc == WMX_OK && parts) rc = launch_dummy_reduce(a, stream);
+  return rc;
+}
+
 int launch_bwd(const wmx_attn_args& a, hipStream_t stream) {
   int rc = launch_bwd_preprocess(a, stream);
+  if (rc == WMX_OK && a.f_units && a.num_f_units > 0) return launch_bwd_fused(a, stream);
   if (bwd_uses_ds(a)) {
     // dQ reads the dS that the dK/dV kernel stores
     if (rc == WMX_OK) rc = launch_bwd_dkv(a, stream);

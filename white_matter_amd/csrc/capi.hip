@@ -71,8 +71,22 @@ int check_common(const wmx_attn_args* a, bool backward) {
     if (a->k_units && a->num_k_units < 0) return fail(WMX_E_INVALID, "negative work-list length");
     if (a->keys_unique < 0 || a->keys_unique > 2) return fail(WMX_E_INVALID, "keys_unique must be 0, 1 or 2");
     if (a->ds_offsets && a->ds_elements < 0) return fail(WMX_E_INVALID, "negative ds_elements");
-  } else if (a->k_units || a->ds_offsets) {
-    return fail(WMX_E_INVALID, "key work lists and dS offsets need a varlen schedule");
+    if (a->f_units) {
+      if (a->num_f_units < 0) return fail(WMX_E_INVALID, "negative work-list length");
+      if (!a->k_units || !a->q_units)
+        return fail(WMX_E_INVALID, "f_units needs k_units and q_units (the segments it does not list)");
+      if (a->unit_fields != WMX_UNIT_FIELDS)
+        return fail(WMX_E_INVALID, "f_units needs entries of WMX_UNIT_FIELDS ints (unit_fields)");
+      if (a->q_heads != a->kv_heads) return fail(WMX_E_INVALID, "f_units needs q_heads == kv_heads");
+      if (a->keys_unique == 0) return fail(WMX_E_INVALID, "f_units needs keys_unique 1 or 2");
+      if ((a->segment_layout & 3) != 3)
+        return fail(WMX_E_INVALID, "f_units needs consecutive query and key slots (segment_layout bits 0 and 1)");
+      for (const int64_t* st : {a->q_stride, a->k_stride, a->v_stride, a->do_stride})
+        if (st[2] < a->head_dim || st[2] >= (int64_t(1) << 23))
+          return fail(WMX_E_INVALID, "f_units needs token strides in [head_dim, 2^23) elements");
+    }
+  } else if (a->k_units || a->ds_offsets || a->f_units) {
+    return fail(WMX_E_INVALID, "key work lists, fused segment lists and dS offsets need a varlen schedule");
   }
   if (a->q_units && a->num_q_units < 0) return fail(WMX_E_INVALID, "negative work-list length");
   if (a->q_seg && (!a->k_seg || !a->q_start || !a->k_qend))

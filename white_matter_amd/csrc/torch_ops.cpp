@@ -181,6 +181,9 @@ struct Schedule {
   int status = kDocMode;
   // packed segments (status kPacked), see wmx_attn_args
   Tensor qi, ki, cu_q, cu_k, q_units, k_units, ds_offsets;
+  // the fused backward's segments and the other backward kernels' lists
+  // without them (wmx_attn_args f_units, q_units, k_units)
+  Tensor f_units, bq_units, bk_units;
   int64_t num_segments = 0, max_q = 0, max_k = 0, layout = 0, keys_unique = 1, ds_elements = 0, key_tile = 0;
   // int32 contiguous copies of the document arrays that were not (status kDocMode)
   std::array<Tensor, 4> docs;
@@ -193,9 +196,9 @@ WeakCache<Schedule> g_cyclic_cache;
 // The packed schedule of these metadata tensors at this stride and residue
 // offset, built on a miss by the Python packer
 // (white_matter::_cyclic_schedule: [facts, query_indices, key_indices,
-// cu_queries, cu_keys, q_units, k_units, ds_offsets], facts = int64 CPU
-// {status, num_segments, max_queries, max_keys, segment_layout, keys_unique,
-// ds_elements, key_tile}).
+// cu_queries, cu_keys, q_units, k_units, ds_offsets, f_units, bq_units,
+// bk_units], facts = int64 CPU {status, num_segments, max_queries, max_keys,
+// segment_layout, keys_unique, ds_elements, key_tile}).
 std::shared_ptr<Schedule> schedule_for(const std::array<Tensor, 4>& m, int64_t q_len, int64_t k_len, int64_t stride,
                                        int64_t offset) {
   auto same = [&](const Schedule& s) {
@@ -221,7 +224,7 @@ std::shared_ptr<Schedule> schedule_for(const std::array<Tensor, 4>& m, int64_t q
   const int64_t* f = facts.data_ptr<int64_t>();
   s->status = (int)f[0];
   if (s->status == kPacked) {
-    TORCH_CHECK(built.size() == 8, "_cyclic_schedule returned an unexpected result");
+    TORCH_CHECK(built.size() == 11, "_cyclic_schedule returned an unexpected result");
     s->num_segments = f[1];
     s->max_q = f[2];
     s->max_k = f[3];
@@ -236,6 +239,9 @@ std::shared_ptr<Schedule> schedule_for(const std::array<Tensor, 4>& m, int64_t q
     s->q_units = built[5].to(at::kInt).contiguous();
     s->k_units = built[6].to(at::kInt).contiguous();
     s->ds_offsets = built[7].to(at::kLong).contiguous();
+    s->f_units = built[8].to(at::kInt).contiguous();
+    s->bq_units = built[9].to(at::kInt).contiguous();
+    s->bk_units = built[10].to(at::kInt).contiguous();
   } else if (s->status == kDocMode) {
     for (int i = 0; i < 4; ++i) s->docs[i] = converted(m[i], at::kInt);
   }
@@ -244,6 +250,14 @@ std::shared_ptr<Schedule> schedule_for(const std::array<Tensor, 4>& m, int64_t q
 }
 
 // --------------------------------------------------------- launch glue ----
+// The fused short-segment backward loads consecutive query and key slots as
+// strided tiles: both layout bits, and token strides of at least head_dim and
+// below 2^23 elements (as wmx_attn_bwd checks).
+bool fused_fits(const wmx_attn_args& a) {
+  auto fits = [&](const int64_t* st) { return st[2] >= a.head_dim && st[2] < (int64_t(1) << 23); };
+  return (a.segment_layout & 3) == 3 && fits(a.q_stride) && fits(a.k_stride) && fits(a.v_stride) && fits(a.do_stride);
+}
+
 void fill_common(wmx_attn_args& a, const Tensor& q, const Tensor& k, const Tensor& v, const Tensor& o, const Tensor& lse,
                  double scale) {
   a.q = q.data_ptr();
@@ -293,6 +307,17 @@ void fill_visibility(wmx_attn_args& a, const Schedule* s, const std::array<Tenso
     if (backward) {
       a.ds_offsets = s->ds_offsets.data_ptr<int64_t>();
       a.ds_elements = s->ds_elements;
+      if (s->f_units.defined() && s->f_units.size(0) > 0 && q.size(1) == k.size(1) &&
+          s->f_units.size(1) == WMX_UNIT_FIELDS && a.unit_fields == WMX_UNIT_FIELDS) {
+        // short segments through the fused kernel; the tiled kernels take the
+        // rest (an empty list still passes a valid pointer, with count 0)
+        a.f_units = s->f_units.data_ptr<int32_t>();
+        a.num_f_units = (int32_t)s->f_units.size(0);
+        a.q_units = s->bq_units.numel() ? s->bq_units.data_ptr<int32_t>() : a.f_units;
+        a.num_q_units = (int32_t)s->bq_units.size(0);
+        a.k_units = s->bk_units.numel() ? s->bk_units.data_ptr<int32_t>() : a.f_units;
+        a.num_k_units = (int32_t)s->bk_units.size(0);
+      }
     }
   } else if (s->status == kDocMode) {
     a.q_seg = either(s->docs[0], (*meta)[0]).data_ptr<int32_t>();
@@ -371,6 +396,15 @@ std::tuple<Tensor, Tensor, Tensor> backward_impl(const Tensor& Q, const Tensor& 
     strides3(dq, a.dq_stride);
     strides3(dk, a.dk_stride);
     strides3(dv, a.dv_stride);
+    if (a.f_units && !fused_fits(a)) {
+      // the tiled kernels for every segment
+      a.f_units = nullptr;
+      a.num_f_units = 0;
+      a.q_units = s->q_units.data_ptr<int32_t>();
+      a.num_q_units = (int32_t)s->q_units.size(0);
+      a.k_units = s->k_units.data_ptr<int32_t>();
+      a.num_k_units = (int32_t)s->k_units.size(0);
+    }
     const int64_t need = wmx_attn_bwd_workspace_size(&a);
     Tensor workspace;
     if (need > 0) {

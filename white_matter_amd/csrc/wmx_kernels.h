@@ -51,6 +51,7 @@ int launch_bwd_preprocess(const wmx_attn_args& a, hipStream_t stream);
 int64_t bwd_workspace_size(const wmx_attn_args& a);
 int64_t bwd_min_workspace_size(const wmx_attn_args& a);
 int launch_bwd(const wmx_attn_args& a, hipStream_t stream);
+int launch_bwd_seg(const wmx_attn_args& a, hipStream_t stream);  // the f_units segments (attn_bwd_seg.hip)
 int launch_bwd_dq(const wmx_attn_args& a, hipStream_t stream);
 int launch_bwd_dkv(const wmx_attn_args& a, hipStream_t stream);
 int64_t decode_workspace_size(const wmx_decode_args& a);

@@ -202,7 +202,9 @@ def _cyclic_schedule(
     facts tensor {status, num_segments, max_queries, max_keys, segment_layout,
     keys_unique, ds_elements, key_tile} and, for status 2 (packed segments), the varlen
     tensors query_indices, key_indices, cu_queries, cu_keys and the work lists
-    q_units, k_units, ds_offsets. Status 1: no query sees a key; status 0: the
+    q_units, k_units, ds_offsets, then the fused backward's segment list and the
+    backward's query-tile and key-tile lists without those segments (used when
+    the call has as many query heads as KV heads). Status 1: no query sees a key; status 0: the
     metadata is not run-structured, or key rows other than the dummy slots
     repeat (the document-mode kernels evaluate the rule per pair)."""
     _kernels.guard_capture("packing cyclic document metadata")
@@ -215,7 +217,7 @@ def _cyclic_schedule(
         return [facts(0)]
     if schedule == "empty":
         return [facts(1)]
-    from .strict_causal_attention import _key_tile, _keys_unique_code, _schedule_flags, _work_units
+    from .strict_causal_attention import _fused_units, _key_tile, _keys_unique_code, _schedule_flags, _work_units
 
     max_q, max_k, flags = _schedule_flags(schedule)
     unique = _keys_unique_code(flags)
@@ -226,10 +228,11 @@ def _cyclic_schedule(
         return [facts(0)]
     key_tile = _key_tile(schedule, stride)
     q_units, k_units, ds_offsets, ds_elements = _work_units(schedule, stride, query_extent=q_len, key_tile=key_tile)
+    f_units, bq_units, bk_units = _fused_units(schedule, stride, q_len, key_tile)
     return [
         facts(2, schedule.cu_queries.numel() - 1, max_q, max_k, flags & 15, unique, ds_elements, key_tile),
         schedule.query_indices, schedule.key_indices, schedule.cu_queries, schedule.cu_keys,
-        q_units, k_units, ds_offsets,
+        q_units, k_units, ds_offsets, f_units, bq_units, bk_units,
     ]
 
 

@@ -501,6 +501,62 @@ def _work_units(
     return units
 
 
+# Segments of at most this many queries take the fused backward
+# (attn_bwd_seg.hip, which holds up to 128). A workgroup walks its segment's
+# key tiles one after another, so the longest listed segment bounds the
+# launch: at C3 stride 8 the limit 96 keeps the one 16-tile segment of 97-128
+# queries on the tiled kernels (1.41-1.43 against 1.44-1.46 ms per pass with
+# 128, 1.56 with none).
+_FUSED_ROWS = 96
+_FUSED_ROWS_MAX = 128  # the kernel's bound (wmx_attn_args f_units)
+
+
+def _fused_units(
+    metadata: StrictCausalMetadata, stride: int, query_extent: int, key_tile: int = _TILE
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """The fused backward's work list and the other backward kernels' lists
+    without its segments (wmx_attn_args f_units, q_units, k_units), cached on
+    the metadata object like `_work_units`: every segment with 1 to
+    _FUSED_ROWS queries and at least one key, heaviest first (most 64-key
+    tiles, then most queries), as entries with the segment's fields; then
+    `_work_units`' query-tile and key-tile entries of the other segments. The
+    forward keeps `_work_units`' full query list."""
+    if not 0 <= _FUSED_ROWS <= _FUSED_ROWS_MAX:
+        raise ValueError(f"the fused backward holds at most {_FUSED_ROWS_MAX} queries")
+    cache = metadata.__dict__.setdefault("_fused", {})
+    lists = cache.get((stride, query_extent, key_tile, _FUSED_ROWS))
+    if lists is None:
+        _kernels.guard_capture("building the fused backward's work lists")
+        q_units, k_units, ds_offsets, _ = _work_units(metadata, stride, query_extent=query_extent, key_tile=key_tile)
+        fused = [
+            (-(-(ke - ks) // _STEP), qe - qs, s)
+            for s, (qs, qe, ks, ke) in enumerate(metadata.segments)
+            if 1 <= qe - qs <= _FUSED_ROWS and ke > ks
+        ]
+        fused.sort(key=lambda e: (-e[0], -e[1], e[2]))
+        ids = torch.tensor([s for _, _, s in fused], dtype=torch.long)
+        fields = _segment_fields(metadata, query_extent, ds_offsets.cpu())
+        f_units = fields.index_select(0, ids)
+        f_units[:, 1] = 0
+        device = metadata.query_indices.device
+
+        def placed(rows: torch.Tensor) -> torch.Tensor:
+            # an empty list keeps an allocation of its own (empty device
+            # tensors share a null address, which reads as aliasing)
+            if rows.shape[0] == 0:
+                return torch.zeros(1, rows.shape[1], dtype=rows.dtype, device=device)[:0]
+            return rows.contiguous().to(device)
+
+        def others(units: torch.Tensor) -> torch.Tensor:
+            host = units.cpu()
+            return placed(host[~torch.isin(host[:, 0].long(), ids)])
+
+        lists = cache[(stride, query_extent, key_tile, _FUSED_ROWS)] = (
+            placed(f_units), others(q_units), others(k_units)
+        )
+    return lists
+
+
 def _key_tile(metadata: StrictCausalMetadata, stride: int = 1) -> int:
     """Keys per dK/dV workgroup for a packed schedule (wmx_attn_args key_tile).
     Strided (cyclic) calls give each key tile few query tiles, so the per-unit

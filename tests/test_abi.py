@@ -165,3 +165,41 @@ def test_missing_library_fails_loudly(monkeypatch, tmp_path):
     finally:
         monkeypatch.delenv("WMX_ATTN_LIBRARY")
         _native.load.cache_clear()
+
+
+def test_fused_segment_list_checks():
+    """wmx_attn_bwd refuses a fused segment list (f_units) the kernel cannot take,
+    before anything is launched."""
+    lib = _native.load()
+    a = _native.AttnArgs()
+    a.head_dim, a.batch, a.q_heads, a.kv_heads, a.q_len, a.kv_len = 128, 1, 2, 2, 64, 64
+    a.query_stride, a.softmax_scale = 8, 0.125
+    a.q = a.k = a.v = a.o = a.lse = a.dout = a.delta = a.dq = a.dk = a.dv = 0x1000
+    for name in ("q_stride", "k_stride", "v_stride", "o_stride", "do_stride", "dq_stride", "dk_stride", "dv_stride"):
+        setattr(a, name, (2 * 64 * 128, 64 * 128, 128))
+    a.query_indices = a.key_indices = a.cu_queries = a.cu_keys = 0x1000
+    a.num_segments, a.query_extent, a.key_extent, a.keys_unique = 1, 64, 64, 1
+    a.f_units, a.num_f_units = 0x1000, 1
+    assert lib.wmx_attn_bwd(ctypes.byref(a), None) == -1
+    assert b"k_units and q_units" in lib.wmx_last_error()
+    a.q_units = a.k_units = 0x1000
+    assert lib.wmx_attn_bwd(ctypes.byref(a), None) == -1
+    assert b"WMX_UNIT_FIELDS" in lib.wmx_last_error()
+    a.unit_fields = _native.UNIT_FIELDS
+    a.q_heads = 4
+    assert lib.wmx_attn_bwd(ctypes.byref(a), None) == -1
+    assert b"q_heads == kv_heads" in lib.wmx_last_error()
+    a.q_heads = 2
+    a.keys_unique = 0
+    assert lib.wmx_attn_bwd(ctypes.byref(a), None) == -1
+    assert b"keys_unique" in lib.wmx_last_error()
+    a.keys_unique = 1
+    assert lib.wmx_attn_bwd(ctypes.byref(a), None) == -1
+    assert b"consecutive" in lib.wmx_last_error()
+    a.segment_layout = 3
+    a.k_stride = (2 * 64 * 2048, 64 * 2048, 1 << 23)  # beyond the strided tile loads' 32-bit offsets
+    assert lib.wmx_attn_bwd(ctypes.byref(a), None) == -1
+    assert b"token strides" in lib.wmx_last_error()
+    a.f_units, a.query_indices = 0x1000, None
+    assert lib.wmx_attn_bwd(ctypes.byref(a), None) == -1
+    assert b"varlen schedule" in lib.wmx_last_error()

@@ -37,30 +37,37 @@ namespace wmx {
 constexpr int kSegRows = 128;  // queries a workgroup holds
 constexpr int kSegKeys = 64;   // keys per step
 
-// P and dS of one step: [query][key] bf16, 64 keys per query row. Groups of 4
-// keys are XOR-swizzled by the query row so that transposed reads (4
-// consecutive rows x 32 keys per 32 lanes) and row reads (32 rows x 4 keys)
-// spread over the 64 banks.
-__device__ __forceinline__ int pd_swz(int q) { return (((q >> 1) & 1) << 5) ^ (((q >> 2) & 3) << 3) ^ (((q >> 4) & 1) << 2); }
-__device__ __forceinline__ int pd_elem(int q, int k) { return q * kSegKeys + (k ^ pd_swz(q)); }
+// P and dS of one step: [query][key] bf16, query rows kPdLd = 68 elements
+// (136 bytes, 34 dwords) apart. Row reads (32 queries x 8 bytes per 32 lanes)
+// then hit 32 distinct even dwords (34 q mod 64): conflict-free; transposed
+// reads (4 consecutive rows x 16 dwords per 32 lanes) are at most two-way.
+// Every address is a per-lane base plus constants (no swizzle to recompute).
+constexpr int kPdLd = kSegKeys + 4;
 
-// MFMA operand contracting over query rows for the 32 key columns c0 ..
-// c0 + 31 (accumulator k-order of k-step s: rows 16 s + 8 (e / 4) + 4 half +
-// e % 4 for element e), as tile_tr_operand.
-__device__ __forceinline__ bf16x8 pd_tr_operand(const bf16* t, int c0, int s, int lane) {
+// Byte offset of this lane's transposed reads of key columns c0 .. c0 + 31
+// (accumulator k-order of k-step s: rows 16 s + 8 (e / 4) + 4 half + e % 4
+// for element e, as tile_tr_operand): k-step s adds 16 rows, the second
+// 8-byte read 8 rows, both immediates.
+__device__ __forceinline__ int pd_tr_base(int c0, int lane) {
   const int li = lane & 15, g = lane >> 4;
   const int c = c0 + 16 * (g & 1) + 4 * (li & 3);
-  const int r = 16 * s + 4 * (g >> 1) + (li >> 2);
-  const u32x2 lo = lds_read_tr4(t + pd_elem(r, c));
-  const u32x2 hi = lds_read_tr4(t + pd_elem(r + 8, c));
+  const int r = 4 * (g >> 1) + (li >> 2);
+  return 2 * (r * kPdLd + c);
+}
+__device__ __forceinline__ bf16x8 pd_tr_get(const bf16* t, int base, int s) {
+  const char* p = (const char*)t + base + 32 * kPdLd * s;
+  const u32x2 lo = lds_read_tr4((const bf16*)p);
+  const u32x2 hi = lds_read_tr4((const bf16*)(p + 16 * kPdLd));
   const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
   return as_bf16x8(v);
 }
 
-// Keys of query row q in the same k-order (16 s + 8 (e / 4) + 4 half + e % 4).
-__device__ __forceinline__ bf16x8 pd_row_operand(const bf16* t, int q, int s, int half) {
-  const u32x2 lo = *reinterpret_cast<const u32x2*>(t + pd_elem(q, 16 * s + 4 * half));
-  const u32x2 hi = *reinterpret_cast<const u32x2*>(t + pd_elem(q, 16 * s + 8 + 4 * half));
+// Keys of query row q in the same k-order (16 s + 8 (e / 4) + 4 half + e % 4):
+// base 2 (q kPdLd + 4 half); k-step s adds 32 s bytes, the second read 16.
+__device__ __forceinline__ bf16x8 pd_row_get(const bf16* t, int base, int s) {
+  const char* p = (const char*)t + base + 32 * s;
+  const u32x2 lo = *reinterpret_cast<const u32x2*>(p);
+  const u32x2 hi = *reinterpret_cast<const u32x2*>(p + 16);
   const u32x4 v = {lo[0], lo[1], hi[0], hi[1]};
   return as_bf16x8(v);
 }
@@ -101,8 +108,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_seg_kernel(const wmx_attn_arg
   __shared__ __attribute__((aligned(1024))) bf16 k_lds0[kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 k_lds1[kTileElems];
   __shared__ __attribute__((aligned(1024))) bf16 v_lds[kTileElems];
-  __shared__ __attribute__((aligned(16))) bf16 p_lds[kSegRows * kSegKeys];
-  __shared__ __attribute__((aligned(16))) bf16 s_lds[kSegRows * kSegKeys];
+  __shared__ __attribute__((aligned(16))) bf16 p_lds[kSegRows * kPdLd];
+  __shared__ __attribute__((aligned(16))) bf16 s_lds[kSegRows * kPdLd];
 
   // the segment from its work-list entry (fields required by the host): its
   // queries are slots qslot0 .. of row qrow, key 0 is slot kslot0 and key
@@ -132,6 +139,12 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_seg_kernel(const wmx_attn_arg
   const int db = p2_live ? p2_u % DB : 0, kb2 = NKH == 2 ? 0 : wave & 1;
   // dQ^T: query block dqb, columns dq0 .. dq0 + PB
   const int dqb = wave >> 1, dq0 = (wave & 1) * PB;
+  // byte offsets into P and dS: phase 1's writes (query qi, keys 32 pkh + 4 half
+  // + 8 g), phase 2's transposed reads (key halves kb2 ..), dQ's row reads
+  int pd_w = 2 * (qi * kPdLd + 32 * pkh + 4 * half), pd_q = 2 * ((32 * dqb + col) * kPdLd + 4 * half);
+  int pd_b[NKH];
+#pragma unroll
+  for (int i = 0; i < NKH; ++i) pd_b[i] = pd_tr_base(32 * (kb2 + i), lane);
 
   // this lane's query statistics (phase 1)
   const float sl2 = a.softmax_scale * kLog2e;
@@ -186,11 +199,18 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_seg_kernel(const wmx_attn_arg
     vp = vslice + slot * a.v_stride[2];
   });
 
-  RowReads<KS> rrd;
-  rrd.init(col, half);
+  // row-read offsets with the wave's 32-row block folded in: K and V rows of
+  // key half pkh, Q and dO rows of query block pqb
+  RowReads<KS> rkv, rqg;
+  rkv.init(col, half);
+  rqg.init(col, half);
+#pragma unroll
+  for (int s = 0; s < KS; ++s) {
+    rkv.off[s] += 8192 * pkh;
+    rqg.off[s] += 8192 * pqb;
+  }
   TrReads<PB> trq;  // transposed reads of the wave's dQ columns of D (K^T)
   trq.init(lane, 32 * dq0);
-  const bf16* const b_src = p2_k ? s_lds : p_lds;  // phase 2: dS or P
 
   // operands that every step reuses, read from LDS once the tiles have
   // landed: the wave's Q rows (phase 1, B operands of S^T over D) and its
@@ -200,7 +220,7 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_seg_kernel(const wmx_attn_arg
   bf16x8 qreg[KS], areg[QS];
   auto fill_registers = [&]() __attribute__((always_inline)) {
 #pragma unroll
-    for (int s = 0; s < KS; ++s) qreg[s] = rrd.get(q_lds, s, pqb);
+    for (int s = 0; s < KS; ++s) qreg[s] = rqg.get(q_lds, s, 0);
     TrReads<1> tra;
     tra.init(lane, 32 * db);
     const bf16* const a_src = p2_k ? q_lds : g_lds;
@@ -245,23 +265,25 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_seg_kernel(const wmx_attn_arg
 
   // phase 1 of step t on tiles kt, vt: S^T and dP^T chains interleaved
   auto phase1 = [&](const bf16* kt, const bf16* vt, int t) __attribute__((always_inline)) {
-    rrd.refresh();
+    rkv.refresh();
+    rqg.refresh();
+    opaque(pd_w);
     constexpr int PF = KS < 2 ? KS : 2;
     f32x16 sacc = f32x16{}, dacc = f32x16{};
     bf16x8 ka[KS], va[KS], ga[KS];
 #pragma unroll
     for (int s = 0; s < PF; ++s) {
-      ka[s] = rrd.get(kt, s, pkh);
-      va[s] = rrd.get(vt, s, pkh);
-      ga[s] = rrd.get(g_lds, s, pqb);
+      ka[s] = rkv.get(kt, s, 0);
+      va[s] = rkv.get(vt, s, 0);
+      ga[s] = rqg.get(g_lds, s, 0);
     }
 #pragma unroll
     for (int s = 0; s < KS; ++s) {
       __builtin_amdgcn_sched_barrier(0);
       if (s + PF < KS) {
-        ka[s + PF] = rrd.get(kt, s + PF, pkh);
-        va[s + PF] = rrd.get(vt, s + PF, pkh);
-        ga[s + PF] = rrd.get(g_lds, s + PF, pqb);
+        ka[s + PF] = rkv.get(kt, s + PF, 0);
+        va[s + PF] = rkv.get(vt, s + PF, 0);
+        ga[s + PF] = rqg.get(g_lds, s + PF, 0);
       }
       sacc = mfma32(ka[s], qreg[s], sacc);
       dacc = mfma32(va[s], ga[s], dacc);
@@ -288,9 +310,8 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_seg_kernel(const wmx_attn_arg
         p[e] = __builtin_amdgcn_exp2f(fmaf(sacc[4 * g + e], sl2, nl2));
         ds[e] = p[e] * (dacc[4 * g + e] - dlt);
       }
-      const int e0 = pd_elem(qi, 32 * pkh + 8 * g + 4 * half);
-      *reinterpret_cast<u32x2*>(p_lds + e0) = u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
-      *reinterpret_cast<u32x2*>(s_lds + e0) = u32x2{pack_bf16x2(ds[0], ds[1]), pack_bf16x2(ds[2], ds[3])};
+      *reinterpret_cast<u32x2*>((char*)p_lds + pd_w + 16 * g) = u32x2{pack_bf16x2(p[0], p[1]), pack_bf16x2(p[2], p[3])};
+      *reinterpret_cast<u32x2*>((char*)s_lds + pd_w + 16 * g) = u32x2{pack_bf16x2(ds[0], ds[1]), pack_bf16x2(ds[2], ds[3])};
     }
   };
 
@@ -299,54 +320,61 @@ __global__ __launch_bounds__(512, 1) void attn_bwd_seg_kernel(const wmx_attn_arg
   // then dQ^T += K^T dS^T over the tile's 64 keys
   auto phase2 = [&](const bf16* kt, int s0, int s1, bool dq_live) __attribute__((always_inline)) {
     trq.refresh();
+    opaque(pd_q);
+#pragma unroll
+    for (int i = 0; i < NKH; ++i) opaque(pd_b[i]);
 #pragma unroll
     for (int i = 0; i < NKH; ++i) kvacc[i] = f32x16{};
-    if (p2_live) {
-      // unrolled over the 8 query k-steps (the A operands are registers
-      // indexed by the step), the steps outside [s0, s1) skipped; the B
-      // operands of the next step read ahead
-      bf16x8 nb[NKH];
+    // unrolled over the 4 query blocks (the A operands are registers indexed
+    // by the k-step), the blocks outside [s0 / 2, s1 / 2) skipped; a block's
+    // B operands are all read before its products, and nothing is carried
+    // from one block to the next (no register copies at the skipped blocks'
+    // joins). The B array is named, not selected at run time: reads through
+    // a selected pointer wait for the V tile's direct-to-LDS loads (the
+    // compiler cannot tell the arrays apart)
+    auto kv_blocks = [&](const bf16* src) __attribute__((always_inline)) {
 #pragma unroll
-      for (int i = 0; i < NKH; ++i) nb[i] = pd_tr_operand(b_src, 32 * (kb2 + i), s0, lane);
-#pragma unroll
-      for (int s = 0; s < QS; ++s) {
-        if (s >= s0 && s < s1) {
+      for (int qb = 0; qb < QS / 2; ++qb) {
+        if (2 * qb >= s0 && 2 * qb < s1) {
           __builtin_amdgcn_sched_barrier(0);
-          bf16x8 cb[NKH];
+          bf16x8 cb[2][NKH];
 #pragma unroll
-          for (int i = 0; i < NKH; ++i) cb[i] = nb[i];
-          if (s + 1 < s1) {
+          for (int j = 0; j < 2; ++j)
 #pragma unroll
-            for (int i = 0; i < NKH; ++i) nb[i] = pd_tr_operand(b_src, 32 * (kb2 + i), s + 1, lane);
-          }
+            for (int i = 0; i < NKH; ++i) cb[j][i] = pd_tr_get(src, pd_b[i], 2 * qb + j);
+          __builtin_amdgcn_sched_barrier(0);  // all reads issued before the first product
 #pragma unroll
-          for (int i = 0; i < NKH; ++i) kvacc[i] = mfma32(areg[s], cb[i], kvacc[i]);
+          for (int j = 0; j < 2; ++j)
+#pragma unroll
+            for (int i = 0; i < NKH; ++i) kvacc[i] = mfma32(areg[2 * qb + j], cb[j][i], kvacc[i]);
         }
       }
+    };
+    if (p2_live) {
+      if (p2_k) kv_blocks(s_lds);
+      else kv_blocks(p_lds);
     }
     __builtin_amdgcn_sched_barrier(0);
     if (dq_live) {
-      const int q = 32 * dqb + col;
-      bf16x8 sb = pd_row_operand(s_lds, q, 0, half), ka[PB];
+      // two groups of two key k-steps: a group's operands read before its
+      // products
 #pragma unroll
-      for (int i = 0; i < PB; ++i)
-        if (dq0 + i < DB) ka[i] = trq.get(kt, i, 0);
-#pragma unroll
-      for (int s = 0; s < kSegKeys / 16; ++s) {
+      for (int hs = 0; hs < kSegKeys / 32; ++hs) {
         __builtin_amdgcn_sched_barrier(0);
-        const bf16x8 cb = sb;
-        bf16x8 ca[PB];
+        bf16x8 cb[2], ca[2][PB];
 #pragma unroll
-        for (int i = 0; i < PB; ++i) ca[i] = ka[i];
-        if (s + 1 < kSegKeys / 16) {
-          sb = pd_row_operand(s_lds, q, s + 1, half);
+        for (int j = 0; j < 2; ++j) {
+          cb[j] = pd_row_get(s_lds, pd_q, 2 * hs + j);
 #pragma unroll
           for (int i = 0; i < PB; ++i)
-            if (dq0 + i < DB) ka[i] = trq.get(kt, i, s + 1);
+            if (dq0 + i < DB) ca[j][i] = trq.get(kt, i, 2 * hs + j);
         }
+        __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-        for (int i = 0; i < PB; ++i)
-          if (dq0 + i < DB) qacc[i] = mfma32(ca[i], cb, qacc[i]);
+        for (int j = 0; j < 2; ++j)
+#pragma unroll
+          for (int i = 0; i < PB; ++i)
+            if (dq0 + i < DB) qacc[i] = mfma32(ca[j][i], cb[j], qacc[i]);
       }
       __builtin_amdgcn_sched_barrier(0);
     }

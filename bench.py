@@ -25,6 +25,7 @@ The CPU baseline times the oracle (float32, dense mask) on a bounded sample.
 from __future__ import annotations
 
 import argparse
+import gc
 import json
 import os
 import sys
@@ -665,6 +666,11 @@ def cyclic_line(device, stride=4, dummy=False):
                                    metadata=metas[r], backend="tilelang")
             torch.autograd.grad(out, (ql[r], kl, vl), grads[r])
 
+    # a full collection now rather than inside the timed passes: among the
+    # many tensors and schedules of a long run, one stalled the host for tens
+    # of milliseconds while the GPU waited for the next launch (a stride-8
+    # pass measured 11.7 instead of 1.38 ms)
+    gc.collect()
     for _ in range(2):
         full_pass()
     ms = Timer()(full_pass, 10)

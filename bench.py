@@ -439,6 +439,8 @@ def main(argv=None) -> int:
     # After an idle period of even a few milliseconds the GPU's clock takes
     # about 50 steps to settle (measured step times dip from 0.43 to 0.52 ms
     # around steps 6-10 after 0.5 s idle, and to 0.48 ms after a few ms).
+    # A garbage collection first, so that none falls in the timed steps.
+    gc.collect()
     torch.cuda.synchronize()
     first = time.perf_counter()
     step()

@@ -27,9 +27,10 @@
 // Two barriers per step. K tiles are double-buffered (the next one issued at
 // the step's start); V has one buffer, refilled after the phase-1 barrier
 // (phase 2 reads no V; a second V buffer measured no faster). A step's dK/dV
-// rows are stored at the start of the next step, before its loads are
-// issued, so that the loads are the newest vector-memory operations when the
-// next barrier waits for them.
+// rows are stored at the start of the next step, so that they complete while
+// that step runs: the step barrier waits for every vector-memory operation of
+// its wave, and stores issued at the end of a step would be waited for at
+// once.
 #include "attn_tiles.h"
 
 namespace wmx {

@@ -90,11 +90,12 @@ def test_edge_segment_sizes_stride_8(dim, dummy, monkeypatch):
     _check(docs, 8, dummy, dim, residues=(0, 3, 7), monkeypatch=monkeypatch)
 
 
+@pytest.mark.parametrize("dummy", [False, True])
 @pytest.mark.parametrize("stride", [1, 2, 4])
-def test_geometric_documents(stride, monkeypatch):
-    torch.manual_seed(stride)
+def test_geometric_documents(stride, dummy, monkeypatch):
+    torch.manual_seed(stride + 10 * dummy)
     docs = bench.geometric_documents(2, 1024, stride, mean=96, lo=4, hi=600).to(DEV)
-    _check(docs, stride, False, 128, residues=(0, stride - 1), heads=4, monkeypatch=monkeypatch)
+    _check(docs, stride, dummy, 128, residues=(0, stride - 1), heads=4, monkeypatch=monkeypatch)
 
 
 def test_repeated_calls_are_identical():
